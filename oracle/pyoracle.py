@@ -1,0 +1,424 @@
+"""ctypes binding of the CPU oracle (oracle/oracle.c) — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, and only
+as the checker or as the timed CPU baseline. The product library never loads it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+
+_lib = None
+
+
+class KvLayout(C.Structure):
+    _fields_ = [
+        ("block_stride_bytes", C.c_uint64),
+        ("layer_stride_bytes", C.c_uint64),
+        ("kv_plane_stride_bytes", C.c_uint64),
+        ("token_stride_bytes", C.c_uint64),
+        ("head_stride_bytes", C.c_uint64),
+        ("pool_bytes", C.c_uint64),
+        ("num_blocks", C.c_uint32),
+        ("num_layers", C.c_uint32),
+        ("block_size", C.c_uint32),
+    ]
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("layers", C.c_int),
+        ("hidden", C.c_int),
+        ("q_heads", C.c_int),
+        ("kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("experts", C.c_int),
+        ("top_k", C.c_int),
+        ("inter", C.c_int),
+        ("vocab", C.c_int),
+        ("eps", C.c_float),
+        ("rope_theta", C.c_double),
+    ]
+
+
+def build():
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        P = C.c_void_p
+        f32, f64, u8, u16, u32, u64, i32 = (C.c_float, C.c_double, C.c_uint8, C.c_uint16,
+                                            C.c_uint32, C.c_uint64, C.c_int)
+        sig = {
+            "oref_bf16_to_f32": (f32, [u16]),
+            "oref_f32_to_bf16": (u16, [f32]),
+            "oref_kv_f32_to_bf16": (u16, [f32]),
+            "oref_e4m3_to_f32": (f32, [u8]),
+            "oref_f32_to_e4m3": (u8, [f32]),
+            "oref_f32_to_e4m3_fast": (u8, [f32]),
+            "oref_e4m3_rne_sat": (u8, [f32]),
+            "oref_fq_e4m3_to_f32": (f32, [u8]),
+            "oref_block_scale": (None, [f32, P, P]),
+            "oref_quant_row": (None, [P, i32, P, P]),
+            "oref_fake_quant_row": (None, [P, i32]),
+            "oref_bf16_round_row": (None, [P, i32]),
+            "oref_quantize_block128": (None, [P, i32]),
+            "oref_prand": (f32, [u64, u64]),
+            "oref_splitmix64": (u64, [u64]),
+            "oref_synth_normal": (f32, [u64, u64, u64, f32]),
+            "oref_synth_bf16": (None, [u64, u64, C.c_size_t, f32, i32, P]),
+            "oref_synth_f32": (None, [u64, u64, C.c_size_t, f32, i32, P]),
+            "oref_synth_fp8": (None, [u64, u64, i32, i32, i32, f32, P, P]),
+            "oref_fp8_grouped": (None, [P, P, i32, i32, i32, i32, P, P, i32, P]),
+            "oref_fp8_grouped_mt": (None, [P, P, i32, i32, i32, i32, P, P, i32, P, i32]),
+            "oref_dequant_matvec": (None, [P, P, i32, i32, P, P]),
+            "oref_bf16_gemv": (None, [P, i32, i32, P, P]),
+            "oref_bf16_gemv_mt": (None, [P, i32, i32, P, P, i32]),
+            "oref_argmax": (u32, [P, i32]),
+            "oref_rmsnorm": (None, [P, P, i32, f32, P]),
+            "oref_rmsnorm_per_head": (None, [P, P, f32, i32, i32, P]),
+            "oref_rope_cos_sin": (None, [f64, i32, i32, P, P]),
+            "oref_apply_rope": (None, [P, P, i32, i32, i32, i32, f64]),
+            "oref_sdpa": (None, [P, P, P, i32, i32, i32, i32, P]),
+            "oref_router_logits": (None, [P, P, i32, i32, P]),
+            "oref_router_logits_f64": (None, [P, P, i32, i32, P]),
+            "oref_moe_plan": (i32, [P, i32, i32, i32, P, P, P, P, P, P]),
+            "oref_reduce_grouped": (None, [P, P, i32, i32, P, i32, P]),
+            "oref_swiglu": (None, [P, i32, P]),
+            "oref_route": (i32, [P, P, i32, i32, i32, P, f32, i32, P, P, P, P]),
+            "oref_moe_forward": (None, [P, P, P, P, i32, i32, i32, i32, P, P, P, i32, P]),
+            "oref_moe_block": (None, [P, P, P, P, i32, i32, i32, i32, P, P, P, i32, P]),
+            "oref_kv_layout_bf16": (None, [u32, u32, u32, u32, u32, P]),
+            "oref_kv_element_offset": (u64, [P, u32, u32, i32, u32, u32, u32]),
+            "oref_kv_write_token": (None, [P, P, u32, u32, u32, i32, P, P]),
+            "oref_kv_read_token": (None, [P, P, u32, u32, u32, i32, P, P]),
+            "oref_paged_attention": (None, [P, P, P, P, i32, i32, i32, i32, i32, P]),
+            "oref_fnv1a64": (u64, [P, C.c_size_t]),
+            "oref_dattn_alloc": (P, [i32, i32, f64]),
+            "oref_dattn_free": (None, [P]),
+            "oref_dattn_set_norms": (None, [P, i32, P, P]),
+            "oref_dattn_attend": (None, [P, i32, i32, P, f32, f32, P]),
+            "oref_dattn_read_row": (None, [P, i32, i32, i32, P, P]),
+            "oref_dattn_write_rows": (None, [P, i32, i32, i32, i32, P, P]),
+            "oref_model_synth": (P, [P, u64, f32, f32, i32]),
+            "oref_model_free": (None, [P]),
+            "oref_model_tensor": (P, [P, i32, i32, P]),
+            "oref_model_embed": (P, [P]),
+            "oref_model_lm_head": (P, [P]),
+            "oref_model_final_norm": (P, [P]),
+            "oref_engine_new": (P, [P, i32, i32, i32]),
+            "oref_engine_free": (None, [P]),
+            "oref_engine_step": (i32, [P, u32, P]),
+            "oref_engine_logits": (None, [P, P, P]),
+            "oref_engine_pos": (i32, [P]),
+            "oref_engine_last_routes": (None, [P, P, P, P]),
+            "oref_engine_last_x": (None, [P, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "arrays passed to the oracle must be contiguous"
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# --------------------------------------------------------------------------- helpers
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """RNE f32 -> bf16 bits (finite inputs), the rule of qwen3_moe.rs:486-493."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def e4m3_table() -> np.ndarray:
+    L = lib()
+    return np.array([L.oref_e4m3_to_f32(b) for b in range(256)], dtype=np.float32)
+
+
+def synth_fp8(seed: int, tensor: int, experts: int, n: int, k: int, sigma: float = 0.02):
+    w = np.empty((experts, n, k), dtype=np.uint8)
+    s = np.empty((experts, n // 128, k // 128), dtype=np.uint16)
+    lib().oref_synth_fp8(seed, tensor, experts, n, k, sigma, ptr(w), ptr(s))
+    return w, s
+
+
+def synth_bf16(seed: int, tensor: int, shape, sigma: float, one_plus: bool = False):
+    out = np.empty(shape, dtype=np.uint16)
+    lib().oref_synth_bf16(seed, tensor, out.size, sigma, int(one_plus), ptr(out))
+    return out
+
+
+def synth_f32(seed: int, tensor: int, shape, sigma: float, one_plus: bool = False):
+    out = np.empty(shape, dtype=np.float32)
+    lib().oref_synth_f32(seed, tensor, out.size, sigma, int(one_plus), ptr(out))
+    return out
+
+
+def fp8_grouped(w, s, ids, x, threads: int = 1):
+    experts, n, k = w.shape
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    groups = ids.size
+    x_rows = 1 if x.size == k else groups
+    y = np.empty((groups, n), dtype=np.float32)
+    lib().oref_fp8_grouped_mt(ptr(w), ptr(s), experts, n, k, groups, ptr(ids), ptr(x), x_rows,
+                              ptr(y), threads)
+    return y
+
+
+def dequant_matvec(w, s, v):
+    rows, cols = w.shape
+    out = np.empty(rows, dtype=np.float32)
+    lib().oref_dequant_matvec(ptr(np.ascontiguousarray(w)), ptr(np.ascontiguousarray(s)), rows,
+                              cols, ptr(np.ascontiguousarray(v, dtype=np.float32)), ptr(out))
+    return out
+
+
+def bf16_gemv(w, x, threads: int = 1):
+    n, k = w.shape
+    y = np.empty(n, dtype=np.float32)
+    lib().oref_bf16_gemv_mt(ptr(w), n, k, ptr(np.ascontiguousarray(x, dtype=np.float32)),
+                            ptr(y), threads)
+    return y
+
+
+def argmax(logits) -> int:
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(lib().oref_argmax(ptr(logits), logits.size))
+
+
+def rmsnorm(x, w, eps: float):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oref_rmsnorm(ptr(x), ptr(np.ascontiguousarray(w, dtype=np.float32)), x.size, eps,
+                       ptr(out))
+    return out
+
+
+def rmsnorm_per_head(x, w, eps: float, heads: int, hd: int):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oref_rmsnorm_per_head(ptr(x), ptr(np.ascontiguousarray(w, dtype=np.float32)), eps,
+                                heads, hd, ptr(out))
+    return out
+
+
+def rope_cos_sin(theta: float, hd: int, pos: int):
+    c = np.empty(hd // 2, dtype=np.float32)
+    s = np.empty(hd // 2, dtype=np.float32)
+    lib().oref_rope_cos_sin(theta, hd, pos, ptr(c), ptr(s))
+    return c, s
+
+
+def apply_rope(q, k, pos: int, qh: int, kvh: int, hd: int, theta: float):
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    lib().oref_apply_rope(ptr(q), ptr(k), pos, qh, kvh, hd, theta)
+    return q, k
+
+
+def sdpa(q, K, V, qh: int, kvh: int, hd: int):
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    ctx = K.shape[0] if K.ndim > 1 else K.size // (kvh * hd)
+    out = np.empty(qh * hd, dtype=np.float32)
+    lib().oref_sdpa(ptr(np.ascontiguousarray(q, dtype=np.float32)), ptr(K), ptr(V), ctx, qh, kvh,
+                    hd, ptr(out))
+    return out
+
+
+def router_logits(gate_bf16, post, refined: bool = False):
+    experts, hidden = gate_bf16.shape
+    out = np.empty(experts, dtype=np.float32)
+    fn = lib().oref_router_logits_f64 if refined else lib().oref_router_logits
+    fn(ptr(np.ascontiguousarray(gate_bf16)), ptr(np.ascontiguousarray(post, dtype=np.float32)),
+       experts, hidden, ptr(out))
+    return out
+
+
+def moe_plan(logits, tokens: int, experts: int, top_k: int):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    a = tokens * top_k
+    te = np.zeros(a, dtype=np.uint32)
+    tw = np.zeros(a, dtype=np.float32)
+    off = np.zeros(experts + 1, dtype=np.uint32)
+    g2a = np.zeros(a, dtype=np.uint32)
+    a2g = np.zeros(a, dtype=np.uint32)
+    gt = np.zeros(a, dtype=np.uint32)
+    rc = lib().oref_moe_plan(ptr(logits), tokens, experts, top_k, ptr(te), ptr(tw), ptr(off),
+                             ptr(g2a), ptr(a2g), ptr(gt))
+    if rc != 0:
+        raise ValueError(f"moe plan refused: rc {rc}")
+    return dict(topk_experts=te, topk_weights=tw, expert_offsets=off, grouped_to_assignment=g2a,
+                assignment_to_grouped=a2g, grouped_token_ids=gt)
+
+
+def route(gate_bf16, norm_w, x, eps: float, top_k: int = 8, refined: bool = True):
+    experts, hidden = gate_bf16.shape
+    ids = np.zeros(top_k, dtype=np.uint32)
+    w = np.zeros(top_k, dtype=np.float32)
+    post = np.zeros(hidden, dtype=np.float32)
+    logits = np.zeros(experts, dtype=np.float32)
+    rc = lib().oref_route(ptr(np.ascontiguousarray(gate_bf16)),
+                          ptr(np.ascontiguousarray(norm_w, dtype=np.float32)), experts, hidden,
+                          top_k, ptr(np.ascontiguousarray(x, dtype=np.float32)), eps, int(refined),
+                          ptr(ids), ptr(w), ptr(post), ptr(logits))
+    if rc != 0:
+        raise ValueError(f"route refused: rc {rc}")
+    return ids, w, post, logits
+
+
+def swiglu(gu, i: int):
+    act = np.empty(i, dtype=np.float32)
+    lib().oref_swiglu(ptr(np.ascontiguousarray(gu, dtype=np.float32)), i, ptr(act))
+    return act
+
+
+def kv_layout(num_blocks, block_size, layers, kv_heads, head_dim) -> KvLayout:
+    lay = KvLayout()
+    lib().oref_kv_layout_bf16(num_blocks, block_size, layers, kv_heads, head_dim, C.byref(lay))
+    return lay
+
+
+def fnv1a64(b: bytes | np.ndarray) -> int:
+    arr = np.frombuffer(bytes(b), dtype=np.uint8) if isinstance(b, (bytes, bytearray)) else \
+        np.ascontiguousarray(b).view(np.uint8).reshape(-1)
+    return int(lib().oref_fnv1a64(ptr(arr), arr.size))
+
+
+class Dattn:
+    """The fused decode-attention cache oracle (bf16 rows, f64 attention)."""
+
+    def __init__(self, layers: int, max_pos: int, theta: float):
+        self.h = lib().oref_dattn_alloc(layers, max_pos, theta)
+
+    def set_norms(self, layer, qn, kn):
+        lib().oref_dattn_set_norms(self.h, layer, ptr(np.ascontiguousarray(qn, dtype=np.float32)),
+                                   ptr(np.ascontiguousarray(kn, dtype=np.float32)))
+
+    def attend(self, layer, pos, qkv, eps, out_scale=1.0):
+        out = np.empty(4096, dtype=np.float32)
+        lib().oref_dattn_attend(self.h, layer, pos,
+                                ptr(np.ascontiguousarray(qkv, dtype=np.float32)), eps, out_scale,
+                                ptr(out))
+        return out
+
+    def read_row(self, layer, head, pos):
+        k = np.empty(128, dtype=np.uint16)
+        v = np.empty(128, dtype=np.uint16)
+        lib().oref_dattn_read_row(self.h, layer, head, pos, ptr(k), ptr(v))
+        return k, v
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oref_dattn_free(self.h)
+            self.h = None
+
+
+class Model:
+    """Synthetic random-init model and the whole-step engine of the oracle."""
+
+    def __init__(self, cfg: dict, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0,
+                 threads: int = 1):
+        self.cfg = Config(**cfg)
+        self.h = lib().oref_model_synth(C.byref(self.cfg), seed, sigma, norm_sigma, threads)
+
+    def tensor(self, layer: int, kind: int):
+        """kind 0..3: (w, s) of qkv, o, gate_up, down; 4: router bf16; 5..8: norms."""
+        c = self.cfg
+        hd, h = c.head_dim, c.hidden
+        sp = C.c_void_p()
+        p = lib().oref_model_tensor(self.h, layer, kind, C.byref(sp))
+        qkv_n = (c.q_heads + 2 * c.kv_heads) * hd
+        shapes = {0: (1, qkv_n, h), 1: (1, h, c.q_heads * hd), 2: (c.experts, 2 * c.inter, h),
+                  3: (c.experts, h, c.inter)}
+        if kind in shapes:
+            e, n, k = shapes[kind]
+            w = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(e, n, k))
+            s = np.ctypeslib.as_array(C.cast(sp, C.POINTER(C.c_uint16)),
+                                      shape=(e, n // 128, k // 128))
+            return w, s
+        if kind == 4:
+            return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(c.experts, h))
+        n = {5: h, 6: h, 7: hd, 8: hd}[kind]
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(n,))
+
+    def embed(self):
+        c = self.cfg
+        p = lib().oref_model_embed(self.h)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(c.vocab, c.hidden))
+
+    def lm_head(self):
+        c = self.cfg
+        p = lib().oref_model_lm_head(self.h)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(c.vocab, c.hidden))
+
+    def final_norm(self):
+        p = lib().oref_model_final_norm(self.h)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(self.cfg.hidden,))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oref_model_free(self.h)
+            self.h = None
+
+
+class Engine:
+    def __init__(self, model: Model, max_pos: int, refined_router: bool = True,
+                 threads: int = 1):
+        self.model = model
+        self.h = lib().oref_engine_new(model.h, max_pos, int(refined_router), threads)
+
+    def step(self, token: int) -> np.ndarray:
+        out = np.empty(self.model.cfg.hidden, dtype=np.float32)
+        rc = lib().oref_engine_step(self.h, token, ptr(out))
+        if rc != 0:
+            raise RuntimeError(f"oracle step failed: {rc}")
+        return out
+
+    def logits(self, hidden) -> np.ndarray:
+        out = np.empty(self.model.cfg.vocab, dtype=np.float32)
+        lib().oref_engine_logits(self.h, ptr(np.ascontiguousarray(hidden, dtype=np.float32)),
+                                 ptr(out))
+        return out
+
+    def last_routes(self):
+        c = self.model.cfg
+        ids = np.empty((c.layers, c.top_k), dtype=np.uint32)
+        w = np.empty((c.layers, c.top_k), dtype=np.float32)
+        m = np.empty(c.layers, dtype=np.float32)
+        lib().oref_engine_last_routes(self.h, ptr(ids), ptr(w), ptr(m))
+        return ids, w, m
+
+    def last_x(self):
+        x = np.empty(self.model.cfg.hidden, dtype=np.float32)
+        lib().oref_engine_last_x(self.h, ptr(x))
+        return x
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oref_engine_free(self.h)
+            self.h = None
