@@ -1,0 +1,112 @@
+// Internal runtime of libomega_gpu: one HIP stream per process, the error strings of every ABI
+// family, pinned staging buffers, a self-resetting counter pool for the kernels' last-arriver
+// reductions, and the device-side kernel declarations shared by the entry points and the decode
+// graph.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdarg>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+
+#include "omega_gpu.h"
+
+namespace omega {
+
+enum Family { F_FP8 = 0, F_GEMM, F_ROUTER, F_DATTN, F_BF16, F_SESSION, F_ATTN, F_MATMUL, F_COUNT };
+
+void set_error(Family f, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error(Family f);
+const char *last_error(Family f);
+const char *rc_name(int rc);
+
+// One lock for every entry point: handles are single-threaded by contract, global state (the
+// stream, staging, workspaces, tuning knobs) is shared.
+std::recursive_mutex &big_lock();
+
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    char arch[64] = {0};
+    int cus = 0;
+    // pinned host staging (grows)
+    void *pin = nullptr;
+    size_t pin_bytes = 0;
+    // device scratch (grows; never used by a captured graph)
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // zero-initialised counters, each kernel leaves the ones it used at zero
+    uint32_t *counters = nullptr;
+    size_t n_counters = 0;
+};
+
+// Initialises on first use (device = current device). Returns nullptr and sets the family's
+// error when HIP is unavailable.
+Ctx *ctx(Family f);
+// Grow helpers; return false (error set) on allocation failure.
+bool ensure_pinned(Family f, Ctx *c, size_t bytes);
+bool ensure_scratch(Family f, Ctx *c, size_t bytes);
+// Counters for standalone calls: [0, n_counters) of the pool (1 << 20 entries).
+uint32_t *counters(Ctx *c);
+
+// HIP call check: on failure sets the family error and returns CHIP_FAIL from the caller.
+#define OMEGA_HIP(fam, call)                                                                    \
+    do {                                                                                        \
+        hipError_t e_ = (call);                                                                 \
+        if (e_ != hipSuccess) {                                                                 \
+            ::omega::set_error((fam), "%s: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, \
+                               __LINE__);                                                       \
+            return OMEGA_GPU_CHIP_FAIL;                                                         \
+        }                                                                                       \
+    } while (0)
+
+inline uint64_t now_ns() {
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+// elapsed of the last ev0 -> ev1 pair, ns
+uint64_t event_ns(Ctx *c);
+void fill_chip(char *target_chip, uint32_t *sm_arch, Ctx *c);
+
+// ------------------------------------------------------------------ shared tunables / mutants
+struct Knobs {
+    int fp8_mutant = 0;
+    int fp8_no_fold = 0;
+    int fp8_sealed = 0;
+    uint32_t fp8_cta_budget = 0;
+    int gemm_mutant = 0;
+    int router_mutant = 0;
+    int dattn_mutant = 0;
+    uint32_t dattn_per_split = 0;
+    uint32_t dattn_depth = 0;
+    int bf16_mutant = 0;
+    uint32_t spin_us = 0;
+};
+Knobs &knobs();
+
+}  // namespace omega
+
+// ---------------------------------------------------------------------------- object layouts
+// Device layout of an FP8 tensor: for every expert, rows in tiles of 64 and columns in steps of
+// 16 bytes, one 1 KiB chunk per (tile, step): byte (r, c) of expert e sits at
+//   e*n*k + ((r/64) * (k/16) + c/16) * 1024 + (r%64) * 16 + c%16
+// so a wavefront reads 1 KiB contiguously per step and lane l owns row 64*tile + l. Scales are
+// f32 [expert][n/128][k/128].
+struct OmegaGpuFp8Tensor {
+    uint32_t experts = 0, n = 0, k = 0;
+    uint8_t *w = nullptr;
+    float *s = nullptr;
+};
+
+// Device layout of a bf16 tensor: rows padded to a multiple of 64, tiles of 64 rows, steps of
+// 8 columns (16 bytes): element (r, c) at ((r/64) * (k/8) + c/8) * 512 + (r%64) * 8 + c%8.
+struct OmegaGpuBf16Tensor {
+    uint32_t n = 0, k = 0, n_pad = 0;
+    uint16_t *w = nullptr;
+};

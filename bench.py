@@ -1,0 +1,255 @@
+"""Benchmark of the Qwen3-30B-A3B FP8 decode step on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): the full 48-layer random-init
+Qwen3-30B-A3B FP8 model (hidden 2048, 32 q / 4 kv heads of 128, 128 experts top-8 with
+intermediate 768, vocab 151936, RMSNorm eps 1e-6, RoPE theta 1e6, bf16 embedding and lm_head
+N(0, 0.02), FP8 projections N(0, 0.02) block-quantised, norm weights 1.0), weights synthesised
+on the device by the library's counter-based generator (the same values the CPU oracle
+generates). A seeded 512-token prompt runs through the decode graph first (untimed), then
+`warmup` greedy tokens, then exactly `steps` timed greedy tokens at bs=1, each one
+hipGraph replay (token id in, greedy token out). value = tokens / second.
+
+The JSON line also carries:
+  roofline: the dominant kernel's algorithmic bytes per launch over its average duration, the
+            durations measured with HIP events on the library stream over a stamped pass of
+            the same decode steps; peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
+            summary for that kernel when one exists (profiles/), else null.
+  cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
+            host cores: a bounded sample of 2 of the 48 layers x 4 tokens plus one full-vocab
+            lm_head, scaled to the 48-layer step.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(REPO, "aien-sovereign-core-mv_amd"), os.path.join(REPO, "oracle")]
+
+import numpy as np  # noqa: E402
+
+METRIC = "Qwen3-30B-A3B FP8 decode tok/s at bs1/bs32; achieved HBM TB/s vs peak"
+L, H, QH, KVH, HD, E, TOPK, I, V = 48, 2048, 32, 4, 128, 128, 8, 768, 151936
+SEED = 20261201
+PEAK_GBS = 8000.0
+
+
+def tid(layer, kind):
+    # tensor ids of the generator, shared with the CPU oracle's synthetic model
+    return 1000 + layer * 16 + kind
+
+
+def algorithmic_bytes(kind, ctx):
+    """HBM bytes one launch of a decode-graph kernel must move (weights, scales, activations)."""
+    if kind == "qkv":      # 5120 x 2048 e4m3 + f32 scales + x in + q out + K/V rows
+        return 5120 * 2048 + 40 * 16 * 4 + H * 4 + 4096 * 4 + 2 * 512 * 2
+    if kind == "attn":     # K and V of 4 heads over ctx positions + q + out
+        return 2 * KVH * ctx * HD * 2 + 2 * 4096 * 4
+    if kind == "o_proj":   # 2048 x 4096 e4m3 + scales + attn in + residual read/write
+        return 2048 * 4096 + 16 * 32 * 4 + 4096 * 4 + 2 * H * 4
+    if kind == "router":   # bf16 gate + norm + x in + x' out
+        return E * H * 2 + 3 * H * 4
+    if kind == "gate_up":  # 8 experts x 1536 x 2048 e4m3 + scales + x' + activation out
+        return TOPK * (1536 * 2048 + 12 * 16 * 4) + H * 4 + TOPK * I * 4
+    if kind == "down":     # 8 experts x 2048 x 768 e4m3 + scales + activations + residual
+        return TOPK * (2048 * 768 + 16 * 6 * 4) + TOPK * I * 4 + 2 * H * 4
+    if kind == "lm_head":  # 151936 x 2048 bf16 + final norm + logits
+        return V * H * 2 + 2 * H * 4 + V * 4
+    return 0
+
+
+def build_model(om, max_pos):
+    t0 = time.time()
+    router = om.Router(L)
+    cache = om.DecodeAttnCache(L, max_pos, 1e6)
+    ones = np.ones(H, np.float32)
+    layers = []
+    for l in range(L):
+        qkv = om.Fp8Tensor.synth(1, 5120, 2048, SEED, tid(l, 0))
+        o = om.Fp8Tensor.synth(1, 2048, 4096, SEED, tid(l, 1))
+        gu = om.Fp8Tensor.synth(E, 1536, 2048, SEED, tid(l, 2))
+        dn = om.Fp8Tensor.synth(E, 2048, 768, SEED, tid(l, 3))
+        layers.append((qkv, o, gu, dn))
+        router.set_layer(l, om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02), ones)
+        router.set_directory(l, np.array([gu.entry(e) for e in range(E)], np.uint64),
+                             np.array([dn.entry(e) for e in range(E)], np.uint64))
+        cache.set_norms(l, np.ones(HD, np.float32), np.ones(HD, np.float32))
+    lm = om.Bf16Tensor.synth(V, H, SEED, 2, 0.02)
+    embed = om.Bf16Tensor.synth(V, H, SEED, 1, 0.02)
+    g = om.DecodeGraph(L, V, 1e-6, router, cache, lm)
+    for l, (qkv, o, gu, dn) in enumerate(layers):
+        g.set_layer(l, qkv, o, gu, dn, ones)
+    g.set_final_norm(ones)
+    g.set_embedding(embed)
+    om.sync()
+    return dict(graph=g, layers=layers, router=router, cache=cache, lm=lm, embed=embed,
+                seconds=time.time() - t0)
+
+
+def cpu_baseline(threads):
+    """The oracle engine on a bounded sample, scaled to the 48-layer step (see module doc)."""
+    import pyoracle as orc
+
+    cfg = dict(layers=2, hidden=H, q_heads=QH, kv_heads=KVH, head_dim=HD, experts=E, top_k=TOPK,
+               inter=I, vocab=V, eps=1e-6, rope_theta=1e6)
+    m = orc.Model(cfg, SEED, sigma=0.02, norm_sigma=0.0, threads=threads)
+    eng = orc.Engine(m, 256, refined_router=True, threads=threads)
+    tokens = 4
+    hid = eng.step(1)   # first touch of every weight page
+    t0 = time.perf_counter()
+    for t in range(tokens):
+        hid = eng.step(2 + t)
+    t_layers = (time.perf_counter() - t0) / tokens / cfg["layers"]
+    t1 = time.perf_counter()
+    eng.logits(hid)
+    t_lm = time.perf_counter() - t1
+    step = t_layers * L + t_lm
+    return {"value": round(1.0 / step, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"C oracle engine (oracle/oracle.c, {threads} threads, per-output-row "
+                      f"parallel GEMV): 2 of 48 layers x {tokens} tokens at positions 1-4 "
+                      f"({t_layers * 1e3:.1f} ms/layer) + one 151936-row lm_head "
+                      f"({t_lm * 1e3:.1f} ms), scaled to 48 layers: {step:.3f} s/token"}
+
+
+def committed_traffic(kind):
+    """HBM bytes per launch of `kind` from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(REPO, "profiles", f"{kind}_traffic.md")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels directly instead of replaying the hipGraph "
+                         "(for profilers that cannot follow graph capture)")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the decode step runs on a single MI355X and this build "
+              "has no multi-GPU path (--gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import omega_amd as om
+
+    if om.gpu_count() == 0:
+        print("bench.py needs an MI355X", file=sys.stderr)
+        sys.exit(3)
+    total = args.prompt + args.warmup + args.steps + 8
+    max_pos = om.round_max_pos(total)
+    model = build_model(om, max_pos)
+    g = model["graph"]
+    if args.eager:
+        g.set_flush_each(2)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, V, args.prompt).tolist()
+    pos = 0
+    tok = prompt[0]
+    t_prompt = time.perf_counter()
+    for p in range(args.prompt):
+        nxt, _ = g.token_id(prompt[p], pos)
+        pos += 1
+        tok = nxt
+    t_prompt = time.perf_counter() - t_prompt
+    for _ in range(args.warmup):
+        tok, _ = g.token_id(tok, pos)
+        pos += 1
+    om.sync()
+    t0 = time.perf_counter()
+    generated = []
+    for _ in range(args.steps):
+        tok, st = g.token_id(tok, pos)
+        generated.append(tok)
+        pos += 1
+    om.sync()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = args.steps / elapsed
+
+    # per-kernel durations: the same decode steps with HIP events between the launches
+    g.set_stamps(True)
+    per_kind = {}
+    stamp_tokens = 4
+    ctx_mid = pos + stamp_tokens // 2
+    for _ in range(stamp_tokens):
+        tok, _ = g.token_id(tok, pos)
+        pos += 1
+        st, kinds = g.stamps()
+        d = np.diff(st.astype(np.int64))
+        for k, dt in zip(kinds, d):
+            name = om.KIND_NAMES[int(k)]
+            per_kind.setdefault(name, []).append(int(dt))
+    g.set_stamps(False)
+    kernels = {}
+    for name, ds in per_kind.items():
+        n_launch = len(ds) / stamp_tokens
+        avg_ns = float(np.mean(ds))
+        b = algorithmic_bytes(name, ctx_mid)
+        kernels[name] = dict(launches_per_token=n_launch, avg_us=round(avg_ns / 1e3, 3),
+                             us_per_token=round(avg_ns * n_launch / 1e3, 2),
+                             algorithmic_bytes=b, gbs=round(b / avg_ns, 1))
+    dom = max(kernels, key=lambda k: kernels[k]["us_per_token"])
+    dk = kernels[dom]
+    achieved = dk["algorithmic_bytes"] / (dk["avg_us"] * 1e3)
+    step_bytes = sum(algorithmic_bytes(k, ctx_mid) * int(v["launches_per_token"])
+                     for k, v in kernels.items())
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads)
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8",
+        "data": "synthetic (random-init weights from the seeded counter-based generator, "
+                "seeded 512-token prompt)",
+        "config": {
+            "workload": "Qwen3-30B-A3B FP8 decode step, bs=1, "
+                        + ("direct kernel launches" if args.eager else "one hipGraph per token")
+                        + f", {args.prompt}-token prompt then greedy decode",
+            "layers": L, "hidden": H, "q_heads": QH, "kv_heads": KVH, "head_dim": HD,
+            "experts": E, "top_k": TOPK, "moe_intermediate": I, "vocab": V,
+            "global_batch": 1, "context": f"{args.prompt + args.warmup}-{pos}",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": committed_traffic(dom),
+        },
+        "step_roofline": {
+            "algorithmic_bytes_per_token": step_bytes,
+            "achieved_GBs": round(step_bytes / (ms_per_step * 1e6), 1),
+            "frac": round(step_bytes / (ms_per_step * 1e6) / PEAK_GBS, 4),
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "extra": {"model_build_s": round(model["seconds"], 1),
+                  "prompt_s": round(t_prompt, 2),
+                  "generated_head": generated[:8]},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
