@@ -1,16 +1,26 @@
-// Decode attention for gfx950: the paged flash-decoding core (GQA over the aien-kv-cache page
-// layout), the q|k|v preparation (per-head RMSNorm, RoPE from a resident table, bf16 K/V
-// append), the fused decode-attention cache (omega_gpu_decode_attn_*) and the paged entry points
-// (omega_gpu_paged_attention_bf16 / _batch_bf16).
+// Decode attention for gfx950: the fused decode-attention cache (omega_gpu_decode_attn_*) with
+// its matrix-core flash-decoding kernel, the paged flash-decoding over external pools
+// (omega_gpu_paged_attention_bf16 / _batch_bf16 / _batch_dev), and the split combine.
 //
 // Contracts: crates/aien-omega-dattn/src/lib.rs:16-29 (fused), crates/aien-omega-gpu/src/ffi.rs:
 // 433-461 and src/lib.rs:913-1028 (paged). Host oracle: scaled_dot_product_attention_single
 // (crates/aien-inference-abi/src/tensor.rs:193-250) over the bf16 rows of the pool, as
-// HostPoolKv::attend does (qwen3_moe_omega.rs:2842-2868).
+// HostPoolKv::attend does (qwen3_moe_omega.rs:2842-2868); the q|k|v preparation is
+// rmsnorm_per_head (qwen3_coder.rs:306-320, f64 sum of squares) then apply_rope
+// (tensor.rs:164-190) and the bf16 append of aien-kv-cache write_token_kv.
 //
-// The fused cache keeps its K/V in the same page layout as the paged pool (16-token pages,
-// [block][layer][K|V][token][kv head][128] bf16) with the identity block table, so one attention
-// kernel serves both ABIs and the persistent-KV export of the cache is a block copy.
+// Fused kernel (k_dattn): per (split, kv head) one wavefront. The tokens before `pos` are cut
+// into tiles of 64 spread over the splits. Both products run on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16) with the f32 operand split into a bf16 (hi, lo) pair: the 16
+// B-columns of S^T = K q^T are the 8 q heads' hi and lo halves, the 16 A-rows of O = P V are
+// the 8 heads' probability hi and lo halves, and hi + lo rows are added at the end — products
+// with the bf16 K / V are exact, so the result carries about 2^-16 relative error per operand
+// instead of bf16's 2^-8. Token order inside a tile is permuted (tau below) so that every lane
+// reads K as 64 contiguous bytes per row and V as 16 contiguous bytes per (dim, 8 tokens), which
+// is why the cache stores each page's V plane transposed ([head][dim][16 tokens]). Split 0 also
+// appends this token's K/V and folds it in as one more online-softmax step. A second small
+// launch combines the splits (k_attn_combine); nothing is exchanged between workgroups inside a
+// launch.
 #include <cmath>
 #include <cstdio>
 #include <vector>
@@ -22,21 +32,296 @@
 namespace omega {
 
 constexpr float kInvSqrt128 = 0.08838834764831845f;
+constexpr uint32_t kVtHead = 4096;  // bytes per kv head of a transposed V plane (128 dims x 32 B)
 
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// token of row m of block b in a 64-token tile
+__device__ __forceinline__ uint32_t tile_token(uint32_t b, uint32_t m) {
+    return 16 * (m / 4) + 8 * (b / 2) + 4 * (b % 2) + (m % 4);
+}
+
+struct DattnTile {
+    u32x4 k[4][4];  // [block][k-step]: K[token][32 g + 8 ks .. +8]
+    u32x4 v[2][8];  // [pv step][n-block]: V^T[dim 16 nb + n][tokens 8 p .. +8] of page g
+};
+
+__device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint32_t tile, uint32_t lane,
+                                           DattnTile &T) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t tok0 = tile * kAttnTile;
+    const uint8_t *lay = a.pool + (uint64_t)a.layer * a.g.layer_stride;
+#pragma unroll
+    for (uint32_t b = 0; b < 4; ++b) {
+        const uint32_t tok = tok0 + tile_token(b, n);
+        const gu32x4 *kp = as_global(lay + (uint64_t)(tok >> 4) * a.g.block_stride +
+                                     (uint64_t)(tok & 15) * a.g.token_stride +
+                                     (uint64_t)h * a.g.head_stride + 64 * g);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) T.k[b][ks] = __builtin_nontemporal_load(kp + ks);
+    }
+    const uint8_t *vp = lay + (uint64_t)((tok0 >> 4) + g) * a.g.block_stride + a.g.plane_stride +
+                        (uint64_t)h * kVtHead + n * 32;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+            T.v[p][nb] = __builtin_nontemporal_load(as_global(vp + nb * 16 * 32 + p * 16));
+}
+
+// RMSNorm of one head held as (dims lane, lane + 64), f64 sum of squares, then RoPE
+__device__ __forceinline__ void head_norm_rope(float &v0, float &v1, float w0, float w1, float rc,
+                                               float rs, float eps, bool rope) {
+    const double ss = wave_sum_f64((double)v0 * (double)v0 + (double)v1 * (double)v1);
+    const float scale = rms_scale(ss, 128, eps);
+    float n0 = v0 * scale * w0;
+    float n1 = v1 * scale * w1;
+    if (rope) {
+        const float r0 = __fsub_rn(__fmul_rn(n0, rc), __fmul_rn(n1, rs));
+        const float r1 = __fadd_rn(__fmul_rn(n0, rs), __fmul_rn(n1, rc));
+        n0 = r0;
+        n1 = r1;
+    }
+    v0 = n0;
+    v1 = n1;
+}
+
+__global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
+    __shared__ float qs[8][128];
+    __shared__ float vs[128];
+    const uint32_t lane = threadIdx.x, s = blockIdx.x, h = blockIdx.y;
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t pos = a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host;
+    const uint32_t tiles = (pos + kAttnTile - 1) / kAttnTile;
+    uint32_t active, tps;
+    attn_split_plan(tiles, gridDim.x, a.tiles_per_split, active, tps);
+    if (s >= active) return;
+    const uint32_t t_begin = s * tps, t_end = min(tiles, t_begin + tps);
+
+    // prologue loads: the 8 q heads (dims lane, lane + 64), norms and the RoPE row at pos
+    const float *qraw = a.qkv + h * 8 * 128;
+    float q0[8], q1[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        q0[r] = *as_global_f32(qraw + r * 128 + lane);
+        q1[r] = *as_global_f32(qraw + r * 128 + 64 + lane);
+    }
+    const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
+    const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
+    const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
+    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f, kw0 = 0.f, kw1 = 0.f;
+    if (s == 0) {
+        k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
+        k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
+        v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
+        v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
+        kw0 = *as_global_f32(a.k_norm + lane);
+        kw1 = *as_global_f32(a.k_norm + 64 + lane);
+    }
+    // the first tile's K/V stream starts before the preparation math
+    DattnTile T;
+    if (t_begin < t_end) dattn_load(a, h, t_begin, lane, T);
+
+    const bool rope = a.mutant != 1;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        head_norm_rope(q0[r], q1[r], qw0, qw1, rc, rs, a.eps, rope);
+        qs[r][lane] = q0[r];
+        qs[r][lane + 64] = q1[r];
+    }
+    float spos[8];
+    if (s == 0) {
+        head_norm_rope(k0, k1, kw0, kw1, rc, rs, a.eps, rope);
+        const uint16_t kb0 = bf16_rne(k0), kb1 = bf16_rne(k1);
+        const uint16_t vb0 = bf16_rne(v0), vb1 = bf16_rne(v1);
+        if (a.mutant != 3) {
+            uint16_t *krow = reinterpret_cast<uint16_t *>(
+                a.pool + kv_row_offset(a.g, pos >> 4, a.layer, 0, pos & 15, h));
+            krow[lane] = kb0;
+            krow[lane + 64] = kb1;
+            const uint32_t vpos = a.mutant == 2 ? min(pos + 1, a.max_pos - 1) : pos;
+            uint8_t *vplane = a.pool + (uint64_t)(vpos >> 4) * a.g.block_stride +
+                              (uint64_t)a.layer * a.g.layer_stride + a.g.plane_stride +
+                              (uint64_t)h * kVtHead + (vpos & 15) * 2;
+            *reinterpret_cast<uint16_t *>(vplane + lane * 32) = vb0;
+            *reinterpret_cast<uint16_t *>(vplane + (lane + 64) * 32) = vb1;
+        }
+        const float kf0 = bf16_to_f32(kb0), kf1 = bf16_to_f32(kb1);
+        vs[lane] = bf16_to_f32(vb0);
+        vs[lane + 64] = bf16_to_f32(vb1);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) spos[r] = wave_sum(fmaf(q0[r], kf0, q1[r] * kf1)) * kInvSqrt128;
+    }
+    __syncthreads();  // qs / vs complete (waits on LDS only: the K/V stream stays in flight)
+
+    // B operand of S^T = K q^T: head column n is head n % 8, its hi (n < 8) or lo (n >= 8) half;
+    // k-step ks of lane group g covers dims 32 g + 8 ks .. +8
+    bf16x8 qop[4];
+    {
+        const uint32_t r = n & 7;
+        const bool hi = n < 8;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const float *qq = &qs[r][32 * g + 8 * ks];
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a0 = qq[2 * j], a1 = qq[2 * j + 1];
+                const uint32_t b0 = hi ? bf16_split_hi(a0) : bf16_split_lo(a0);
+                const uint32_t b1 = hi ? bf16_split_hi(a1) : bf16_split_lo(a1);
+                w[j] = b0 | (b1 << 16);
+            }
+            qop[ks] = as_bf16x8(w);
+        }
+    }
+
+    float m_l = -INFINITY, l_l = 0.f;  // online-softmax state of head n % 8
+    f32x4 O[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t t = t_begin; t < t_end; ++t) {
+        if (t != t_begin) dattn_load(a, h, t, lane, T);
+        const uint32_t tok0 = t * kAttnTile;
+        float sc[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[b][ks]), qop[ks], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float full = acc[i] + dpp_f32<DPP_ROR8>(acc[i]);  // hi + lo columns
+                const uint32_t tok = tok0 + tile_token(b, 4 * g + i);
+                sc[b][i] = tok < pos ? full * kInvSqrt128 : -INFINITY;
+            }
+        }
+        float mx = sc[0][0];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[b][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_l, mx);
+        const float alpha = expf(m_l - m_new);
+        float pr[4][4];
+        float psum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pr[b][i] = expf(sc[b][i] - m_new);
+                psum += pr[b][i];
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l_l = l_l * alpha + psum;
+        m_l = m_new;
+        // rescale the accumulators: rows 4 g + i hold head (4 g + i) % 8
+        float ah[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) ah[r] = readlane_f32(alpha, r);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = (g & 1) ? ah[4 + i] : ah[i];
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
+        }
+        // A operand of O = P V: row n = head n % 8, its hi or lo half; k = 8 g + j is token
+        // 16 g + 8 p + j of the tile (blocks 2p and 2p + 1 of the scores)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            u32x4 w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float a0 = j < 2 ? pr[2 * p][2 * j] : pr[2 * p + 1][2 * j - 4];
+                const float a1 = j < 2 ? pr[2 * p][2 * j + 1] : pr[2 * p + 1][2 * j - 3];
+                const uint32_t b0 = n < 8 ? bf16_split_hi(a0) : bf16_split_lo(a0);
+                const uint32_t b1 = n < 8 ? bf16_split_hi(a1) : bf16_split_lo(a1);
+                w[j] = b0 | (b1 << 16);
+            }
+            const bf16x8 pop = as_bf16x8(w);
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb)
+                O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, as_bf16x8(T.v[p][nb]), O[nb], 0, 0, 0);
+        }
+    }
+    // hi rows (lane groups 0, 1) + lo rows (groups 2, 3)
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[nb][i] += __shfl_xor(O[nb][i], 32, 64);
+    float mh[8], lh[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        mh[r] = readlane_f32(m_l, r);
+        lh[r] = readlane_f32(l_l, r);
+    }
+    if (s == 0) {
+        // this token: one more online-softmax step with score spos and value vs
+        float aold[8], pp[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const float m_new = fmaxf(mh[r], spos[r]);
+            aold[r] = expf(mh[r] - m_new);
+            pp[r] = expf(spos[r] - m_new);
+            lh[r] = lh[r] * aold[r] + pp[r];
+            mh[r] = m_new;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = (g & 1) ? aold[4 + i] : aold[i];
+            const float pi = (g & 1) ? pp[4 + i] : pp[i];
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) O[nb][i] = fmaf(pi, vs[16 * nb + n], O[nb][i] * ai);
+        }
+    }
+    float *part = a.part + ((size_t)h * 8 * kDattnSplits + s) * kPartStride;
+    if (g < 2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float *pp = part + (size_t)(4 * g + i) * kDattnSplits * kPartStride;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) pp[4 + 16 * nb + n] = O[nb][i];
+        }
+    }
+    if (lane < 8) {
+        float mm = 0.f, ll = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            if (lane == (uint32_t)r) {
+                mm = mh[r];
+                ll = lh[r];
+            }
+        float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
+        pp[0] = mm;
+        pp[1] = ll;
+    }
+}
+
+hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_dattn, dim3(kDattnSplits, 4), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------ paged (VALU)
+// One wavefront per (split, kv head, seq): lane = token for Q K (K row per lane, q read
+// wave-uniformly), lane = dim pair for P V.
 template <int R>  // q heads per kv head
 __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
     __shared__ float P[R][64];
     const uint32_t lane = threadIdx.x;
     const uint32_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const uint32_t ctx = a.context_lens ? (uint32_t)a.context_lens[b]
-                                        : (a.pos_dev ? *a.pos_dev : a.pos_host) + 1;
-    const uint32_t S = a.splits;
-    // tokens per split: whole 64-token sub-chunks
-    const uint32_t per = ((ctx + S - 1) / S + 63) / 64 * 64;
-    const uint32_t start = c * per;
-    const uint32_t end = min(ctx, start + per);
+    const uint32_t ctx = (uint32_t)a.context_lens[b];
+    const uint32_t tiles = (ctx + kAttnTile - 1) / kAttnTile;
+    uint32_t active, tps;
+    attn_split_plan(tiles, gridDim.x, 0, active, tps);
+    if (c >= active) return;
+    const uint32_t start = c * tps * kAttnTile;
+    const uint32_t end = min(ctx, start + tps * kAttnTile);
     const float *q = a.q + ((size_t)b * a.qh + h * R) * 128;
-    const int32_t *tab = a.block_tables ? a.block_tables + (size_t)b * a.max_blocks : nullptr;
+    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
     const uint32_t bs = a.g.block_size;
 
     float m[R], l[R], o0[R], o1[R];
@@ -54,7 +339,7 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) sc[r] = 0.f;
         if (valid) {
-            const uint32_t blk = tab ? (uint32_t)tab[tok / bs] : tok / bs;
+            const uint32_t blk = (uint32_t)tab[tok / bs];
             const gu32x4 *kp = as_global(a.pool + kv_row_offset(a.g, blk, a.layer, 0, tok % bs, h));
             u32x4 kv[16];
 #pragma unroll
@@ -63,8 +348,8 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
             for (int i = 0; i < 16; ++i) {
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
-                    const float k0 = __uint_as_float(kv[i][qd] << 16);
-                    const float k1 = __uint_as_float(kv[i][qd] & 0xffff0000u);
+                    const float k0 = bf16_lo(kv[i][qd]);
+                    const float k1 = bf16_hi(kv[i][qd]);
                     const int d = i * 8 + qd * 2;
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
@@ -74,10 +359,9 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
                 }
             }
         }
-        // online softmax over this sub-chunk
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float s = valid ? sc[r] * kInvSqrt128 : -INFINITY;
+            const float s = valid ? sc[r] * kInvSqrt128 : -INFINITY;
             float mx = s;
             for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
             const float mn = fmaxf(m[r], mx);
@@ -92,27 +376,36 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
             P[r][lane] = p;
         }
         __syncthreads();
-        // P V: lane owns dims 2*lane, 2*lane+1
         const uint32_t nt = min(64u, end - sub);
-        for (uint32_t t = 0; t < nt; ++t) {
-            uint32_t tv = sub + t;
-            if (a.mutant == 2) tv = min(tv + 1, ctx - 1);
-            const uint32_t blk = tab ? (uint32_t)tab[tv / bs] : tv / bs;
-            const uint32_t w2 =
-                *as_global_u32(a.pool + kv_row_offset(a.g, blk, a.layer, 1, tv % bs, h) + lane * 4);
-            const float v0 = __uint_as_float(w2 << 16), v1 = __uint_as_float(w2 & 0xffff0000u);
+        for (uint32_t t0 = 0; t0 < nt; t0 += 16) {
+            // 16 V rows in flight per lane (a dim pair each)
+            uint32_t w2[16];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                o0[r] = fmaf(P[r][t], v0, o0[r]);
-                o1[r] = fmaf(P[r][t], v1, o1[r]);
+            for (int j = 0; j < 16; ++j) {
+                uint32_t tv = sub + t0 + j;
+                if (a.mutant == 2) tv = min(tv + 1, ctx - 1);
+                w2[j] = 0;
+                if (t0 + j < nt) {
+                    const uint32_t blk = (uint32_t)tab[tv / bs];
+                    w2[j] = *as_global_u32(a.pool + kv_row_offset(a.g, blk, a.layer, 1, tv % bs, h) + lane * 4);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (t0 + j >= nt) break;
+                const float v0 = bf16_lo(w2[j]), v1 = bf16_hi(w2[j]);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    o0[r] = fmaf(P[r][t0 + j], v0, o0[r]);
+                    o1[r] = fmaf(P[r][t0 + j], v1, o1[r]);
+                }
             }
         }
         __syncthreads();
     }
-    // partials of this split: m, l, o
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float *pp = a.part + (((size_t)b * a.qh + h * R + r) * S + c) * 132;
+        float *pp = a.part + (((size_t)b * a.qh + h * R + r) * a.splits + c) * kPartStride;
         if (lane == 0) {
             pp[0] = m[r];
             pp[1] = l[r];
@@ -120,33 +413,6 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
         pp[4 + 2 * lane] = o0[r];
         pp[5 + 2 * lane] = o1[r];
     }
-    __threadfence();
-    uint32_t last = 0;
-    uint32_t *cnt = a.counters + (size_t)b * a.kvh + h;
-    if (lane == 0) last = atomicAdd(cnt, 1u) == S - 1;
-    last = __shfl(last, 0, 64);
-    if (!last) return;
-    __threadfence();
-    const uint32_t nact = (ctx + per - 1) / per;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float *pp = a.part + ((size_t)b * a.qh + h * R + r) * S * 132;
-        float M = -INFINITY;
-        for (uint32_t s2 = 0; s2 < nact; ++s2) M = fmaxf(M, __builtin_nontemporal_load(&pp[s2 * 132]));
-        float L = 0.f, O0 = 0.f, O1 = 0.f;
-        for (uint32_t s2 = 0; s2 < nact; ++s2) {
-            const float ms = __builtin_nontemporal_load(&pp[s2 * 132]);
-            const float wgt = a.mutant == 4 ? 1.0f : expf(ms - M);
-            L = fmaf(__builtin_nontemporal_load(&pp[s2 * 132 + 1]), wgt, L);
-            O0 = fmaf(__builtin_nontemporal_load(&pp[s2 * 132 + 4 + 2 * lane]), wgt, O0);
-            O1 = fmaf(__builtin_nontemporal_load(&pp[s2 * 132 + 5 + 2 * lane]), wgt, O1);
-        }
-        const float inv = a.out_scale / L;
-        float *op = a.out + ((size_t)b * a.qh + h * R + r) * 128;
-        op[2 * lane] = O0 * inv;
-        op[2 * lane + 1] = O1 * inv;
-    }
-    if (lane == 0) atomicExch(cnt, 0u);
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
@@ -161,17 +427,35 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-__global__ __launch_bounds__(64) void k_qkv_prep(const HeadPrep p, const float *qkv,
-                                                 const uint32_t *pos_dev, uint32_t pos_host) {
-    const uint32_t head = blockIdx.x, lane = threadIdx.x;
-    const uint32_t pos = pos_dev ? *pos_dev : pos_host;
-    prep_head(p, head, pos, qkv[head * 128 + lane], qkv[head * 128 + 64 + lane]);
+// ------------------------------------------------------------------------ split combine
+// Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l); fused partials are
+// dims in order. Either way partial dim d sits at 4 + d, so one combine serves both.
+__global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
+    const uint32_t head = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    uint32_t tiles;
+    if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + kAttnTile - 1) / kAttnTile;
+    else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + kAttnTile - 1) / kAttnTile;
+    uint32_t active, tps;
+    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);
+    const float *pp = a.part + ((size_t)b * a.qh + head) * a.splits * kPartStride;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < active; ++s) M = fmaxf(M, pp[s * kPartStride]);
+    float L = 0.f, O0 = 0.f, O1 = 0.f;
+    for (uint32_t s = 0; s < active; ++s) {
+        const float *q = pp + s * kPartStride;
+        const float w = a.mutant == 4 ? 1.0f : expf(q[0] - M);
+        L = fmaf(q[1], w, L);
+        O0 = fmaf(q[4 + lane], w, O0);
+        O1 = fmaf(q[68 + lane], w, O1);
+    }
+    const float inv = a.out_scale / L;
+    float *op = a.out + ((size_t)b * a.qh + head) * 128;
+    op[lane] = O0 * inv;
+    op[lane + 64] = O1 * inv;
 }
 
-hipError_t launch_qkv_prep(const HeadPrep &p, const float *qkv, const uint32_t *pos_dev,
-                           uint32_t pos_host, hipStream_t st) {
-    hipLaunchKernelGGL(k_qkv_prep, dim3(p.qh + 2 * p.kvh), dim3(64), 0, st, p, qkv, pos_dev,
-                       pos_host);
+hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.qh, a.seqs), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -188,12 +472,10 @@ void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out
         }
 }
 
-// splits per (seq, kv head): enough items to cover the GPU, at least 64 tokens each
-uint32_t attn_splits(uint32_t max_ctx, uint32_t seqs, uint32_t kvh, uint32_t cus) {
-    const uint32_t want = (4 * cus + seqs * kvh - 1) / (seqs * kvh);
-    const uint32_t most = (max_ctx + 63) / 64;
-    uint32_t s = want < most ? want : most;
-    return s < 1 ? 1 : s;
+// splits of a paged launch: one tile of 64 tokens per item up to 64 items per (seq, kv head)
+uint32_t paged_splits(uint32_t max_ctx) {
+    const uint32_t t = (max_ctx + kAttnTile - 1) / kAttnTile;
+    return t < 1 ? 1 : (t > 64 ? 64 : t);
 }
 
 KvGeom geom_of(const OmegaGpuKvLayout &l) {
@@ -213,44 +495,33 @@ KvGeom geom_of(const OmegaGpuKvLayout &l) {
 struct OmegaGpuDecodeAttnCache {
     uint32_t layers = 0, max_pos = 0;
     double theta = 0;
-    uint8_t *pool = nullptr;      // [max_pos/16 blocks][layers][K|V][16][4][128] bf16
+    uint8_t *pool = nullptr;      // [max_pos/16 pages][layers][K|V^T] (16 KiB planes)
     omega::KvGeom g{};
     float *q_norm = nullptr, *k_norm = nullptr;  // [layers][128]
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_pos][64]
-    // call buffers
-    float *qkv = nullptr, *q = nullptr, *out = nullptr, *part = nullptr;
-    uint32_t *counters = nullptr;
-    uint32_t part_splits = 0;
+    // call buffers of the standalone entry
+    float *qkv = nullptr, *out = nullptr, *part = nullptr;
 };
 
 using namespace omega;
 
 namespace omega {
 // for the decode graph
-HeadPrep cache_prep(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, float *q_out) {
-    HeadPrep p;
-    p.q_out = q_out;
-    p.pool = c->pool;
-    p.g = c->g;
-    p.layer = layer;
-    p.q_norm = c->q_norm + (size_t)layer * 128;
-    p.k_norm = c->k_norm + (size_t)layer * 128;
-    p.rope_cos = c->rope_cos;
-    p.rope_sin = c->rope_sin;
-    p.eps = eps;
-    p.qh = 32;
-    p.kvh = 4;
-    p.mutant = knobs().dattn_mutant;
-    return p;
-}
-AttnArgs cache_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, const float *q) {
-    AttnArgs a;
-    a.q = q;
+DattnArgs cache_dattn(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, const float *qkv,
+                      float *part) {
+    DattnArgs a;
+    a.qkv = qkv;
     a.pool = c->pool;
     a.g = c->g;
     a.layer = layer;
-    a.qh = 32;
-    a.kvh = 4;
+    a.max_pos = c->max_pos;
+    a.q_norm = c->q_norm + (size_t)layer * 128;
+    a.k_norm = c->k_norm + (size_t)layer * 128;
+    a.rope_cos = c->rope_cos;
+    a.rope_sin = c->rope_sin;
+    a.eps = eps;
+    a.tiles_per_split = knobs().dattn_per_split / kAttnTile;
+    a.part = part;
     a.mutant = knobs().dattn_mutant;
     return a;
 }
@@ -292,7 +563,6 @@ int omega_gpu_decode_attn_cache_alloc(uint32_t layers, uint32_t max_pos, double 
     const size_t pool_bytes = (size_t)(max_pos / 16) * c->g.block_stride;
     std::vector<float> cs((size_t)max_pos * 64), sn((size_t)max_pos * 64);
     rope_table(rope_theta, max_pos, cs.data(), sn.data());
-    c->part_splits = 64;
     hipError_t e = hipMalloc(&c->pool, pool_bytes);
     if (e == hipSuccess) e = hipMemset(c->pool, 0, pool_bytes);
     if (e == hipSuccess) e = hipMalloc(&c->q_norm, (size_t)layers * 128 * 4);
@@ -304,11 +574,8 @@ int omega_gpu_decode_attn_cache_alloc(uint32_t layers, uint32_t max_pos, double 
     if (e == hipSuccess) e = hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&c->qkv, 5120 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->q, 4096 * 4);
     if (e == hipSuccess) e = hipMalloc(&c->out, 4096 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->part, (size_t)32 * c->part_splits * 132 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->counters, 64 * 4);
-    if (e == hipSuccess) e = hipMemset(c->counters, 0, 64 * 4);
+    if (e == hipSuccess) e = hipMalloc(&c->part, (size_t)32 * kDattnSplits * kPartStride * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         set_error(F_DATTN, "decode attn cache alloc (%u layers x %u): %s", layers, max_pos,
@@ -325,8 +592,7 @@ void omega_gpu_decode_attn_cache_free(OmegaGpuDecodeAttnCache *c) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *cx = ctx(F_DATTN);
     if (cx) (void)hipStreamSynchronize(cx->stream);
-    void *ps[] = {c->pool, c->q_norm, c->k_norm, c->rope_cos, c->rope_sin, c->qkv,
-                  c->q, c->out, c->part, c->counters};
+    void *ps[] = {c->pool, c->q_norm, c->k_norm, c->rope_cos, c->rope_sin, c->qkv, c->out, c->part};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     delete c;
@@ -372,31 +638,34 @@ int omega_gpu_decode_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t p
     if (!ensure_pinned(F_DATTN, cx, 5120 * 4)) return OMEGA_GPU_CHIP_FAIL;
     memcpy(cx->pin, qkv, 5120 * 4);
     OMEGA_HIP(F_DATTN, hipMemcpyAsync(c->qkv, cx->pin, 5120 * 4, hipMemcpyHostToDevice, cx->stream));
-    HeadPrep p = cache_prep(c, layer, eps, c->q);
-    AttnArgs a = cache_attn(c, layer, c->q);
+    DattnArgs a = cache_dattn(c, layer, eps, c->qkv, c->part);
     a.pos_host = pos;
-    uint32_t per_split = knobs().dattn_per_split;
-    a.splits = per_split ? (pos + per_split) / per_split : attn_splits(pos + 1, 1, 4, cx->cus);
-    if (a.splits > c->part_splits) a.splits = c->part_splits;
-    a.out_scale = out_scale;
-    a.part = c->part;
-    a.counters = c->counters;
-    a.out = c->out;
+    CombineArgs cb;
+    cb.part = c->part;
+    cb.splits = kDattnSplits;
+    cb.pos_host = pos;
+    cb.tiles_per_split = a.tiles_per_split;
+    cb.qh = 32;
+    cb.out_scale = out_scale;
+    cb.out = c->out;
+    cb.mutant = a.mutant;
     OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev0, cx->stream));
-    OMEGA_HIP(F_DATTN, launch_qkv_prep(p, c->qkv, nullptr, pos, cx->stream));
-    OMEGA_HIP(F_DATTN, launch_attention(a, cx->stream));
+    OMEGA_HIP(F_DATTN, launch_dattn(a, cx->stream));
+    OMEGA_HIP(F_DATTN, launch_attn_combine(cb, cx->stream));
     OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev1, cx->stream));
     OMEGA_HIP(F_DATTN, hipMemcpyAsync(cx->pin, c->out, 4096 * 4, hipMemcpyDeviceToHost, cx->stream));
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
     memcpy(out, cx->pin, 4096 * 4);
     if (info) {
+        uint32_t active, tps;
+        attn_split_plan((pos + kAttnTile - 1) / kAttnTile, kDattnSplits, a.tiles_per_split, active, tps);
         memset(info, 0, sizeof(*info));
         info->layer = layer;
         info->pos = pos;
-        info->splits = a.splits;
-        info->per_split = ((pos + 1 + a.splits - 1) / a.splits + 63) / 64 * 64;
-        info->depth = 16;
-        info->grid_x = a.splits;
+        info->splits = active;
+        info->per_split = tps * kAttnTile;
+        info->depth = 32;
+        info->grid_x = kDattnSplits;
         info->grid_y = 4;
         info->threads = 64;
         info->kv_bytes = 2ull * 4 * (pos + 1) * 256;
@@ -424,12 +693,14 @@ int omega_gpu_decode_attn_cache_write(OmegaGpuDecodeAttnCache *c, uint32_t layer
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
     for (uint32_t i = 0; i < count; ++i) {
         const uint32_t p = pos + i;
-        const uint64_t ko = (uint64_t)(p / 16) * c->g.block_stride + (uint64_t)layer * c->g.layer_stride +
-                            (uint64_t)(p % 16) * c->g.token_stride + (uint64_t)kv_head * c->g.head_stride;
+        const uint64_t page = (uint64_t)(p / 16) * c->g.block_stride + (uint64_t)layer * c->g.layer_stride;
+        const uint64_t ko = page + (uint64_t)(p % 16) * c->g.token_stride + (uint64_t)kv_head * c->g.head_stride;
+        const uint64_t vo = page + c->g.plane_stride + (uint64_t)kv_head * kVtHead + (p % 16) * 2;
         OMEGA_HIP(F_DATTN, hipMemcpyAsync(c->pool + ko, k_bf16 + (size_t)i * 128, 256,
                                           hipMemcpyHostToDevice, cx->stream));
-        OMEGA_HIP(F_DATTN, hipMemcpyAsync(c->pool + ko + c->g.plane_stride, v_bf16 + (size_t)i * 128,
-                                          256, hipMemcpyHostToDevice, cx->stream));
+        // V is stored transposed: one column of the page's [dim][16 tokens] block
+        OMEGA_HIP(F_DATTN, hipMemcpy2DAsync(c->pool + vo, 32, v_bf16 + (size_t)i * 128, 2, 2, 128,
+                                            hipMemcpyHostToDevice, cx->stream));
     }
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
     return OMEGA_GPU_OK;
@@ -447,10 +718,11 @@ int omega_gpu_decode_attn_cache_read(OmegaGpuDecodeAttnCache *c, uint32_t layer,
     Ctx *cx = ctx(F_DATTN);
     if (!cx) return OMEGA_GPU_CHIP_FAIL;
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
-    const uint64_t ko = (uint64_t)(pos / 16) * c->g.block_stride + (uint64_t)layer * c->g.layer_stride +
-                        (uint64_t)(pos % 16) * c->g.token_stride + (uint64_t)kv_head * c->g.head_stride;
+    const uint64_t page = (uint64_t)(pos / 16) * c->g.block_stride + (uint64_t)layer * c->g.layer_stride;
+    const uint64_t ko = page + (uint64_t)(pos % 16) * c->g.token_stride + (uint64_t)kv_head * c->g.head_stride;
+    const uint64_t vo = page + c->g.plane_stride + (uint64_t)kv_head * kVtHead + (pos % 16) * 2;
     OMEGA_HIP(F_DATTN, hipMemcpy(k_bf16, c->pool + ko, 256, hipMemcpyDeviceToHost));
-    OMEGA_HIP(F_DATTN, hipMemcpy(v_bf16, c->pool + ko + c->g.plane_stride, 256, hipMemcpyDeviceToHost));
+    OMEGA_HIP(F_DATTN, hipMemcpy2D(v_bf16, 2, c->pool + vo, 32, 2, 128, hipMemcpyDeviceToHost));
     return OMEGA_GPU_OK;
 }
 
@@ -583,12 +855,8 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
         g.layer_stride = 0;
         lay = 0;
     }
-    const uint32_t splits = attn_splits(max_ctx, seqs, kvh, cx->cus);
-    if ((size_t)seqs * kvh > cx->n_counters) {
-        set_error(F_ATTN, "paged attention: %u sequences x %u heads exceed the counter pool", seqs, kvh);
-        return OMEGA_GPU_ATTN_TOO_LARGE;
-    }
-    const size_t part_bytes = (size_t)seqs * qh * splits * 132 * 4;
+    const uint32_t splits = paged_splits(max_ctx);
+    const size_t part_bytes = (size_t)seqs * qh * splits * kPartStride * 4;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     // device scratch: q | out | table | lens | partials | staged pages
     const size_t o_q = 0, o_out = al(qf * 4), o_tab = o_out + al(qf * 4);
@@ -635,11 +903,18 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
     a.kvh = kvh;
     a.splits = splits;
     a.part = pd;
-    a.counters = counters(cx);
-    a.out = od;
     a.mutant = knobs().dattn_mutant;
+    CombineArgs cb;
+    cb.part = pd;
+    cb.splits = splits;
+    cb.context_lens = lens_dev;
+    cb.seqs = seqs;
+    cb.qh = qh;
+    cb.out = od;
+    cb.mutant = a.mutant;
     OMEGA_HIP(F_ATTN, hipEventRecord(cx->ev0, cx->stream));
     OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
+    OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
     OMEGA_HIP(F_ATTN, hipEventRecord(cx->ev1, cx->stream));
     OMEGA_HIP(F_ATTN, hipMemcpyAsync(pin, od, qf * 4, hipMemcpyDeviceToHost, cx->stream));
     OMEGA_HIP(F_ATTN, hipStreamSynchronize(cx->stream));
@@ -739,9 +1014,9 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     if (rc) return rc;
     Ctx *cx = ctx(F_ATTN);
     if (!cx) return OMEGA_GPU_ATTN_CHIP_FAIL;
-    const uint32_t splits = attn_splits(max_context, num_seqs, num_kv_heads, cx->cus);
-    if ((size_t)num_seqs * num_kv_heads > cx->n_counters) return OMEGA_GPU_ATTN_TOO_LARGE;
-    if (!ensure_scratch(F_ATTN, cx, (size_t)num_seqs * num_q_heads * splits * 132 * 4))
+    // every context must fit max_context: the split count is planned from it
+    const uint32_t splits = paged_splits(max_context);
+    if (!ensure_scratch(F_ATTN, cx, (size_t)num_seqs * num_q_heads * splits * kPartStride * 4))
         return OMEGA_GPU_ATTN_CHIP_FAIL;
     AttnArgs a;
     a.q = q_dev;
@@ -756,10 +1031,17 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     a.kvh = num_kv_heads;
     a.splits = splits;
     a.part = static_cast<float *>(cx->scratch);
-    a.counters = counters(cx);
-    a.out = out_dev;
     a.mutant = knobs().dattn_mutant;
+    CombineArgs cb;
+    cb.part = a.part;
+    cb.splits = splits;
+    cb.context_lens = context_lens_dev;
+    cb.seqs = num_seqs;
+    cb.qh = num_q_heads;
+    cb.out = out_dev;
+    cb.mutant = a.mutant;
     OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
+    OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
     return OMEGA_GPU_ATTN_OK;
 }
 

@@ -1,153 +1,191 @@
 // bf16 streaming GEMV (the lm_head) for gfx950 with an optional fused RMSNorm prologue and a
-// fused two-level argmax, plus the omega_gpu_bf16_* entry points.
+// fused argmax, plus the omega_gpu_bf16_* entry points.
 //
 // Contract: crates/aien-omega-bf16/src/lib.rs:15-24 — y[r] = sum_c W[r][c] * x[c] over an
 // [n][k] bf16 matrix, f32, deterministic summation order. The greedy token is the lowest index
 // of the max (crates/aien-omega-dgraph/src/lib.rs:347-349, tensor.rs:299-318).
 //
-// Kernel shape: one wavefront per 64-row tile (lane l owns row 64*tile + l) streaming 1 KiB per
-// 8-column step, 16 steps in flight per batch; the activation row is wave-uniform (scalar loads).
-// Each tile writes its (max, index); the last tile to finish reduces the tile maxima in order.
+// Kernel shape (rows.hpp): row-major rows, two per wavefront (8 KiB, eight 1 KiB chunks), the
+// activation phases in registers; workgroups of four wavefronts loop over the rows with a grid
+// sized to the chip, so the norm prologue runs once per wavefront. The argmax packs
+// (value, ~index) into one 64-bit key whose integer maximum is the greedy token; each
+// workgroup issues one fire-and-forget atomicMax into one of kArgmaxSlots slots and the host
+// takes the maximum of the slots (no ordering between workgroups is involved).
 #include <cmath>
 #include <vector>
 
-#include "device.hpp"
 #include "kernels.hpp"
+#include "rows.hpp"
 #include "runtime.hpp"
 
 namespace omega {
 
-__device__ __forceinline__ void dot8_bf16(u32x4 v, const float *xx, float &p0, float &p1) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t w = v[q];
-        p0 = fmaf(__uint_as_float(w << 16), xx[2 * q], p0);
-        p1 = fmaf(__uint_as_float(w & 0xffff0000u), xx[2 * q + 1], p1);
+// order-preserving key: larger value wins, then the lower index; NaN never beats a number
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t ord = 0;
+    if (v == v) {
+        const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0
+        ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     }
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
 }
 
-// better(a, b): a strictly greater, or equal with the lower index
-__device__ __forceinline__ bool better(float va, uint32_t ia, float vb, uint32_t ib) {
-    return va > vb || (va == vb && ia < ib);
+uint32_t argmax_from_slots(const unsigned long long *slots) {
+    unsigned long long best = 0;
+    for (uint32_t i = 0; i < kArgmaxSlots; ++i)
+        if (slots[i] > best) best = slots[i];
+    return 0xffffffffu - (uint32_t)(best & 0xffffffffu);
 }
 
-__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+constexpr int kLmK = 2048;
+constexpr int kLmRows = 2;
+constexpr uint32_t kLmBlocks = 2048;
+
+template <bool NORM, bool ARGMAX>
+__global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
+    using S = Bf16Slab<kLmK, kLmRows>;
+    constexpr int P = S::P;
+    static_assert(!NORM || P * 8 * 64 == kLmK, "the phases must partition the row");
+    __shared__ unsigned long long best_w[4];
+    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
+    float xr[P][8];
+    float nw[P][8];
+    S::load_x(a.x, lane, xr);
+    if (NORM) S::load_x(a.norm_w, lane, nw);
+    if (NORM) {
+        const float scale = rms_scale(phases_sumsq(xr), kLmK, a.eps);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const uint32_t oi = __shfl_xor(i, o, 64);
-        if (better(ov, oi, v, i)) {
-            v = ov;
-            i = oi;
+        for (int ph = 0; ph < P; ++ph)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xr[ph][i] = xr[ph][i] * scale * nw[ph][i];
+        if (a.hidden_out && blockIdx.x == 0 && wid == 0) {
+#pragma unroll
+            for (int ph = 0; ph < P; ++ph) {
+                float4 *o = reinterpret_cast<float4 *>(a.hidden_out + S::col(ph, lane));
+                o[0] = make_float4(xr[ph][0], xr[ph][1], xr[ph][2], xr[ph][3]);
+                o[1] = make_float4(xr[ph][4], xr[ph][5], xr[ph][6], xr[ph][7]);
+            }
+        }
+    }
+    const uint32_t items = (a.n + kLmRows - 1) / kLmRows;
+    const uint32_t stride = gridDim.x * 4;
+    unsigned long long best = 0;
+    for (uint32_t item = blockIdx.x * 4 + wid; item < items; item += stride) {
+        const uint32_t r0 = item * kLmRows;
+        const bool two = r0 + 1 < a.n;
+        S slab;
+        const gu32x4 *p = as_global(a.w + (size_t)r0 * kLmK) + lane;
+#pragma unroll
+        for (int c = 0; c < S::CH; ++c)
+            slab.v[c] = (two || c < S::CH / 2) ? __builtin_nontemporal_load(p + c * 64) : u32x4{0u, 0u, 0u, 0u};
+        float acc[kLmRows] = {0.f, 0.f};
+        slab.dot(xr, acc, lane);
+        float v = reduce_rows(acc, lane);
+        if (a.mutant == 1) {
+            v = -v;
+            acc[0] = -acc[0];
+            acc[1] = -acc[1];
+        }
+        if (lane < (two ? 2u : 1u)) a.y[r0 + lane] = v;
+        if (ARGMAX) {
+            const unsigned long long k0 = argmax_key(acc[0], r0);
+            if (k0 > best) best = k0;
+            if (two) {
+                const unsigned long long k1 = argmax_key(acc[1], r0 + 1);
+                if (k1 > best) best = k1;
+            }
+        }
+    }
+    if (ARGMAX) {
+        if (lane == 0) best_w[wid] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long b = best_w[0];
+            for (int w = 1; w < 4; ++w) b = best_w[w] > b ? best_w[w] : b;
+            if (b) atomicMax(&a.argmax[blockIdx.x % kArgmaxSlots], b);
         }
     }
 }
 
-// RMSNorm prologue kernel (final norm): hidden = x * scale * w with the f64 sum of squares
-__global__ __launch_bounds__(256) void k_rmsnorm_row(const float *x, const float *w, float eps,
-                                                     uint32_t k, float *out) {
-    __shared__ double red[4];
-    double ss = 0.0;
-    for (uint32_t c = threadIdx.x; c < k; c += 256) ss += (double)x[c] * (double)x[c];
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+// any k (a multiple of 256 up to 16384): the row staged in LDS, one or two rows per wavefront
+__global__ __launch_bounds__(256) void k_bf16_any(const Bf16RowsArgs a, uint32_t rpw) {
+    extern __shared__ float xs[];
+    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
+    const uint32_t k = a.k;
+    for (uint32_t c = threadIdx.x; c < k; c += 256) xs[c] = a.x[c];
     __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    const float scale = (float)(1.0 / sqrt(ss / (double)k + (double)eps));
-    for (uint32_t c = threadIdx.x; c < k; c += 256) out[c] = x[c] * scale * w[c];
-}
-
-constexpr int BF16_BATCH = 16;
-
-__global__ __launch_bounds__(64) void k_bf16_gemv(const Bf16GemvArgs a) {
-    const uint32_t lane = threadIdx.x;
-    const uint32_t t = blockIdx.x;
-    const uint32_t ksteps = a.k >> 3;
-    const gu32x4 *p = as_global(a.w + (size_t)t * ksteps * 512) + lane;
-    float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
-    for (uint32_t j = 0; j < ksteps; j += BF16_BATCH) {
-        u32x4 wv[BF16_BATCH];
+    const uint32_t kb = 2 * k;
+    const uint32_t ch = rpw * kb / 1024;
+    const uint32_t items = (a.n + rpw - 1) / rpw;
+    for (uint32_t item = blockIdx.x * 4 + wid; item < items; item += gridDim.x * 4) {
+        const uint32_t r0 = item * rpw;
+        const uint32_t rows = min(rpw, a.n - r0);
+        const gu32x4 *base = as_global(a.w + (size_t)r0 * k) + lane;
+        float acc[2] = {0.f, 0.f};
+        for (uint32_t c0 = 0; c0 < ch; c0 += 8) {
+            u32x4 v[8];
 #pragma unroll
-        for (int i = 0; i < BF16_BATCH; ++i) wv[i] = __builtin_nontemporal_load(p + (size_t)(j + i) * 64);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t c = c0 + i;
+                const uint32_t rl = (c * 1024 + 16 * lane) / kb;
+                v[i] = (c < ch && rl < rows) ? __builtin_nontemporal_load(base + (size_t)c * 64)
+                                             : u32x4{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
-        for (int i = 0; i < BF16_BATCH; i += 2) {
-            dot8_bf16(wv[i], a.x + (j + i) * 8, p0, p1);
-            dot8_bf16(wv[i + 1], a.x + (j + i + 1) * 8, p2, p3);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t c = c0 + i;
+                if (c >= ch) break;
+                const uint32_t o = c * 1024 + 16 * lane;
+                const uint32_t rl = o / kb, col = (o % kb) / 2;
+                const float p = bf16_dot8(v[i], xs + col);
+                acc[0] += rl == 0 ? p : 0.f;
+                acc[1] += rl == 1 ? p : 0.f;
+            }
         }
-    }
-    float v = (p0 + p1) + (p2 + p3);
-    if (a.mutant == 1) v = -v;
-    const uint32_t r = t * 64 + lane;
-    if (r < a.n) a.y[r] = v;
-    if (!a.token) return;
-    float best = r < a.n ? v : -INFINITY;
-    uint32_t bi = r < a.n ? r : 0xffffffffu;
-    wave_argmax(best, bi);
-    if (lane == 0) {
-        a.arg_val[t] = best;
-        a.arg_idx[t] = bi;
-    }
-    __threadfence();
-    uint32_t last = 0;
-    if (lane == 0) last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
-    last = __shfl(last, 0, 64);
-    if (!last) return;
-    __threadfence();
-    const uint32_t tiles = gridDim.x;
-    float bv = -INFINITY;
-    uint32_t bidx = 0xffffffffu;
-    for (uint32_t q = lane; q < tiles; q += 64) {
-        const float qv = __builtin_nontemporal_load(&a.arg_val[q]);
-        const uint32_t qi = __builtin_nontemporal_load(&a.arg_idx[q]);
-        if (better(qv, qi, bv, bidx)) {
-            bv = qv;
-            bidx = qi;
-        }
-    }
-    wave_argmax(bv, bidx);
-    if (lane == 0) {
-        *a.token = bidx;
-        atomicExch(a.counter, 0u);
+        float v = reduce_rows(acc, lane);
+        if (a.mutant == 1) v = -v;
+        if (lane < rows) a.y[r0 + lane] = v;
     }
 }
 
-hipError_t launch_bf16_gemv(const Bf16GemvArgs &a, hipStream_t st) {
-    Bf16GemvArgs b = a;
-    if (a.norm_w) {
-        hipLaunchKernelGGL(k_rmsnorm_row, dim3(1), dim3(256), 0, st, a.x, a.norm_w, a.eps, a.k,
-                           a.hidden_out);
-        b.x = a.hidden_out;
+hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st) {
+    if (a.k == (uint32_t)kLmK) {
+        const uint32_t items = (a.n + kLmRows - 1) / kLmRows;
+        uint32_t blocks = (items + 3) / 4;
+        if (blocks > kLmBlocks) blocks = kLmBlocks;
+        if (a.norm_w && a.argmax)
+            hipLaunchKernelGGL((k_bf16_lm<true, true>), dim3(blocks), dim3(256), 0, st, a);
+        else if (a.norm_w)
+            hipLaunchKernelGGL((k_bf16_lm<true, false>), dim3(blocks), dim3(256), 0, st, a);
+        else if (a.argmax)
+            hipLaunchKernelGGL((k_bf16_lm<false, true>), dim3(blocks), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((k_bf16_lm<false, false>), dim3(blocks), dim3(256), 0, st, a);
+        return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_bf16_gemv, dim3(a.n_pad / 64), dim3(64), 0, st, b);
+    if (a.norm_w || a.argmax) return hipErrorInvalidValue;
+    const uint32_t rpw = (2 * a.k) % 1024 == 0 ? 1 : 2;
+    const uint32_t items = (a.n + rpw - 1) / rpw;
+    uint32_t blocks = (items + 3) / 4;
+    if (blocks > kLmBlocks) blocks = kLmBlocks;
+    hipLaunchKernelGGL(k_bf16_any, dim3(blocks), dim3(256), a.k * 4, st, a, rpw);
     return hipGetLastError();
 }
 
-__global__ void k_bf16_relayout(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst,
-                                uint32_t n, uint32_t n_pad, uint32_t k, uint32_t *bad) {
-    const uint32_t ksteps = k >> 3;
-    const size_t chunks = (size_t)n_pad * ksteps;
+__global__ void k_bf16_scan(const uint16_t *__restrict__ w, size_t chunks, uint32_t *bad) {
+    uint32_t b = 0;
     for (size_t c = blockIdx.x * (size_t)blockDim.x + threadIdx.x; c < chunks;
          c += (size_t)gridDim.x * blockDim.x) {
-        const uint32_t r = (uint32_t)(c / ksteps), j = (uint32_t)(c % ksteps);
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (r < n) {
-            v = *reinterpret_cast<const u32x4 *>(src + (size_t)r * k + j * 8);
-            uint32_t bad_here = 0;
+        const u32x4 v = __builtin_nontemporal_load(as_global(w) + c);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                // exponent all ones: inf or NaN
-                bad_here |= ((v[q] & 0x7f80u) == 0x7f80u) | ((v[q] & 0x7f800000u) == 0x7f800000u);
-            }
-            if (bad_here) atomicOr(bad, 1u);
-        }
-        *reinterpret_cast<u32x4 *>(dst + ((size_t)(r >> 6) * ksteps + j) * 512 + (r & 63) * 8) = v;
+        for (int q = 0; q < 4; ++q)  // exponent all ones: inf or NaN
+            b |= ((v[q] & 0x7f80u) == 0x7f80u) | ((v[q] & 0x7f800000u) == 0x7f800000u);
     }
+    if (b) atomicOr(bad, 1u);
 }
 
-hipError_t launch_bf16_relayout(const uint16_t *src, uint16_t *dst, uint32_t n, uint32_t n_pad,
-                                uint32_t k, uint32_t *bad_flag, hipStream_t st) {
-    hipLaunchKernelGGL(k_bf16_relayout, dim3(4096), dim3(256), 0, st, src, dst, n, n_pad, k,
-                       bad_flag);
+hipError_t launch_bf16_scan(const uint16_t *w, size_t count, uint32_t *flag, hipStream_t st) {
+    hipLaunchKernelGGL(k_bf16_scan, dim3(2048), dim3(256), 0, st, w, count / 8, flag);
     return hipGetLastError();
 }
 
@@ -166,23 +204,22 @@ static int bf16_run(const OmegaGpuBf16Tensor *t, const float *x, float *y, Omega
     Ctx *c = ctx(F_BF16);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     const size_t xb = ((size_t)t->k * 4 + 255) & ~(size_t)255;
-    const size_t yb = ((size_t)t->n_pad * 4 + 255) & ~(size_t)255;
+    const size_t yb = ((size_t)t->n * 4 + 255) & ~(size_t)255;
     if (!ensure_scratch(F_BF16, c, xb + yb) || !ensure_pinned(F_BF16, c, xb + yb))
         return OMEGA_GPU_CHIP_FAIL;
     uint8_t *dev = static_cast<uint8_t *>(c->scratch);
     uint8_t *pin = static_cast<uint8_t *>(c->pin);
     memcpy(pin, x, (size_t)t->k * 4);
     OMEGA_HIP(F_BF16, hipMemcpyAsync(dev, pin, (size_t)t->k * 4, hipMemcpyHostToDevice, c->stream));
-    Bf16GemvArgs a;
+    Bf16RowsArgs a;
     a.w = t->w;
     a.x = reinterpret_cast<const float *>(dev);
     a.n = t->n;
-    a.n_pad = t->n_pad;
     a.k = t->k;
     a.y = reinterpret_cast<float *>(dev + xb);
     a.mutant = knobs().bf16_mutant;
     OMEGA_HIP(F_BF16, hipEventRecord(c->ev0, c->stream));
-    OMEGA_HIP(F_BF16, launch_bf16_gemv(a, c->stream));
+    OMEGA_HIP(F_BF16, launch_bf16_rows(a, c->stream));
     OMEGA_HIP(F_BF16, hipEventRecord(c->ev1, c->stream));
     OMEGA_HIP(F_BF16, hipMemcpyAsync(pin + xb, a.y, (size_t)t->n * 4, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_BF16, hipStreamSynchronize(c->stream));
@@ -191,10 +228,10 @@ static int bf16_run(const OmegaGpuBf16Tensor *t, const float *x, float *y, Omega
         memset(info, 0, sizeof(*info));
         info->n = t->n;
         info->k = t->k;
-        info->rows_per_warp = 64;
-        info->warps_per_cta = 1;
-        info->depth = BF16_BATCH;
-        info->grid_x = t->n_pad / 64;
+        info->rows_per_warp = t->k == (uint32_t)kLmK ? kLmRows : ((2 * t->k) % 1024 == 0 ? 1 : 2);
+        info->warps_per_cta = 4;
+        info->depth = 8;
+        info->grid_x = kLmBlocks;
         info->steps = t->k / 8;
         info->weight_bytes = (uint64_t)t->n * t->k * 2;
         info->elapsed_ns = event_ns(c);
@@ -228,20 +265,17 @@ int omega_gpu_bf16_tensor_upload(uint32_t n, uint32_t k, const uint16_t *w_bf16,
     OmegaGpuBf16Tensor *t = new OmegaGpuBf16Tensor();
     t->n = n;
     t->k = k;
-    t->n_pad = (n + 63) / 64 * 64;
-    const size_t bytes = (size_t)n * k * 2, pbytes = (size_t)t->n_pad * k * 2;
-    uint16_t *raw = nullptr;
+    t->n_pad = n;
+    const size_t count = (size_t)n * k;
     uint32_t *flag = nullptr;
     uint32_t bad = 0;
-    hipError_t e = hipMalloc(&t->w, pbytes);
-    if (e == hipSuccess) e = hipMalloc(&raw, bytes);
+    hipError_t e = hipMalloc(&t->w, count * 2);
     if (e == hipSuccess) e = hipMalloc(&flag, 4);
     if (e == hipSuccess) e = hipMemsetAsync(flag, 0, 4, c->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(raw, w_bf16, bytes, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) e = launch_bf16_relayout(raw, t->w, n, t->n_pad, k, flag, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(t->w, w_bf16, count * 2, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = launch_bf16_scan(t->w, count, flag, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (raw) (void)hipFree(raw);
     if (flag) (void)hipFree(flag);
     if (e != hipSuccess || bad) {
         if (e != hipSuccess) set_error(F_BF16, "bf16 upload: %s", hipGetErrorString(e));
@@ -267,9 +301,9 @@ int omega_gpu_bf16_tensor_synth(uint32_t n, uint32_t k, uint64_t seed, uint64_t 
     OmegaGpuBf16Tensor *t = new OmegaGpuBf16Tensor();
     t->n = n;
     t->k = k;
-    t->n_pad = (n + 63) / 64 * 64;
-    hipError_t e = hipMalloc(&t->w, (size_t)t->n_pad * k * 2);
-    if (e == hipSuccess) e = launch_bf16_synth(t->w, n, t->n_pad, k, seed, tensor_id, sigma, c->stream);
+    t->n_pad = n;
+    hipError_t e = hipMalloc(&t->w, (size_t)n * k * 2);
+    if (e == hipSuccess) e = launch_bf16_synth(t->w, n, k, seed, tensor_id, sigma, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         set_error(F_BF16, "bf16 synth: %s", hipGetErrorString(e));

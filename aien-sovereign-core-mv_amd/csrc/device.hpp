@@ -1,6 +1,13 @@
-// Device helpers shared by the kernels: wave reductions, bf16 rounding, and the per-head
-// preparation of the fused decode attention (per-head RMSNorm of q and k, RoPE from the table,
-// bf16 append of K and V into the page pool).
+// Device helpers shared by the kernels: global-address-space loads, deterministic wave
+// reductions (DPP inside 16-lane rows, readlane across rows), e4m3 / bf16 widening dot products,
+// bf16 rounding and the hi/lo split that feeds f32 values to the bf16 matrix cores, and the
+// aien-kv-cache row offsets.
+//
+// No kernel in this library communicates between workgroups inside a launch: on gfx950 a
+// device-scope release fence writes back the XCD's L2 and a returning atomic is a round trip to
+// memory, both microseconds. Cross-workgroup reductions happen in the consumer kernel, after
+// the launch boundary, or through fire-and-forget atomics whose result is order-independent
+// (integer max).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,14 +19,23 @@
 namespace omega {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+typedef const __attribute__((address_space(1))) u32x2 gu32x2;
 typedef const __attribute__((address_space(1))) uint32_t gu32;
 typedef const __attribute__((address_space(1))) float gf32;
+typedef const __attribute__((address_space(1))) f32x4 gf32x4;
 
 // Buffers reached through argument structs are global memory: give their loads the global
 // address space (global_load, not flat_load).
 __device__ __forceinline__ const gu32x4 *as_global(const void *p) {
     return (const gu32x4 *)(uintptr_t)p;
+}
+__device__ __forceinline__ const gu32x2 *as_global_u32x2(const void *p) {
+    return (const gu32x2 *)(uintptr_t)p;
 }
 __device__ __forceinline__ const gu32 *as_global_u32(const void *p) {
     return (const gu32 *)(uintptr_t)p;
@@ -27,19 +43,122 @@ __device__ __forceinline__ const gu32 *as_global_u32(const void *p) {
 __device__ __forceinline__ const gf32 *as_global_f32(const void *p) {
     return (const gf32 *)(uintptr_t)p;
 }
+__device__ __forceinline__ const gf32x4 *as_global_f32x4(const void *p) {
+    return (const gf32x4 *)(uintptr_t)p;
+}
 
-__device__ __forceinline__ double wave_sum_f64x(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
+
+// ------------------------------------------------------------------ reductions
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_XOR1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_MIRROR = 0x140;
+constexpr int DPP_ROR8 = 0x128;       // row_ror:8 (lane i of a row reads lane (i + 8) % 16)
+
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum of each 16-lane row, bitwise identical in every lane of the row (each step adds a value
+// to its mirror partner, and f32 addition is commutative).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<DPP_XOR1>(v);
+    v += dpp_f32<DPP_XOR2>(v);
+    v += dpp_f32<DPP_HALF_MIRROR>(v);
+    v += dpp_f32<DPP_MIRROR>(v);
     return v;
 }
-
-__device__ __forceinline__ uint16_t bf16_rne(float v) {
-    // crates/aien-kv-cache/src/lib.rs:116-121 (finite values)
-    uint32_t u = __float_as_uint(v);
-    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+// Sum over the wavefront in a fixed order, the same value in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    const float a = readlane_f32(v, 0), b = readlane_f32(v, 16);
+    const float c = readlane_f32(v, 32), d = readlane_f32(v, 48);
+    return (a + b) + (c + d);
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f32<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+    return v;
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)(u >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// f64 sum over the wavefront in a fixed order, the same value in every lane
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<DPP_XOR1>(v);
+    v += dpp_f64<DPP_XOR2>(v);
+    v += dpp_f64<DPP_HALF_MIRROR>(v);
+    v += dpp_f64<DPP_MIRROR>(v);
+    return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
 }
 
+// ------------------------------------------------------------------ widening dot products
+// 16 e4m3 bytes (one lane's 16 B) times 16 activations; the native OCP-fp8 convert.
+__device__ __forceinline__ void dot4_fp8(uint32_t w, const float *xx, float &p) {
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    p = fmaf(lo.x, xx[0], p);
+    p = fmaf(lo.y, xx[1], p);
+    p = fmaf(hi.x, xx[2], p);
+    p = fmaf(hi.y, xx[3], p);
+}
+__device__ __forceinline__ float fp8_dot16(const u32x4 w, const float *x) {
+    float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+    dot4_fp8(w.x, x + 0, p0);
+    dot4_fp8(w.y, x + 4, p1);
+    dot4_fp8(w.z, x + 8, p2);
+    dot4_fp8(w.w, x + 12, p3);
+    return (p0 + p1) + (p2 + p3);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// 8 bf16 (one lane's 16 B) times 8 activations
+__device__ __forceinline__ float bf16_dot8(const u32x4 w, const float *x) {
+    float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        p0 = fmaf(bf16_lo(w[q]), x[2 * q], p0);
+        p1 = fmaf(bf16_hi(w[q]), x[2 * q + 1], p1);
+    }
+    return p0 + p1;
+}
+
+// ------------------------------------------------------------------ bf16 rounding
+__device__ __forceinline__ uint16_t bf16_rne(float v) {
+    // crates/aien-kv-cache/src/lib.rs:116-121 (finite values)
+    const uint32_t u = __float_as_uint(v);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+// f32 -> (hi, lo) bf16 pair with hi + lo = v to about 2^-17 relative: what the bf16 matrix
+// cores take in place of an f32 operand (products with bf16 data stay exact in f32)
+__device__ __forceinline__ uint16_t bf16_split_hi(float v) { return bf16_rne(v); }
+__device__ __forceinline__ uint16_t bf16_split_lo(float v) {
+    return bf16_rne(v - bf16_to_f32(bf16_rne(v)));
+}
+
+// ------------------------------------------------------------------ KV rows
 __device__ __forceinline__ uint64_t kv_row_offset(const KvGeom &g, uint32_t block, uint32_t layer,
                                                   uint32_t plane, uint32_t token, uint32_t head) {
     return (uint64_t)block * g.block_stride + (uint64_t)layer * g.layer_stride +
@@ -47,44 +166,9 @@ __device__ __forceinline__ uint64_t kv_row_offset(const KvGeom &g, uint32_t bloc
            (uint64_t)head * g.head_stride;
 }
 
-// One wavefront prepares head `head` of the q|k|v row (heads 0..qh-1 are q, then kvh k heads,
-// then kvh v heads). Lane l holds dims l (v0) and l + 64 (v1), so the rotate-half pair of RoPE is
-// in-lane. Mirrors rmsnorm_per_head (qwen3_coder.rs:306-320, f64 sum of squares) then
-// apply_rope (tensor.rs:164-190) and the bf16 append (aien-kv-cache write_token_kv).
-__device__ __forceinline__ void prep_head(const HeadPrep &p, uint32_t head, uint32_t pos, float v0,
-                                          float v1) {
-    const uint32_t lane = threadIdx.x & 63;
-    const bool is_q = head < p.qh, is_k = !is_q && head < p.qh + p.kvh;
-    if (is_q || is_k) {
-        double ss = (double)v0 * (double)v0 + (double)v1 * (double)v1;
-        ss = wave_sum_f64x(ss);
-        const float scale = (float)(1.0 / sqrt(ss / 128.0 + (double)p.eps));
-        const float *w = is_q ? p.q_norm : p.k_norm;
-        float n0 = v0 * scale * w[lane];
-        float n1 = v1 * scale * w[lane + 64];
-        if (p.mutant != 1) {
-            const float c = p.rope_cos[(size_t)pos * 64 + lane];
-            const float s = p.rope_sin[(size_t)pos * 64 + lane];
-            const float r0 = __fsub_rn(__fmul_rn(n0, c), __fmul_rn(n1, s));
-            const float r1 = __fadd_rn(__fmul_rn(n0, s), __fmul_rn(n1, c));
-            n0 = r0;
-            n1 = r1;
-        }
-        if (is_q) {
-            p.q_out[head * 128 + lane] = n0;
-            p.q_out[head * 128 + lane + 64] = n1;
-            return;
-        }
-        v0 = n0;
-        v1 = n1;
-    }
-    if (p.mutant == 3) return;
-    const uint32_t kvhead = is_k ? head - p.qh : head - p.qh - p.kvh;
-    const uint32_t plane = is_k ? 0 : 1;
-    uint16_t *row = reinterpret_cast<uint16_t *>(
-        p.pool + kv_row_offset(p.g, pos / p.g.block_size, p.layer, plane, pos % p.g.block_size, kvhead));
-    row[lane] = bf16_rne(v0);
-    row[lane + 64] = bf16_rne(v1);
+// RMSNorm scale with the f64 sum of squares (tensor.rs:94-110)
+__device__ __forceinline__ float rms_scale(double sumsq, uint32_t k, float eps) {
+    return (float)(1.0 / sqrt(sumsq / (double)k + (double)eps));
 }
 
 }  // namespace omega

@@ -5,22 +5,28 @@
 // norm, the bf16 lm_head and the argmax; the greedy token is the lowest index of the max. The
 // residual row stays on the device for the whole token.
 //
-// MI355X shape: six kernels per layer, each fusing what the reference runs as separate launches —
-//   1. q|k|v GEMV with the input RMSNorm as its prologue and q/k RMSNorm + RoPE + bf16 K/V
-//      append as its epilogue,
-//   2. paged flash-decoding attention over the cache (identity page table),
-//   3. o GEMV whose epilogue adds into the residual row,
-//   4. router (RMSNorm, logits, top-8, weights, group tables),
-//   5. gate|up grouped GEMV whose epilogue is the SwiGLU,
-//   6. down grouped GEMV whose epilogue is the weighted combine plus the residual add,
-// plus the final RMSNorm and the lm_head GEMV with a fused two-level argmax: 6 * layers + 2
-// launches, captured once as a hipGraph and replayed per token. The position lives in device
-// memory, so the same graph serves every token; the host copies the embedding row in and the
-// token out.
+// MI355X shape: seven launches per layer, none of which waits on another workgroup of its own
+// launch (every cross-workgroup reduction sits at a launch boundary):
+//   1. q|k|v GEMV, the input RMSNorm in its prologue (layer 0 in token-id mode also gathers the
+//      embedding row and publishes it as the residual),
+//   2. matrix-core flash-decoding over the cache: q/k RMSNorm + RoPE in its prologue, this
+//      token's K/V append, one wavefront per (64-token tile range, kv head),
+//   3. the combine of the attention splits,
+//   4. o GEMV whose epilogue adds into the residual row,
+//   5. router logits (post-attention RMSNorm, exact f64 dot products),
+//   6. gate|up GEMV of the 8 routed experts: the top-8 ranking in its prologue, SwiGLU in its
+//      epilogue,
+//   7. down GEMV: one workgroup = the 8 experts' wavefronts for 8 rows, combined in slot order
+//      in LDS and added into the residual,
+// then the lm_head with the final RMSNorm in its prologue and the argmax folded in: 7L + 1
+// launches captured once as a hipGraph and replayed per token. The position and token id live
+// in device memory, so one graph serves every token.
 #include <cstdio>
 #include <vector>
 
 #include "kernels.hpp"
+#include "route.hpp"
+#include "rows.hpp"
 #include "runtime.hpp"
 
 namespace omega {
@@ -28,30 +34,139 @@ RouterArgs router_args(const OmegaGpuRouter *r, uint32_t layer, const float *x, 
                        int norm_topk, float out_scale);
 uint32_t router_layers(const OmegaGpuRouter *r);
 uint32_t router_rows(const OmegaGpuRouter *r);
-HeadPrep cache_prep(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, float *q_out);
-AttnArgs cache_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, const float *q);
+DattnArgs cache_dattn(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, const float *qkv,
+                      float *part);
 uint32_t cache_layers(const OmegaGpuDecodeAttnCache *c);
 uint32_t cache_max_pos(const OmegaGpuDecodeAttnCache *c);
+
+constexpr uint32_t kHidden = 2048, kInter = 768, kExperts = 128;
+
+// ---------------------------------------------------------------- gate|up + SwiGLU
+struct GateUpArgs {
+    const uint8_t *w = nullptr;  // [128][1536][2048] e4m3, gate rows then up rows
+    const float *s = nullptr;    // [128][12][16]
+    const float *logits = nullptr;
+    int norm_topk = 1;
+    int route_mutant = 0;
+    const float *xn = nullptr;   // post-attention normed row x'
+    float *act = nullptr;        // [8][768]
+    // workgroup 0 publishes the route: ids / weights for the down launch, the group tables
+    // from the layer's directories, and the per-layer log
+    uint32_t *ids = nullptr;
+    float *weights = nullptr;
+    const uint64_t *dir_gu = nullptr, *dir_dn = nullptr;
+    uint64_t *tab_gu = nullptr, *tab_dn = nullptr;
+    uint32_t *log_ids = nullptr;
+    float *log_w = nullptr;
+    int graph_mutant = 0;        // 1: gate and up swapped
+};
+
+constexpr uint32_t kGuPairs = 2;  // gate/up row pairs per wavefront
+
+__global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
+    using S = Fp8Slab<kHidden, kGuPairs>;
+    constexpr int P = S::P;
+    const uint32_t lane = lane_id();
+    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t slot = item / (kInter / kGuPairs), j0 = (item % (kInter / kGuPairs)) * kGuPairs;
+    float xr[P][16];
+    S::load_x(a.xn, lane, xr);
+    Route r;
+    route_topk(a.logits, kExperts, 0, a.norm_topk, a.route_mutant, r);
+    if (item == 0 && lane < (uint32_t)kTopK) {
+        uint32_t id = 0;
+        float wt = 0.f;
+#pragma unroll
+        for (int s = 0; s < kTopK; ++s)
+            if (lane == (uint32_t)s) {
+                id = r.id[s];
+                wt = r.w[s];
+            }
+        a.ids[lane] = id;
+        a.weights[lane] = wt;
+        if (a.log_ids) a.log_ids[lane] = id;
+        if (a.log_w) a.log_w[lane] = wt;
+        a.tab_gu[2 * lane] = a.dir_gu[2 * id];
+        a.tab_gu[2 * lane + 1] = a.dir_gu[2 * id + 1];
+        a.tab_dn[2 * lane] = a.dir_dn[2 * id];
+        a.tab_dn[2 * lane + 1] = a.dir_dn[2 * id + 1];
+    }
+    uint32_t e = r.id[0];
+#pragma unroll
+    for (int s = 1; s < kTopK; ++s)
+        if (slot == (uint32_t)s) e = r.id[s];
+    const uint8_t *we = a.w + (size_t)e * 2 * kInter * kHidden;
+    const float *se = a.s + (size_t)e * (2 * kInter / 128) * (kHidden / 128);
+    S gate, up;
+    gate.load(we + (size_t)j0 * kHidden, lane);
+    up.load(we + (size_t)(kInter + j0) * kHidden, lane);
+    float scg[P], scu[P];
+    S::load_scales(se + (size_t)(j0 >> 7) * (kHidden / 128), lane, 1.0f, 0, scg);
+    S::load_scales(se + (size_t)((kInter + j0) >> 7) * (kHidden / 128), lane, 1.0f, 0, scu);
+    float ag[kGuPairs], au[kGuPairs];
+#pragma unroll
+    for (uint32_t j = 0; j < kGuPairs; ++j) ag[j] = au[j] = 0.f;
+    gate.dot(xr, scg, ag, lane);
+    up.dot(xr, scu, au, lane);
+    float gv = reduce_rows(ag, lane);
+    float uv = reduce_rows(au, lane);
+    if (a.graph_mutant == 1) {
+        const float t = gv;
+        gv = uv;
+        uv = t;
+    }
+    if (lane < kGuPairs) a.act[slot * kInter + j0 + lane] = gv / (1.0f + expf(-gv)) * uv;
+}
+
+// ---------------------------------------------------------------- down + combine + residual
+struct DownArgs {
+    const uint8_t *w = nullptr;  // [128][2048][768] e4m3
+    const float *s = nullptr;    // [128][16][6]
+    const uint32_t *ids = nullptr;
+    const float *weights = nullptr;
+    const float *act = nullptr;  // [8][768]
+    float *x = nullptr;          // residual [2048]
+    int graph_mutant = 0;        // 2: slot 7 dropped from the combine
+};
+
+constexpr uint32_t kDnRows = 8;  // output rows per workgroup (one wavefront per slot)
+
+__global__ __launch_bounds__(512) void k_down(const DownArgs a) {
+    using S = Fp8Slab<kInter, kDnRows>;
+    constexpr int P = S::P;
+    __shared__ float red[kTopK][kDnRows];
+    const uint32_t lane = lane_id(), slot = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * kDnRows;
+    float xr[P][16];
+    S::load_x(a.act + slot * kInter, lane, xr);
+    const uint32_t e = *as_global_u32(a.ids + slot);
+    S slab;
+    slab.load(a.w + ((size_t)e * kHidden + row0) * kInter, lane);
+    float sc[P];
+    S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f, 0, sc);
+    float acc[kDnRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kDnRows; ++j) acc[j] = 0.f;
+    slab.dot(xr, sc, acc, lane);
+    const float v = reduce_rows(acc, lane);
+    if (lane < kDnRows) red[slot][lane] = v;
+    __syncthreads();
+    if (threadIdx.x < kDnRows) {
+        float moe = 0.f;
+#pragma unroll
+        for (int s = 0; s < kTopK; ++s) {
+            const float wgt = (a.graph_mutant == 2 && s == 7) ? 0.f : *as_global_f32(a.weights + s);
+            moe += wgt * red[s][threadIdx.x];
+        }
+        a.x[row0 + threadIdx.x] += moe;
+    }
+}
+
 }  // namespace omega
 
 using namespace omega;
 
 namespace {
-
-// x = bf16 row `*tok` of the embedding (tiled bf16 layout of the GEMV tensors), widened to f32
-// (Qwen3MoeOmegaWeights::embed_row, qwen3_moe_omega.rs:1108-1115: token modulo the vocabulary)
-__global__ __launch_bounds__(256) void k_embed_gather(const uint16_t *w, uint32_t n, uint32_t k,
-                                                      const uint32_t *tok, float *x) {
-    const uint32_t r = *tok % n;
-    const uint32_t ksteps = k >> 3;
-    for (uint32_t c = threadIdx.x; c < k; c += 256) {
-        const uint16_t b = w[((size_t)(r >> 6) * ksteps + (c >> 3)) * 512 + (r & 63) * 8 + (c & 7)];
-        x[c] = __uint_as_float((uint32_t)b << 16);
-    }
-}
-
-constexpr uint32_t kAttnSplits = 64;
-constexpr size_t kPartialFloats = 256 * 1024;
 
 struct GLayer {
     const OmegaGpuFp8Tensor *qkv = nullptr, *o = nullptr, *gu = nullptr, *dn = nullptr;
@@ -60,6 +175,14 @@ struct GLayer {
 
 const char *kKindNames[12] = {"norm", "qkv", "attn", "o_proj", "res_add", "router",
                               "gate_up", "swiglu", "down", "combine_norm", "lm_head", "argmax"};
+
+// device words the host writes before every token: pos, token id, then the argmax slots
+struct GraphIo {
+    uint32_t pos;
+    uint32_t tok;
+    uint32_t pad[14];
+    unsigned long long argmax[kArgmaxSlots];
+};
 
 }  // namespace
 
@@ -72,15 +195,13 @@ struct OmegaGpuDecodeGraph {
     float *final_norm = nullptr;
     bool final_set = false;
     // device state
-    float *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *hidden = nullptr;
-    float *logits = nullptr, *partial = nullptr, *attn_part = nullptr, *arg_val = nullptr;
-    uint32_t *arg_idx = nullptr, *token = nullptr, *pos = nullptr, *counters = nullptr;
+    float *x = nullptr, *qkv = nullptr, *attn = nullptr, *part = nullptr, *act = nullptr;
+    float *hidden = nullptr, *logits = nullptr;
+    GraphIo *io = nullptr;
     uint32_t *route_log = nullptr;  // [layers][8] routed ids of the last token
     float *route_log_w = nullptr;   // [layers][8] their weights
-    // pinned io
-    uint8_t *pin = nullptr;
+    GraphIo *pin = nullptr;         // pinned host twin of io
     const OmegaGpuBf16Tensor *embed = nullptr;  // optional: device embedding (token-id entry)
-    uint32_t *tok_in = nullptr;                 // device token id the gather reads
     // graphs: [0] x from the host, [1] x gathered from the embedding by token id
     hipGraph_t graph_v[2] = {nullptr, nullptr};
     hipGraphExec_t exec_v[2] = {nullptr, nullptr};
@@ -101,12 +222,6 @@ namespace {
 int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &kinds,
                   std::vector<hipEvent_t> *ev, bool sync_each, bool gather) {
     kinds.clear();
-    if (gather) {
-        hipLaunchKernelGGL(k_embed_gather, dim3(1), dim3(256), 0, st, g->embed->w, g->embed->n,
-                           g->embed->k, g->tok_in, g->x);
-        OMEGA_HIP(F_SESSION, hipGetLastError());
-        kinds.push_back(OMEGA_GPU_DGRAPH_K_NORM);
-    }
     const float eps = g->cfg.eps;
     size_t e_i = 0;
     auto mark = [&](uint8_t kind) -> hipError_t {
@@ -122,10 +237,11 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         OMEGA_HIP(F_SESSION, hipEventRecord((*ev)[0], st));
         e_i = 1;
     }
+    const uint32_t *pos_dev = &g->io->pos;
     for (uint32_t l = 0; l < g->cfg.layers; ++l) {
         const GLayer &L = g->layers[l];
-        // 1. q|k|v with the input norm prologue and the q/k norm + RoPE + KV append epilogue
-        Fp8GemvArgs a;
+        // 1. q|k|v with the input norm prologue
+        Fp8RowsArgs a;
         a.w = L.qkv->w;
         a.s = L.qkv->s;
         a.n = L.qkv->n;
@@ -134,25 +250,35 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         a.x = g->x;
         a.norm_w = L.input_norm;
         a.eps = eps;
-        a.partial = g->partial;
-        a.counters = g->counters;
-        a.prep = cache_prep(g->cache, l, eps, g->q);
-        a.pos_dev = g->pos;
-        int steps = fp8_gemv_plan(a, EPI_QKV);
-        OMEGA_HIP(F_SESSION, launch_fp8_gemv_epi(a, steps, EPI_QKV, st));
+        a.y = g->qkv;
+        int xsrc = XS_NORM;
+        if (gather && l == 0) {
+            xsrc = XS_EMBED_NORM;
+            a.embed = g->embed->w;
+            a.embed_tok = &g->io->tok;
+            a.embed_rows = g->embed->n;
+            a.x_out = g->x;
+        }
+        OMEGA_HIP(F_SESSION, launch_fp8_rows(a, EPI_STORE, xsrc, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_QKV));
-        // 2. attention
-        AttnArgs at = cache_attn(g->cache, l, g->q);
-        at.pos_dev = g->pos;
-        at.splits = kAttnSplits;
-        at.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
-        at.part = g->attn_part;
-        at.counters = g->counters + 64;
-        at.out = g->attn;
-        OMEGA_HIP(F_SESSION, launch_attention(at, st));
+        // 2. attention (q/k norm + RoPE, K/V append) and 3. the split combine
+        DattnArgs da = cache_dattn(g->cache, l, eps, g->qkv, g->part);
+        da.pos_dev = pos_dev;
+        OMEGA_HIP(F_SESSION, launch_dattn(da, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
-        // 3. o projection into the residual
-        Fp8GemvArgs o;
+        CombineArgs cb;
+        cb.part = g->part;
+        cb.splits = kDattnSplits;
+        cb.pos_dev = pos_dev;
+        cb.tiles_per_split = da.tiles_per_split;
+        cb.qh = 32;
+        cb.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
+        cb.out = g->attn;
+        cb.mutant = da.mutant;
+        OMEGA_HIP(F_SESSION, launch_attn_combine(cb, st));
+        OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
+        // 4. o projection into the residual
+        Fp8RowsArgs o;
         o.w = L.o->w;
         o.s = L.o->s;
         o.n = L.o->n;
@@ -160,67 +286,58 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         o.groups = 1;
         o.x = g->attn;
         o.y = g->x;
-        o.partial = g->partial;
-        o.counters = g->counters + 128;
-        steps = fp8_gemv_plan(o, EPI_RESID);
-        OMEGA_HIP(F_SESSION, launch_fp8_gemv_epi(o, steps, EPI_RESID, st));
+        OMEGA_HIP(F_SESSION, launch_fp8_rows(o, EPI_RESID, XS_F32, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_O_PROJ));
-        // 4. router: x' * 2^64 and the group tables stay on the device
-        RouterArgs ra = router_args(g->router, l, g->x, eps, g->cfg.norm_topk, 0x1p64f);
-        ra.route_log = g->route_log + (size_t)l * 8;
-        ra.route_log_w = g->route_log_w + (size_t)l * 8;
-        OMEGA_HIP(F_SESSION, launch_router(ra, st));
+        // 5. router logits and x'
+        RouterArgs ra = router_args(g->router, l, g->x, eps, g->cfg.norm_topk, 1.0f);
+        OMEGA_HIP(F_SESSION, launch_router_logits(ra, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ROUTER));
-        // 5. gate|up of the 8 routed experts, SwiGLU epilogue
-        Fp8GemvArgs gu;
-        gu.tab = ra.tab_gu;
-        gu.x = ra.xout;
-        gu.x_scale = 0x1p-64f;
-        gu.n = L.gu->n;
-        gu.k = L.gu->k;
-        gu.groups = 8;
-        gu.y = g->act;
-        gu.partial = g->partial;
-        gu.counters = g->counters + 256;
+        // 6. ranking + gate|up of the 8 routed experts + SwiGLU
+        GateUpArgs gu;
+        gu.w = L.gu->w;
+        gu.s = L.gu->s;
+        gu.logits = ra.logits;
+        gu.norm_topk = ra.norm_topk;
+        gu.route_mutant = ra.mutant;
+        gu.xn = ra.xout;
+        gu.act = g->act;
+        gu.ids = ra.ids;
+        gu.weights = ra.weights;
+        gu.dir_gu = ra.dir_gu;
+        gu.dir_dn = ra.dir_dn;
+        gu.tab_gu = ra.tab_gu;
+        gu.tab_dn = ra.tab_dn;
+        gu.log_ids = g->route_log + (size_t)l * 8;
+        gu.log_w = g->route_log_w + (size_t)l * 8;
         gu.graph_mutant = g->mutant;
-        steps = fp8_gemv_plan(gu, EPI_SWIGLU);
-        OMEGA_HIP(F_SESSION, launch_fp8_gemv_epi(gu, steps, EPI_SWIGLU, st));
+        hipLaunchKernelGGL(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
+        OMEGA_HIP(F_SESSION, hipGetLastError());
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_GATE_UP));
-        // 6. down of the 8 experts, weighted combine + residual epilogue
-        Fp8GemvArgs dn;
-        dn.tab = ra.tab_dn;
-        dn.x = g->act;
-        dn.x_stride = L.dn->k;
-        dn.n = L.dn->n;
-        dn.k = L.dn->k;
-        dn.groups = 8;
-        dn.y = g->x;
-        dn.partial = g->partial;
-        dn.counters = g->counters + 512;
-        dn.comb_w = ra.weights;
+        // 7. down of the 8 experts, weighted combine + residual
+        DownArgs dn;
+        dn.w = L.dn->w;
+        dn.s = L.dn->s;
+        dn.ids = ra.ids;
+        dn.weights = ra.weights;
+        dn.act = g->act;
+        dn.x = g->x;
         dn.graph_mutant = g->mutant;
-        steps = fp8_gemv_plan(dn, EPI_COMBINE);
-        OMEGA_HIP(F_SESSION, launch_fp8_gemv_epi(dn, steps, EPI_COMBINE, st));
+        hipLaunchKernelGGL(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
+        OMEGA_HIP(F_SESSION, hipGetLastError());
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_DOWN));
     }
     // final norm + lm_head + argmax
-    Bf16GemvArgs b;
+    Bf16RowsArgs b;
     b.w = g->lm->w;
+    b.n = g->lm->n;
+    b.k = g->lm->k;
     b.x = g->x;
     b.norm_w = g->final_norm;
     b.eps = eps;
-    b.n = g->lm->n;
-    b.n_pad = g->lm->n_pad;
-    b.k = g->lm->k;
-    b.y = g->logits;
     b.hidden_out = g->hidden;
-    b.arg_val = g->arg_val;
-    b.arg_idx = g->arg_idx;
-    b.token = g->token;
-    b.counter = g->counters + 1024;
-    OMEGA_HIP(F_SESSION, launch_bf16_gemv(b, st));
-    // launch_bf16_gemv enqueues the norm and the GEMV: two launches
-    kinds.push_back(OMEGA_GPU_DGRAPH_K_NORM);
+    b.y = g->logits;
+    b.argmax = g->io->argmax;
+    OMEGA_HIP(F_SESSION, launch_bf16_rows(b, st));
     OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_LM_HEAD));
     return OMEGA_GPU_OK;
 }
@@ -303,7 +420,7 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
                   cfg->layers);
         return OMEGA_GPU_BAD_ARGS;
     }
-    if (router_rows(r) != 128) {
+    if (router_rows(r) != kExperts) {
         set_error(F_SESSION, "decode graph: the router must be the 128-expert shape");
         return OMEGA_GPU_BAD_ARGS;
     }
@@ -319,37 +436,31 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     g->cache = ca;
     g->lm = lm;
     g->layers.resize(cfg->layers);
-    const uint32_t tiles = lm->n_pad / 64;
     hipError_t e = hipSuccess;
     auto M = [&](void **p, size_t bytes) {
         if (e == hipSuccess) e = hipMalloc(p, bytes);
         if (e == hipSuccess) e = hipMemset(*p, 0, bytes);
     };
-    M((void **)&g->x, 2048 * 4);
-    M((void **)&g->q, 4096 * 4);
+    M((void **)&g->x, kHidden * 4);
+    M((void **)&g->qkv, 5120 * 4);
     M((void **)&g->attn, 4096 * 4);
-    M((void **)&g->act, 8 * 768 * 4);
-    M((void **)&g->hidden, 2048 * 4);
-    M((void **)&g->logits, (size_t)lm->n_pad * 4);
-    M((void **)&g->partial, kPartialFloats * 4);
-    M((void **)&g->attn_part, (size_t)32 * kAttnSplits * 132 * 4);
-    M((void **)&g->arg_val, (size_t)tiles * 4);
-    M((void **)&g->arg_idx, (size_t)tiles * 4);
-    M((void **)&g->token, 4);
-    M((void **)&g->pos, 8);
-    M((void **)&g->counters, 2048 * 4);
-    M((void **)&g->final_norm, 2048 * 4);
+    M((void **)&g->part, (size_t)32 * kDattnSplits * kPartStride * 4);
+    M((void **)&g->act, kTopK * kInter * 4);
+    M((void **)&g->hidden, kHidden * 4);
+    M((void **)&g->logits, (size_t)lm->n * 4);
+    M((void **)&g->io, sizeof(GraphIo));
+    M((void **)&g->final_norm, kHidden * 4);
     M((void **)&g->route_log, (size_t)cfg->layers * 8 * 4);
     M((void **)&g->route_log_w, (size_t)cfg->layers * 8 * 4);
-    for (auto &L : g->layers) M((void **)&L.input_norm, 2048 * 4);
-    g->tok_in = g->pos + 1;
-    if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, 2048 * 4 + 256, hipHostMallocDefault);
+    for (auto &L : g->layers) M((void **)&L.input_norm, kHidden * 4);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         set_error(F_SESSION, "decode graph create: %s", hipGetErrorString(e));
         omega_gpu_decode_graph_free(g);
         return OMEGA_GPU_CHIP_FAIL;
     }
+    memset(g->pin, 0, sizeof(GraphIo));
     *out = g;
     return OMEGA_GPU_OK;
 }
@@ -364,9 +475,8 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
         if (g->graph_v[v]) (void)hipGraphDestroy(g->graph_v[v]);
     }
     for (hipEvent_t e : g->events) (void)hipEventDestroy(e);
-    void *ps[] = {g->x, g->q, g->attn, g->act, g->hidden, g->logits, g->partial, g->attn_part,
-                  g->arg_val, g->arg_idx, g->token, g->pos, g->counters, g->final_norm,
-                  g->route_log, g->route_log_w};
+    void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
+                  g->final_norm, g->route_log, g->route_log_w};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     for (auto &L : g->layers)
@@ -405,7 +515,7 @@ int omega_gpu_decode_graph_set_layer(OmegaGpuDecodeGraph *g, uint32_t layer, con
     L.o = to;
     L.gu = tg;
     L.dn = td;
-    OMEGA_HIP(F_SESSION, hipMemcpy(L.input_norm, input_norm, 2048 * 4, hipMemcpyHostToDevice));
+    OMEGA_HIP(F_SESSION, hipMemcpy(L.input_norm, input_norm, kHidden * 4, hipMemcpyHostToDevice));
     g->mark_dirty();
     return OMEGA_GPU_OK;
 }
@@ -417,7 +527,7 @@ int omega_gpu_decode_graph_set_final_norm(OmegaGpuDecodeGraph *g, const float *f
         set_error(F_SESSION, "decode graph set_final_norm: NULL pointer");
         return OMEGA_GPU_BAD_ARGS;
     }
-    OMEGA_HIP(F_SESSION, hipMemcpy(g->final_norm, final_norm, 2048 * 4, hipMemcpyHostToDevice));
+    OMEGA_HIP(F_SESSION, hipMemcpy(g->final_norm, final_norm, kHidden * 4, hipMemcpyHostToDevice));
     g->final_set = true;
     return OMEGA_GPU_OK;
 }
@@ -453,22 +563,22 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
         if (rc) return rc;
         record_ns = now_ns() - r0;
     }
-    uint8_t *pin = g->pin;
-    memcpy(pin + 2048 * 4, &pos, 4);
-    memcpy(pin + 2048 * 4 + 4, &token_in, 4);
+    // pos, token id and cleared argmax slots in one copy; the embedding row in another
+    GraphIo *pin = g->pin;
+    memset(pin, 0, sizeof(GraphIo));
+    pin->pos = pos;
+    pin->tok = token_in;
+    float *xin = reinterpret_cast<float *>(pin + 1);
+    OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->io, pin, sizeof(GraphIo), hipMemcpyHostToDevice, c->stream));
     if (x_embed) {
-        memcpy(pin, x_embed, 2048 * 4);
-        OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->x, pin, 2048 * 4, hipMemcpyHostToDevice, c->stream));
-        OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->pos, pin + 2048 * 4, 4, hipMemcpyHostToDevice, c->stream));
-    } else {
-        // pos and the token id sit next to each other: one 8-byte copy
-        OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->pos, pin + 2048 * 4, 8, hipMemcpyHostToDevice, c->stream));
+        memcpy(xin, x_embed, kHidden * 4);
+        OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->x, xin, kHidden * 4, hipMemcpyHostToDevice, c->stream));
     }
     OMEGA_HIP(F_SESSION, hipEventRecord(c->ev0, c->stream));
     if (eager) {
         std::vector<hipEvent_t> *ev = nullptr;
         if (g->stamps) {
-            int rc = ensure_events(g, 6 * (size_t)g->cfg.layers + 2);
+            int rc = ensure_events(g, 7 * (size_t)g->cfg.layers + 2);
             if (rc) return rc;
             ev = &g->events;
         }
@@ -479,9 +589,10 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     }
     const uint32_t launches = (uint32_t)g->kinds.size();
     OMEGA_HIP(F_SESSION, hipEventRecord(c->ev1, c->stream));
-    OMEGA_HIP(F_SESSION, hipMemcpyAsync(pin + 2048 * 4 + 64, g->token, 4, hipMemcpyDeviceToHost, c->stream));
+    OMEGA_HIP(F_SESSION, hipMemcpyAsync(pin->argmax, g->io->argmax, sizeof(pin->argmax),
+                                        hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
-    memcpy(token, pin + 2048 * 4 + 64, 4);
+    *token = argmax_from_slots(pin->argmax);
     g->stamps_valid = g->stamps;
     if (st) {
         memset(st, 0, sizeof(*st));
@@ -548,8 +659,8 @@ int omega_gpu_decode_graph_read(OmegaGpuDecodeGraph *g, float *x, float *hidden,
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
-    if (x) OMEGA_HIP(F_SESSION, hipMemcpy(x, g->x, 2048 * 4, hipMemcpyDeviceToHost));
-    if (hidden) OMEGA_HIP(F_SESSION, hipMemcpy(hidden, g->hidden, 2048 * 4, hipMemcpyDeviceToHost));
+    if (x) OMEGA_HIP(F_SESSION, hipMemcpy(x, g->x, kHidden * 4, hipMemcpyDeviceToHost));
+    if (hidden) OMEGA_HIP(F_SESSION, hipMemcpy(hidden, g->hidden, kHidden * 4, hipMemcpyDeviceToHost));
     if (logits) OMEGA_HIP(F_SESSION, hipMemcpy(logits, g->logits, (size_t)g->cfg.vocab * 4, hipMemcpyDeviceToHost));
     return OMEGA_GPU_OK;
 }
@@ -587,16 +698,14 @@ int omega_gpu_decode_graph_stamps(const OmegaGpuDecodeGraph *g, uint64_t *stamps
         set_error(F_SESSION, "decode graph stamps: off, or no token since they were switched on");
         return OMEGA_GPU_BAD_ARGS;
     }
-    // one event per recorded point: the first before any launch, then one per mark; the norm
-    // of the lm_head tail shares the lm_head's mark
-    const uint32_t marks = (uint32_t)g->events.size();
-    const uint32_t n = marks - 1;
-    if (cap < marks) {
-        set_error(F_SESSION, "decode graph stamps: capacity %u < %u", cap, marks);
+    // one event before the first launch, then one after each launch
+    const uint32_t n = (uint32_t)g->kinds.size();
+    if (cap < n + 1) {
+        set_error(F_SESSION, "decode graph stamps: capacity %u < %u", cap, n + 1);
         return OMEGA_GPU_TOO_LARGE;
     }
     stamps[0] = 0;
-    for (uint32_t i = 1; i < marks; ++i) {
+    for (uint32_t i = 1; i <= n; ++i) {
         float ms = 0.f;
         hipError_t e = hipEventElapsedTime(&ms, g->events[0], g->events[i]);
         if (e != hipSuccess) {
@@ -605,12 +714,7 @@ int omega_gpu_decode_graph_stamps(const OmegaGpuDecodeGraph *g, uint64_t *stamps
         }
         stamps[i] = (uint64_t)((double)ms * 1e6);
     }
-    // kinds per mark (the norm launch folds into the lm_head interval)
-    uint32_t j = 0;
-    for (size_t i = 0; i < g->kinds.size() && j < n; ++i) {
-        if (g->kinds[i] == OMEGA_GPU_DGRAPH_K_NORM) continue;
-        kinds[j++] = g->kinds[i];
-    }
+    for (uint32_t i = 0; i < n; ++i) kinds[i] = g->kinds[i];
     return (int)n;
 }
 

@@ -4,9 +4,9 @@
 // activation row x[token_rows[i]]; expert_ids non-decreasing; y is m*n in row-table order and
 // bit-identical to calling the GEMV once per row. m <= 1024 rows, <= 256 segments.
 //
-// This cut runs the rows through the GEMV kernel in launches of up to 64 rows (one wavefront per
-// (row, 64-row tile, k-split), the same summation order as the single GEMV, hence bit-identical
-// results).
+// This cut runs the rows through the GEMV kernel in launches of up to 64 rows (the row table
+// becomes the group table; every output row is computed by the same wavefront program as the
+// single GEMV, hence bit-identical results).
 #include <vector>
 
 #include "kernels.hpp"
@@ -57,18 +57,16 @@ int omega_gpu_fp8gemm_f32(const OmegaGpuFp8Tensor *t, uint32_t m, const uint32_t
     Ctx *c = ctx(F_GEMM);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     const size_t k = t->k, n = t->n;
-    Fp8GemvArgs a;
+    Fp8RowsArgs a;
     a.w = t->w;
     a.s = t->s;
     a.n = t->n;
     a.k = t->k;
     a.mutant = knobs().gemm_mutant;
     a.groups = 64;
-    const int steps = fp8_gemv_plan(a, EPI_STORE);
     const size_t xb = ((size_t)m * k * 4 + 255) & ~(size_t)255;
     const size_t yb = ((size_t)m * n * 4 + 255) & ~(size_t)255;
-    const size_t pb = a.splits > 1 ? (size_t)a.splits * 64 * n * 4 : 0;
-    if (!ensure_scratch(F_GEMM, c, xb + yb + pb) || !ensure_pinned(F_GEMM, c, xb + yb))
+    if (!ensure_scratch(F_GEMM, c, xb + yb) || !ensure_pinned(F_GEMM, c, xb + yb))
         return OMEGA_GPU_CHIP_FAIL;
     uint8_t *dev = static_cast<uint8_t *>(c->scratch);
     uint8_t *pin = static_cast<uint8_t *>(c->pin);
@@ -83,9 +81,7 @@ int omega_gpu_fp8gemm_f32(const OmegaGpuFp8Tensor *t, uint32_t m, const uint32_t
         a.x = reinterpret_cast<const float *>(dev) + (size_t)r0 * k;
         a.x_stride = (uint32_t)k;
         a.y = reinterpret_cast<float *>(dev + xb) + (size_t)r0 * n;
-        a.partial = reinterpret_cast<float *>(dev + xb + yb);
-        a.counters = counters(c);
-        OMEGA_HIP(F_GEMM, launch_fp8_gemv(a, steps, c->stream));
+        OMEGA_HIP(F_GEMM, launch_fp8_rows(a, EPI_STORE, XS_F32, c->stream));
         streamed += (uint64_t)g * n * k;
     }
     OMEGA_HIP(F_GEMM, hipEventRecord(c->ev1, c->stream));
@@ -99,9 +95,10 @@ int omega_gpu_fp8gemm_f32(const OmegaGpuFp8Tensor *t, uint32_t m, const uint32_t
         info->n = t->n;
         info->k = t->k;
         info->mt = 1;
-        info->warps_per_cta = 1;
+        info->warps_per_cta = 4;
         info->lane_bytes = 16;
-        info->grid_x = (m < 64 ? m : 64) * a.splits * (t->n / 64);
+        a.groups = m < 64 ? m : 64;
+        info->grid_x = fp8_rows_blocks(a);
         info->grid_y = (m + 63) / 64;
         info->passes_max = 1;
         info->weight_bytes = (uint64_t)segments * n * k;

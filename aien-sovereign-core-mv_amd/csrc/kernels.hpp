@@ -9,93 +9,73 @@
 
 namespace omega {
 
-// The KV of the fused cache and of the paged pool share one page layout (aien-kv-cache):
-// element (block, layer, plane, token, head, dim) at block*BS + layer*LS + plane*PS + token*TS +
-// head*HS + dim*2, bf16. The fused cache is a pool with the identity block table.
+// The KV of the paged pool (aien-kv-cache): element (block, layer, plane, token, head, dim) at
+// block*BS + layer*LS + plane*PS + token*TS + head*HS + dim*2, bf16. The fused decode cache uses
+// the same pages with the identity block table, but its V plane is stored transposed per page:
+// element (token, head, dim) of V at plane + head*4096 + dim*32 + (token % 16)*2.
 struct KvGeom {
     uint64_t block_stride, layer_stride, plane_stride, token_stride, head_stride;
     uint32_t block_size;
 };
 
-// Everything one head of the fused q|k|v row needs to be prepared (device.hpp prep_head).
-struct HeadPrep {
-    float *q_out = nullptr;          // [qh][128] post-norm, post-rope q
-    uint8_t *pool = nullptr;         // page pool (identity block table)
-    KvGeom g{};
-    uint32_t layer = 0;
-    const float *q_norm = nullptr, *k_norm = nullptr;      // [128]
-    const float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_pos][64]
-    float eps = 1e-6f;
-    uint32_t qh = 32, kvh = 4;
-    int mutant = 0;                  // 1: no RoPE; 3: K/V not written
-};
-
-// ---------------------------------------------------------------- FP8 GEMV (row-per-lane)
+// ---------------------------------------------------------------- FP8 GEMV (row-major)
 enum Fp8Epi : int {
-    EPI_STORE = 0,    // y[g][r] = v
-    EPI_RESID = 1,    // y[r] += v          (o_proj into the residual row)
-    EPI_SWIGLU = 2,   // y[g][j] = silu(v[j]) * v[n/2 + j]   (gate|up pairs -> activation)
-    EPI_COMBINE = 3,  // y[r] += sum_g w[g] * v[g][r], slots in order (down -> MoE out + residual)
-    EPI_QKV = 4,      // per 128-row head: q/k RMSNorm + RoPE -> q_out, K/V bf16 -> page pool
+    EPI_STORE = 0,  // y[g][r] = v
+    EPI_RESID = 1,  // y[r] += v          (o_proj into the residual row)
+};
+enum XSrc : int {
+    XS_F32 = 0,         // x (f32, group g at x + g * x_stride)
+    XS_NORM = 1,        // RMSNorm(x) * norm_w   (k = 2048)
+    XS_EMBED_NORM = 2,  // x = bf16 embedding row *embed_tok % embed_rows, then RMSNorm
 };
 
-struct Fp8GemvArgs {
-    const uint8_t *w = nullptr;   // tensor base (expert 0), tiled layout
-    const float *s = nullptr;     // f32 scales base (expert 0)
+struct Fp8RowsArgs {
+    const uint8_t *w = nullptr;     // tensor base (expert 0), row-major [experts][n][k]
+    const float *s = nullptr;       // f32 scales [experts][n/128][k/128]
     const uint64_t *tab = nullptr;  // device group table {w_va, s_va} x groups, or null
-    const float *x = nullptr;     // activation; group g reads x + g * x_stride
+    const float *x = nullptr;
     uint32_t x_stride = 0;
-    float x_scale = 1.0f;         // folded into the block scales (exact power of two)
-    const float *norm_w = nullptr;  // input RMSNorm weight (prologue), or null
+    float x_scale = 1.0f;           // folded into the block scales (exact power of two)
+    const float *norm_w = nullptr;
     float eps = 1e-6f;
-    uint32_t n = 0, k = 0, groups = 1, splits = 1;
+    const uint16_t *embed = nullptr;     // XS_EMBED_NORM
+    const uint32_t *embed_tok = nullptr;
+    uint32_t embed_rows = 0;
+    float *x_out = nullptr;         // XS_EMBED_NORM: workgroup 0 stores the widened row here
+    uint32_t n = 0, k = 0, groups = 1;
     float *y = nullptr;
-    float *partial = nullptr;     // [splits][groups][n] when splits > 1 or EPI_COMBINE
-    uint32_t *counters = nullptr; // one per output tile, zero on entry, zero on exit
-    const float *comb_w = nullptr;  // EPI_COMBINE slot weights (device)
-    int mutant = 0;               // omega_gpu_fp8_test_set_mutant
-    int graph_mutant = 0;         // omega_gpu_decode_graph_test_set_mutant (swiglu / combine)
-    HeadPrep prep{};              // EPI_QKV
-    const uint32_t *pos_dev = nullptr;  // EPI_QKV position (device), else pos_host
-    uint32_t pos_host = 0;
-    uint32_t ids[64] = {0};       // expert id per group when tab == null
+    int mutant = 0;                 // omega_gpu_fp8_test_set_mutant
+    uint32_t ids[64] = {0};         // expert id per group when tab == null
 };
+hipError_t launch_fp8_rows(const Fp8RowsArgs &a, int epi, int xsrc, hipStream_t st);
+uint32_t fp8_rows_per_wave(uint32_t k);
+uint32_t fp8_rows_blocks(const Fp8RowsArgs &a);
 
-// steps = 16-byte column steps per work item (8 or 16); the grid is computed from the args.
-hipError_t launch_fp8_gemv(const Fp8GemvArgs &a, int steps, hipStream_t st);
-hipError_t launch_fp8_gemv_epi(const Fp8GemvArgs &a, int steps, int epi, hipStream_t st);
-// work items (= workgroups) a launch of these args uses
-uint32_t fp8_gemv_items(const Fp8GemvArgs &a, int steps);
-// choose the steps and splits for a shape (fills a.splits); returns steps
-int fp8_gemv_plan(Fp8GemvArgs &a, int epi);
-
-// upload helpers
-hipError_t launch_fp8_relayout(const uint8_t *src, uint8_t *dst, uint32_t experts, uint32_t n,
-                               uint32_t k, uint32_t *nan_flag, hipStream_t st);
 hipError_t launch_fp8_synth(uint8_t *w, float *s, uint32_t experts, uint32_t n, uint32_t k,
                             uint64_t seed, uint64_t tensor, float sigma, hipStream_t st);
+// sets *flag when any byte is an e4m3 NaN (0x7f / 0xff)
+hipError_t launch_fp8_nan_scan(const uint8_t *w, size_t bytes, uint32_t *flag, hipStream_t st);
 
-// ---------------------------------------------------------------- bf16 GEMV + argmax
-struct Bf16GemvArgs {
-    const uint16_t *w = nullptr;  // tiled layout, n_pad rows
+// ---------------------------------------------------------------- bf16 GEMV (+ argmax)
+struct Bf16RowsArgs {
+    const uint16_t *w = nullptr;  // row-major [n][k]
+    uint32_t n = 0, k = 0;
     const float *x = nullptr;
-    const float *norm_w = nullptr;  // optional RMSNorm of x first (final norm)
+    const float *norm_w = nullptr;  // RMSNorm(x) first (k = 2048)
     float eps = 1e-6f;
-    uint32_t n = 0, n_pad = 0, k = 0;
+    float *hidden_out = nullptr;    // with norm_w: workgroup 0 stores the normed row here
     float *y = nullptr;
-    float *hidden_out = nullptr;    // when norm_w: the normed row is also written here
-    // argmax (optional): per-tile partials and the result
-    float *arg_val = nullptr;
-    uint32_t *arg_idx = nullptr;
-    uint32_t *token = nullptr;
-    uint32_t *counter = nullptr;
+    unsigned long long *argmax = nullptr;  // [kArgmaxSlots] packed (value, ~index) maxima
     int mutant = 0;
 };
-hipError_t launch_bf16_gemv(const Bf16GemvArgs &a, hipStream_t st);
-hipError_t launch_bf16_relayout(const uint16_t *src, uint16_t *dst, uint32_t n, uint32_t n_pad,
-                                uint32_t k, uint32_t *bad_flag, hipStream_t st);
-hipError_t launch_bf16_synth(uint16_t *w, uint32_t n, uint32_t n_pad, uint32_t k, uint64_t seed,
-                             uint64_t tensor, float sigma, hipStream_t st);
+constexpr uint32_t kArgmaxSlots = 64;
+hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st);
+hipError_t launch_bf16_synth(uint16_t *w, uint32_t n, uint32_t k, uint64_t seed, uint64_t tensor,
+                             float sigma, hipStream_t st);
+// sets *flag when any element is NaN or infinite
+hipError_t launch_bf16_scan(const uint16_t *w, size_t count, uint32_t *flag, hipStream_t st);
+// host side of the argmax: the greedy token from the slots (lowest index of the maximum)
+uint32_t argmax_from_slots(const unsigned long long *slots);
 
 // ---------------------------------------------------------------- router
 struct RouterArgs {
@@ -108,48 +88,92 @@ struct RouterArgs {
     int norm_topk = 1;
     float out_scale = 1.0f;
     uint32_t experts = 128, shared = 0, hidden = 2048, top_k = 8;
-    float *logits = nullptr;          // [rows] scratch
+    float *logits = nullptr;          // [rows]
     float *xout = nullptr;            // [hidden] x' * out_scale
     uint32_t *ids = nullptr;          // [slots]
     float *weights = nullptr;         // [slots]
     uint64_t *tab_gu = nullptr;       // [slots][2]
     uint64_t *tab_dn = nullptr;
-    uint32_t *counter = nullptr;
-    uint32_t *route_log = nullptr;    // optional: ids also written here (decode graph log)
-    float *route_log_w = nullptr;     // optional: weights also written here
+    uint32_t *route_log = nullptr;    // optional copies of ids / weights (decode graph log)
+    float *route_log_w = nullptr;
     int mutant = 0;
 };
-hipError_t launch_router(const RouterArgs &a, hipStream_t st);
+// logits (and x'); then the ranking of the logits (ids, weights, group tables)
+hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st);
+hipError_t launch_router_topk(const RouterArgs &a, hipStream_t st);
 
 // ---------------------------------------------------------------- attention
+constexpr uint32_t kAttnTile = 64;       // tokens per tile (one wavefront)
+constexpr uint32_t kDattnSplits = 64;    // split workgroups per kv head of the fused kernel
+constexpr uint32_t kPartStride = 132;    // floats per (head, split) partial: m, l, -, -, o[128]
 
-// Paged flash-decoding: grid (splits, kv heads, seqs), one wavefront per item; the tokens of a
-// (seq, kv head) are cut into `splits` ranges of whole 64-token sub-chunks, each item keeps an
-// online softmax over its range, and the last item of the (seq, kv head) combines the ranges in
-// order. q is read wave-uniformly (scalar loads); K rows are read one per lane, V one dim pair
-// per lane.
-struct AttnArgs {
-    const float *q = nullptr;               // [seqs][qh][128] post-norm, post-rope
-    const uint8_t *pool = nullptr;          // page pool (device-readable)
+// How `tiles` tiles of 64 tokens spread over at most `splits` split items: `tps` tiles each
+// (forced_tps when non-zero and it fits), `active` items hold work; with no tiles one item still
+// runs (the fused kernel folds the current token into split 0).
+__host__ __device__ inline void attn_split_plan(uint32_t tiles, uint32_t splits, uint32_t forced_tps,
+                                                uint32_t &active, uint32_t &tps) {
+    if (tiles == 0) {
+        active = 1;
+        tps = 0;
+        return;
+    }
+    tps = forced_tps ? forced_tps : (tiles + splits - 1) / splits;
+    if ((tiles + tps - 1) / tps > splits) tps = (tiles + splits - 1) / splits;
+    active = (tiles + tps - 1) / tps;
+}
+
+// Fused decode attention over the cache: per (split, kv head) one wavefront prepares the 8 q
+// heads (RMSNorm, RoPE) from the raw q|k|v row, runs the matrix-core flash-decoding of its tiles
+// of the tokens before `pos`, and split 0 also appends this token's K/V and folds it in.
+struct DattnArgs {
+    const float *qkv = nullptr;      // raw q|k|v [5120]
+    uint8_t *pool = nullptr;
     KvGeom g{};
-    uint32_t layer = 0;
-    const int32_t *block_tables = nullptr;  // [seqs][max_blocks]; null: identity (block = p/16)
-    uint32_t max_blocks = 0;
-    const int32_t *context_lens = nullptr;  // [seqs]; null: ctx = (*pos_dev or pos_host) + 1
+    uint32_t layer = 0, max_pos = 0;
+    const float *q_norm = nullptr, *k_norm = nullptr;      // [128] of the layer
+    const float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_pos][64]
+    float eps = 1e-6f;
     const uint32_t *pos_dev = nullptr;
     uint32_t pos_host = 0;
+    uint32_t tiles_per_split = 0;    // 0: spread over every split
+    float *part = nullptr;           // [32][kDattnSplits][kPartStride]
+    int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written
+};
+hipError_t launch_dattn(const DattnArgs &a, hipStream_t st);
+
+// Paged flash-decoding over an external pool: grid (splits, kv heads, seqs), one wavefront
+// per item, partials as above.
+struct AttnArgs {
+    const float *q = nullptr;               // [seqs][qh][128] post-norm, post-rope
+    const uint8_t *pool = nullptr;
+    KvGeom g{};
+    uint32_t layer = 0;
+    const int32_t *block_tables = nullptr;  // [seqs][max_blocks]
+    uint32_t max_blocks = 0;
+    const int32_t *context_lens = nullptr;  // [seqs]
     uint32_t seqs = 1, qh = 32, kvh = 4;
-    uint32_t splits = 1;                    // items per (seq, kv head)
-    float out_scale = 1.0f;
-    float *part = nullptr;                  // [seqs][qh][splits][132]: m, l, -, -, o[128]
-    uint32_t *counters = nullptr;           // [seqs][kvh], zero on entry and exit
-    float *out = nullptr;                   // [seqs][qh][128]
-    int mutant = 0;                         // 2: V one position late; 4: combine ignores the max
+    uint32_t splits = 1;
+    float *part = nullptr;                  // [seqs][qh][splits][kPartStride]
+    int mutant = 0;                         // 2: V one position late
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
-// standalone preparation of a raw q|k|v row: one wavefront per head (qh + 2 kvh of them)
-hipError_t launch_qkv_prep(const HeadPrep &p, const float *qkv, const uint32_t *pos_dev,
-                           uint32_t pos_host, hipStream_t st);
+
+// Combines the split partials of every (seq, q head): out = sum w_s o_s / sum w_s l_s with
+// w_s = exp(m_s - max m), times out_scale.
+struct CombineArgs {
+    const float *part = nullptr;
+    uint32_t splits = 1;                    // partial slots per head
+    const uint32_t *pos_dev = nullptr;      // fused: tiles before pos, plus the token itself
+    uint32_t pos_host = 0;
+    uint32_t tiles_per_split = 0;           // as the fused kernel's
+    const int32_t *context_lens = nullptr;  // paged: tiles of the context
+    uint32_t seqs = 1, qh = 32;
+    float out_scale = 1.0f;
+    float *out = nullptr;                   // [seqs][qh][128]
+    int mutant = 0;                         // 4: ignore the maxima
+};
+hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st);
+
 // RoPE table of one position range (host twin of the oracle's rope_cos_sin)
 void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out);
 

@@ -1,160 +1,97 @@
-// One-launch MoE router for gfx950 (RMSNorm, router logits, softmax, top-k, renormalised
-// weights, the normed row and both grouped-GEMV group tables) and the omega_gpu_router_* entry
-// points.
+// MoE router for gfx950 (RMSNorm, router logits, softmax, top-k, renormalised weights, the
+// normed row and both grouped-GEMV group tables) and the omega_gpu_router_* entry points.
 //
 // Contract: crates/aien-omega-router/src/lib.rs:16-28. Host oracle: FakeRouter::route
 // (crates/aien-inference-abi/src/qwen3_moe_omega.rs:1943-1998) and MoeBatchPlan::from_logits
-// (moe_plan.rs:86-171): rank by total order descending, ties to the lower id, weight =
-// exp(l - max) / sum over the selected of exp(l - max).
+// (moe_plan.rs:86-171).
 //
-// Kernel shape: ROUTER_WGS workgroups of four wavefronts. Every workgroup normalises the row
-// itself (f64 sum of squares, the RMSNorm of tensor.rs:94-110) into LDS, scores its share of the
-// gate rows — each logit accumulates the exact f32 products in f64 and rounds once, so the value
-// does not depend on the summation order and equals the CPU oracle's — and writes its slice of
-// x' * out_scale. The last workgroup to finish runs the top-k on one wavefront with shuffles.
+// Two launches: k_router_logits gives one gate row to each wavefront (bf16, 4 KiB, the normed
+// row's phases in registers — each lane normalises with the f64 sum of squares over the whole
+// row, rows.hpp). Each logit accumulates the exact f32 products in f64 and rounds once, so its
+// value does not depend on the summation order and equals the CPU oracle's. Workgroup 0 also
+// writes x' * out_scale. k_router_topk ranks the logits on one wavefront (route.hpp) and fills
+// the ids, weights and group tables. The decode graph runs the ranking inside its gate|up
+// kernel instead.
 #include <cmath>
 #include <vector>
 
 #include "kernels.hpp"
+#include "route.hpp"
+#include "rows.hpp"
 #include "runtime.hpp"
 
 namespace omega {
 
-constexpr int ROUTER_WGS = 32;
+constexpr uint32_t kRouterHidden = 2048;
 
-__device__ __forceinline__ int32_t total_key(float f) {
-    int32_t b = __float_as_int(f);
-    return b < 0 ? (b ^ 0x7fffffff) : b;
-}
-
-__global__ __launch_bounds__(256) void k_router(const RouterArgs a) {
-    __shared__ float post[2048];
-    __shared__ double red[4];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t H = a.hidden;
-    // RMSNorm of the residual row
-    double ss = 0.0;
-    for (uint32_t c = tid; c < H; c += 256) ss += (double)a.x[c] * (double)a.x[c];
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    const float scale = (float)(1.0 / sqrt(ss / (double)H + (double)a.eps));
-    for (uint32_t c = tid; c < H; c += 256) {
-        const float wn = a.mutant == 1 ? 1.0f : a.norm_w[c];
-        post[c] = a.x[c] * scale * wn;
-    }
-    __syncthreads();
-    // this workgroup's slice of x' * out_scale
-    const uint32_t per = H / gridDim.x;
-    for (uint32_t c = blockIdx.x * per + tid; c < (blockIdx.x + 1) * per; c += 256)
-        a.xout[c] = post[c] * a.out_scale;
-    // logits of rows blockIdx.x + gridDim.x * (4 * i + wave)
+__global__ __launch_bounds__(256) void k_router_logits(const RouterArgs a) {
+    using S = Bf16Slab<kRouterHidden, 1>;
+    constexpr int P = S::P;
+    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * 4 + wid;
     const uint32_t rows = a.experts + a.shared;
-    for (uint32_t row = blockIdx.x + gridDim.x * wave; row < rows; row += gridDim.x * 4) {
-        const uint16_t *g = a.gate + (size_t)row * H;
-        double acc = 0.0;
-        for (uint32_t c = lane * 8; c < H; c += 512) {
-            const uint4 v = *reinterpret_cast<const uint4 *>(g + c);
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    float xr[P][8], nw[P][8];
+    S::load_x(a.x, lane, xr);
+    S::load_x(a.norm_w, lane, nw);
+    S slab;
+    if (row < rows) slab.load(a.gate + (size_t)row * kRouterHidden, lane);
+    const float scale = rms_scale(phases_sumsq(xr), kRouterHidden, a.eps);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc += (double)__uint_as_float(w4[q] << 16) * (double)post[c + 2 * q];
-                acc += (double)__uint_as_float(w4[q] & 0xffff0000u) * (double)post[c + 2 * q + 1];
-            }
+    for (int ph = 0; ph < P; ++ph)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xr[ph][i] = xr[ph][i] * scale * (a.mutant == 1 ? 1.0f : nw[ph][i]);
+    if (blockIdx.x == 0 && wid == 0) {
+#pragma unroll
+        for (int ph = 0; ph < P; ++ph) {
+            float *o = a.xout + S::col(ph, lane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = xr[ph][i] * a.out_scale;
         }
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        if (lane == 0) a.logits[row] = (float)acc;
     }
-    // the last workgroup ranks
-    __threadfence();
-    __shared__ uint32_t last;
-    if (tid == 0) last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!last || wave != 0) return;
-    __threadfence();
-    const uint32_t E = a.experts;  // 128 or 256: E / 64 candidates per lane
-    float lv[4];
-    int32_t key[4];
-    bool taken[4];
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t id = lane + 64 * q;
-        taken[q] = id >= E;
-        lv[q] = taken[q] ? 0.f : __builtin_nontemporal_load(&a.logits[id]);
-        key[q] = total_key(lv[q]);
-    }
-    uint32_t sel_id[8];
-    float sel_v[8];
-    for (uint32_t s = 0; s < a.top_k; ++s) {
-        int32_t bk = INT32_MIN;
-        uint32_t bi = 0xffffffffu;
-        float bv = 0.f;
+    if (row >= rows) return;
+    double acc = 0.0;
+#pragma unroll
+    for (int c = 0; c < S::CH; ++c) {
+        const u32x4 w = slab.v[c];
+#pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const uint32_t id = lane + 64 * q;
-            if (!taken[q] && (bi == 0xffffffffu || key[q] > bk)) {
-                bk = key[q];
-                bi = id;
-                bv = lv[q];
-            }
+            acc += (double)bf16_lo(w[q]) * (double)xr[c][2 * q];
+            acc += (double)bf16_hi(w[q]) * (double)xr[c][2 * q + 1];
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            const int32_t ok = __shfl_xor(bk, o, 64);
-            const uint32_t oi = __shfl_xor(bi, o, 64);
-            const float ov = __shfl_xor(bv, o, 64);
-            const bool take = oi != 0xffffffffu &&
-                              (bi == 0xffffffffu || ok > bk || (ok == bk && oi < bi));
-            if (take) {
-                bk = ok;
-                bi = oi;
-                bv = ov;
-            }
-        }
-        sel_id[s] = bi;
-        sel_v[s] = bv;
-        const uint32_t mask_id = a.mutant == 2 ? (bi ^ 1u) : bi;
-        for (int q = 0; q < 4; ++q)
-            if (lane + 64 * q == mask_id) taken[q] = true;
     }
-    if (lane == 0) {
-        const float mx = sel_v[0];
-        float p[8];
-        float sum = 0.f;
-        for (uint32_t s = 0; s < a.top_k; ++s) {
-            p[s] = expf(sel_v[s] - mx);
-            sum += p[s];
-        }
-        if (!a.norm_topk) {
-            sum = 0.f;
-            for (uint32_t id = 0; id < E; ++id) sum += expf(__builtin_nontemporal_load(&a.logits[id]) - mx);
-        }
-        for (uint32_t s = 0; s < a.top_k; ++s) {
-            const uint32_t id = sel_id[s];
-            a.ids[s] = id;
-            a.weights[s] = a.mutant == 4 ? p[s] : p[s] / sum;
-            if (a.route_log) a.route_log[s] = id;
-            if (a.route_log_w) a.route_log_w[s] = a.weights[s];
-            const uint32_t did = a.mutant == 3 ? (id ^ 1u) : id;
-            a.tab_gu[2 * s] = a.dir_gu[2 * did];
-            a.tab_gu[2 * s + 1] = a.dir_gu[2 * did + 1];
-            a.tab_dn[2 * s] = a.dir_dn[2 * did];
-            a.tab_dn[2 * s + 1] = a.dir_dn[2 * did + 1];
-        }
-        if (a.shared) {
-            const uint32_t s = a.top_k;
-            const float ls = __builtin_nontemporal_load(&a.logits[E]);
-            a.ids[s] = E;
-            a.weights[s] = 1.0f / (1.0f + expf(-ls));
-            a.tab_gu[2 * s] = a.dir_gu[2 * E];
-            a.tab_gu[2 * s + 1] = a.dir_gu[2 * E + 1];
-            a.tab_dn[2 * s] = a.dir_dn[2 * E];
-            a.tab_dn[2 * s + 1] = a.dir_dn[2 * E + 1];
-        }
-        atomicExch(a.counter, 0u);
+    acc = wave_sum_f64(acc);
+    if (lane == 0) a.logits[row] = (float)acc;
+}
+
+__global__ __launch_bounds__(64) void k_router_topk(const RouterArgs a) {
+    Route r;
+    route_topk(a.logits, a.experts, a.shared, a.norm_topk, a.mutant, r);
+    const uint32_t lane = lane_id();
+    const uint32_t slots = kTopK + (a.shared ? 1 : 0);
+#pragma unroll
+    for (uint32_t s = 0; s < kTopK + 1; ++s) {
+        if (lane != s || s >= slots) continue;
+        const uint32_t id = r.id[s];
+        a.ids[s] = id;
+        a.weights[s] = r.w[s];
+        if (a.route_log) a.route_log[s] = id;
+        if (a.route_log_w) a.route_log_w[s] = r.w[s];
+        const uint32_t did = (a.mutant == 3 && s < (uint32_t)kTopK) ? (id ^ 1u) : id;
+        a.tab_gu[2 * s] = a.dir_gu[2 * did];
+        a.tab_gu[2 * s + 1] = a.dir_gu[2 * did + 1];
+        a.tab_dn[2 * s] = a.dir_dn[2 * did];
+        a.tab_dn[2 * s + 1] = a.dir_dn[2 * did + 1];
     }
 }
 
-hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_router, dim3(ROUTER_WGS), dim3(256), 0, st, a);
+hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st) {
+    const uint32_t rows = a.experts + a.shared;
+    hipLaunchKernelGGL(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_router_topk(const RouterArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_router_topk, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -168,7 +105,7 @@ struct OmegaGpuRouter {
     uint64_t *dir_dn = nullptr;
     // launch buffers (fixed addresses for the router's life)
     float *xin = nullptr, *xout = nullptr, *logits = nullptr, *weights = nullptr;
-    uint32_t *ids = nullptr, *counter = nullptr;
+    uint32_t *ids = nullptr;
     uint64_t *tab_gu = nullptr, *tab_dn = nullptr;
 };
 
@@ -195,7 +132,6 @@ RouterArgs router_args(const OmegaGpuRouter *r, uint32_t layer, const float *x, 
     a.weights = r->weights;
     a.tab_gu = r->tab_gu;
     a.tab_dn = r->tab_dn;
-    a.counter = r->counter;
     a.mutant = knobs().router_mutant;
     return a;
 }
@@ -236,7 +172,6 @@ int omega_gpu_router_alloc_shape(uint32_t layers, uint32_t experts, uint32_t sha
     if (e == hipSuccess) e = hipMalloc(&r->logits, 512 * 4);
     if (e == hipSuccess) e = hipMalloc(&r->weights, 16 * 4);
     if (e == hipSuccess) e = hipMalloc(&r->ids, 16 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->counter, 4);
     if (e == hipSuccess) e = hipMalloc(&r->tab_gu, 16 * 16);
     if (e == hipSuccess) e = hipMalloc(&r->tab_dn, 16 * 16);
     if (e == hipSuccess) e = hipMemset(r->gate, 0, (size_t)layers * r->rows * 2048 * 2);
@@ -246,7 +181,6 @@ int omega_gpu_router_alloc_shape(uint32_t layers, uint32_t experts, uint32_t sha
     if (e == hipSuccess) e = hipMemset(r->xout, 0, 2048 * 4);
     if (e == hipSuccess) e = hipMemset(r->tab_gu, 0, 256);
     if (e == hipSuccess) e = hipMemset(r->tab_dn, 0, 256);
-    if (e == hipSuccess) e = hipMemset(r->counter, 0, 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         set_error(F_ROUTER, "router alloc: %s", hipGetErrorString(e));
@@ -263,7 +197,7 @@ void omega_gpu_router_free(OmegaGpuRouter *r) {
     Ctx *c = ctx(F_ROUTER);
     if (c) (void)hipStreamSynchronize(c->stream);
     void *ps[] = {r->gate, r->norm, r->dir_gu, r->dir_dn, r->xin, r->xout, r->logits,
-                  r->weights, r->ids, r->counter, r->tab_gu, r->tab_dn};
+                  r->weights, r->ids, r->tab_gu, r->tab_dn};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     delete r;
@@ -328,7 +262,8 @@ int omega_gpu_router(OmegaGpuRouter *r, uint32_t layer, const float *x, float ep
     OMEGA_HIP(F_ROUTER, hipMemcpyAsync(r->xin, pin, 2048 * 4, hipMemcpyHostToDevice, c->stream));
     RouterArgs a = router_args(r, layer, r->xin, eps, norm_topk, out_scale);
     OMEGA_HIP(F_ROUTER, hipEventRecord(c->ev0, c->stream));
-    OMEGA_HIP(F_ROUTER, launch_router(a, c->stream));
+    OMEGA_HIP(F_ROUTER, launch_router_logits(a, c->stream));
+    OMEGA_HIP(F_ROUTER, launch_router_topk(a, c->stream));
     OMEGA_HIP(F_ROUTER, hipEventRecord(c->ev1, c->stream));
     OMEGA_HIP(F_ROUTER, hipMemcpyAsync(pin, r->ids, 16 * 4, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_ROUTER, hipMemcpyAsync(pin + 64, r->weights, 16 * 4, hipMemcpyDeviceToHost, c->stream));
@@ -338,7 +273,7 @@ int omega_gpu_router(OmegaGpuRouter *r, uint32_t layer, const float *x, float ep
     if (info) {
         memset(info, 0, sizeof(*info));
         info->layer = layer;
-        info->warps = ROUTER_WGS * 4;
+        info->warps = r->rows + 1;
         info->depth = 1;
         info->threads = 256;
         info->weight_bytes = (uint64_t)r->rows * 2048 * 2;

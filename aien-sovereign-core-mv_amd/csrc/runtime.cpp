@@ -74,13 +74,6 @@ Ctx *ctx(Family f) {
         set_error(f, "stream/event create: %s", hipGetErrorString(e));
         return nullptr;
     }
-    c.n_counters = 1u << 20;
-    if ((e = hipMalloc(&c.counters, c.n_counters * sizeof(uint32_t))) != hipSuccess ||
-        (e = hipMemset(c.counters, 0, c.n_counters * sizeof(uint32_t))) != hipSuccess ||
-        (e = hipDeviceSynchronize()) != hipSuccess) {
-        set_error(f, "counter pool: %s", hipGetErrorString(e));
-        return nullptr;
-    }
     g_ctx = c;
     g_ctx_ready = true;
     return &g_ctx;
@@ -118,8 +111,6 @@ bool ensure_scratch(Family f, Ctx *c, size_t bytes) {
     c->scratch_bytes = want;
     return true;
 }
-
-uint32_t *counters(Ctx *c) { return c->counters; }
 
 uint64_t event_ns(Ctx *c) {
     float ms = 0.f;

@@ -1,7 +1,6 @@
 // Internal runtime of libomega_gpu: one HIP stream per process, the error strings of every ABI
-// family, pinned staging buffers, a self-resetting counter pool for the kernels' last-arriver
-// reductions, and the device-side kernel declarations shared by the entry points and the decode
-// graph.
+// family, pinned staging buffers and a device scratch area for the standalone entry points, and
+// the object layouts shared by the entry points and the decode graph.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -39,9 +38,6 @@ struct Ctx {
     // device scratch (grows; never used by a captured graph)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
-    // zero-initialised counters, each kernel leaves the ones it used at zero
-    uint32_t *counters = nullptr;
-    size_t n_counters = 0;
 };
 
 // Initialises on first use (device = current device). Returns nullptr and sets the family's
@@ -50,8 +46,6 @@ Ctx *ctx(Family f);
 // Grow helpers; return false (error set) on allocation failure.
 bool ensure_pinned(Family f, Ctx *c, size_t bytes);
 bool ensure_scratch(Family f, Ctx *c, size_t bytes);
-// Counters for standalone calls: [0, n_counters) of the pool (1 << 20 entries).
-uint32_t *counters(Ctx *c);
 
 // HIP call check: on failure sets the family error and returns CHIP_FAIL from the caller.
 #define OMEGA_HIP(fam, call)                                                                    \
@@ -93,19 +87,15 @@ Knobs &knobs();
 }  // namespace omega
 
 // ---------------------------------------------------------------------------- object layouts
-// Device layout of an FP8 tensor: for every expert, rows in tiles of 64 and columns in steps of
-// 16 bytes, one 1 KiB chunk per (tile, step): byte (r, c) of expert e sits at
-//   e*n*k + ((r/64) * (k/16) + c/16) * 1024 + (r%64) * 16 + c%16
-// so a wavefront reads 1 KiB contiguously per step and lane l owns row 64*tile + l. Scales are
-// f32 [expert][n/128][k/128].
+// Device layout of an FP8 tensor: row-major e4m3 bytes [experts][n][k] (a wavefront streams
+// whole rows), scales f32 [experts][n/128][k/128].
 struct OmegaGpuFp8Tensor {
     uint32_t experts = 0, n = 0, k = 0;
     uint8_t *w = nullptr;
     float *s = nullptr;
 };
 
-// Device layout of a bf16 tensor: rows padded to a multiple of 64, tiles of 64 rows, steps of
-// 8 columns (16 bytes): element (r, c) at ((r/64) * (k/8) + c/8) * 512 + (r%64) * 8 + c%8.
+// Device layout of a bf16 tensor: row-major [n][k] (n_pad == n).
 struct OmegaGpuBf16Tensor {
     uint32_t n = 0, k = 0, n_pad = 0;
     uint16_t *w = nullptr;
