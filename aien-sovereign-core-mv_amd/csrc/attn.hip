@@ -301,7 +301,7 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_dattn, dim3(kDattnSplits, 4), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_dattn, dim3(kDattnSplits, 4), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
 }
 
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.qh, a.seqs), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_attn_combine, dim3(a.qh, a.seqs), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -154,13 +154,13 @@ hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st) {
         uint32_t blocks = (items + 3) / 4;
         if (blocks > kLmBlocks) blocks = kLmBlocks;
         if (a.norm_w && a.argmax)
-            hipLaunchKernelGGL((k_bf16_lm<true, true>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<true, true>), dim3(blocks), dim3(256), 0, st, a);
         else if (a.norm_w)
-            hipLaunchKernelGGL((k_bf16_lm<true, false>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<true, false>), dim3(blocks), dim3(256), 0, st, a);
         else if (a.argmax)
-            hipLaunchKernelGGL((k_bf16_lm<false, true>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<false, true>), dim3(blocks), dim3(256), 0, st, a);
         else
-            hipLaunchKernelGGL((k_bf16_lm<false, false>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<false, false>), dim3(blocks), dim3(256), 0, st, a);
         return hipGetLastError();
     }
     if (a.norm_w || a.argmax) return hipErrorInvalidValue;
@@ -168,7 +168,7 @@ hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st) {
     const uint32_t items = (a.n + rpw - 1) / rpw;
     uint32_t blocks = (items + 3) / 4;
     if (blocks > kLmBlocks) blocks = kLmBlocks;
-    hipLaunchKernelGGL(k_bf16_any, dim3(blocks), dim3(256), a.k * 4, st, a, rpw);
+    OMEGA_LAUNCH(k_bf16_any, dim3(blocks), dim3(256), a.k * 4, st, a, rpw);
     return hipGetLastError();
 }
 

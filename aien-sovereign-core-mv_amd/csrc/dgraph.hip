@@ -211,7 +211,8 @@ struct OmegaGpuDecodeGraph {
     bool stamps = false;
     int flush_each = 0;  // 1: synchronise after every launch; 2: direct launches, no graph
     std::vector<uint8_t> kinds;
-    std::vector<hipEvent_t> events;
+    std::vector<hipEvent_t> events;   // one before the first launch, one after each launch
+    std::vector<hipEvent_t> kevents;  // start / stop pair per launch, recorded by the dispatch
     bool stamps_valid = false;
 };
 
@@ -220,10 +221,19 @@ namespace {
 // Enqueues one token's kernels on `st`. With `ev` (stamps), records an event before the first
 // launch and after each one.
 int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &kinds,
-                  std::vector<hipEvent_t> *ev, bool sync_each, bool gather) {
+                  std::vector<hipEvent_t> *ev, std::vector<hipEvent_t> *kev, bool sync_each,
+                  bool gather) {
     kinds.clear();
     const float eps = g->cfg.eps;
-    size_t e_i = 0;
+    size_t e_i = 0, k_i = 0;
+    // the next launch records its own start / stop (stamp mode)
+    auto arm = [&]() {
+        if (kev && k_i + 1 < kev->size()) {
+            launch_stamp().start = (*kev)[k_i];
+            launch_stamp().stop = (*kev)[k_i + 1];
+            k_i += 2;
+        }
+    };
     auto mark = [&](uint8_t kind) -> hipError_t {
         kinds.push_back(kind);
         if (ev && e_i < ev->size()) {
@@ -259,11 +269,13 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
             a.embed_rows = g->embed->n;
             a.x_out = g->x;
         }
+        arm();
         OMEGA_HIP(F_SESSION, launch_fp8_rows(a, EPI_STORE, xsrc, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_QKV));
         // 2. attention (q/k norm + RoPE, K/V append) and 3. the split combine
         DattnArgs da = cache_dattn(g->cache, l, eps, g->qkv, g->part);
         da.pos_dev = pos_dev;
+        arm();
         OMEGA_HIP(F_SESSION, launch_dattn(da, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
         CombineArgs cb;
@@ -275,6 +287,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         cb.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
         cb.out = g->attn;
         cb.mutant = da.mutant;
+        arm();
         OMEGA_HIP(F_SESSION, launch_attn_combine(cb, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
         // 4. o projection into the residual
@@ -286,10 +299,12 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         o.groups = 1;
         o.x = g->attn;
         o.y = g->x;
+        arm();
         OMEGA_HIP(F_SESSION, launch_fp8_rows(o, EPI_RESID, XS_F32, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_O_PROJ));
         // 5. router logits and x'
         RouterArgs ra = router_args(g->router, l, g->x, eps, g->cfg.norm_topk, 1.0f);
+        arm();
         OMEGA_HIP(F_SESSION, launch_router_logits(ra, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ROUTER));
         // 6. ranking + gate|up of the 8 routed experts + SwiGLU
@@ -310,7 +325,8 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         gu.log_ids = g->route_log + (size_t)l * 8;
         gu.log_w = g->route_log_w + (size_t)l * 8;
         gu.graph_mutant = g->mutant;
-        hipLaunchKernelGGL(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
+        arm();
+        OMEGA_LAUNCH(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
         OMEGA_HIP(F_SESSION, hipGetLastError());
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_GATE_UP));
         // 7. down of the 8 experts, weighted combine + residual
@@ -322,7 +338,8 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         dn.act = g->act;
         dn.x = g->x;
         dn.graph_mutant = g->mutant;
-        hipLaunchKernelGGL(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
+        arm();
+        OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
         OMEGA_HIP(F_SESSION, hipGetLastError());
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_DOWN));
     }
@@ -337,16 +354,17 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
     b.hidden_out = g->hidden;
     b.y = g->logits;
     b.argmax = g->io->argmax;
+    arm();
     OMEGA_HIP(F_SESSION, launch_bf16_rows(b, st));
     OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_LM_HEAD));
     return OMEGA_GPU_OK;
 }
 
-int ensure_events(OmegaGpuDecodeGraph *g, size_t n) {
-    while (g->events.size() < n) {
+int ensure_events(std::vector<hipEvent_t> &v, size_t n) {
+    while (v.size() < n) {
         hipEvent_t e;
         OMEGA_HIP(F_SESSION, hipEventCreate(&e));
-        g->events.push_back(e);
+        v.push_back(e);
     }
     return OMEGA_GPU_OK;
 }
@@ -361,7 +379,7 @@ int rebuild(OmegaGpuDecodeGraph *g, Ctx *c, int v) {
         g->graph_v[v] = nullptr;
     }
     OMEGA_HIP(F_SESSION, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_token(g, c->stream, g->kinds, nullptr, false, v == 1);
+    int rc = enqueue_token(g, c->stream, g->kinds, nullptr, nullptr, false, v == 1);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &graph);
     if (rc) {
@@ -475,6 +493,7 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
         if (g->graph_v[v]) (void)hipGraphDestroy(g->graph_v[v]);
     }
     for (hipEvent_t e : g->events) (void)hipEventDestroy(e);
+    for (hipEvent_t e : g->kevents) (void)hipEventDestroy(e);
     void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
                   g->final_norm, g->route_log, g->route_log_w};
     for (void *p : ps)
@@ -576,13 +595,16 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     }
     OMEGA_HIP(F_SESSION, hipEventRecord(c->ev0, c->stream));
     if (eager) {
-        std::vector<hipEvent_t> *ev = nullptr;
+        std::vector<hipEvent_t> *ev = nullptr, *kev = nullptr;
         if (g->stamps) {
-            int rc = ensure_events(g, 7 * (size_t)g->cfg.layers + 2);
+            const size_t launches = 7 * (size_t)g->cfg.layers + 1;
+            int rc = ensure_events(g->events, launches + 1);
+            if (!rc) rc = ensure_events(g->kevents, 2 * launches);
             if (rc) return rc;
             ev = &g->events;
+            kev = &g->kevents;
         }
-        int rc = enqueue_token(g, c->stream, g->kinds, ev, g->flush_each == 1, v == 1);
+        int rc = enqueue_token(g, c->stream, g->kinds, ev, kev, g->flush_each == 1, v == 1);
         if (rc) return rc;
     } else {
         OMEGA_HIP(F_SESSION, hipGraphLaunch(g->exec_v[v], c->stream));
@@ -715,6 +737,31 @@ int omega_gpu_decode_graph_stamps(const OmegaGpuDecodeGraph *g, uint64_t *stamps
         stamps[i] = (uint64_t)((double)ms * 1e6);
     }
     for (uint32_t i = 0; i < n; ++i) kinds[i] = g->kinds[i];
+    return (int)n;
+}
+
+int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g || !ns) return OMEGA_GPU_BAD_ARGS;
+    if (!g->stamps || !g->stamps_valid) {
+        set_error(F_SESSION, "decode graph kernel_ns: off, or no token since stamps were switched on");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    const uint32_t n = (uint32_t)g->kinds.size();
+    if (cap < n || g->kevents.size() < 2 * (size_t)n) {
+        set_error(F_SESSION, "decode graph kernel_ns: capacity %u < %u", cap, n);
+        return OMEGA_GPU_TOO_LARGE;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        float ms = 0.f;
+        hipError_t e = hipEventElapsedTime(&ms, g->kevents[2 * i], g->kevents[2 * i + 1]);
+        if (e != hipSuccess) {
+            set_error(F_SESSION, "decode graph kernel_ns: %s", hipGetErrorString(e));
+            return OMEGA_GPU_CHIP_FAIL;
+        }
+        ns[i] = (uint64_t)((double)ms * 1e6);
+    }
     return (int)n;
 }
 

@@ -170,7 +170,7 @@ uint32_t fp8_rows_blocks(const Fp8RowsArgs &a) {
 
 template <int K, int RPW, int EPI, int XSRC>
 static hipError_t launch_k(const Fp8RowsArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL((k_fp8_rows<K, RPW, EPI, XSRC>), dim3(fp8_rows_blocks(a)), dim3(256), 0, st, a);
+    OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC>), dim3(fp8_rows_blocks(a)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -182,8 +182,8 @@ hipError_t launch_fp8_rows(const Fp8RowsArgs &a, int epi, int xsrc, hipStream_t 
         case 2048: return launch_k<2048, 4, EPI_STORE, XS_F32>(a, st);
         case 4096: return launch_k<4096, 2, EPI_STORE, XS_F32>(a, st);
         default:
-            hipLaunchKernelGGL(k_fp8_rows_any, dim3(fp8_rows_blocks(a)), dim3(256), 0, st, a,
-                               fp8_rows_per_wave(a.k));
+            OMEGA_LAUNCH(k_fp8_rows_any, dim3(fp8_rows_blocks(a)), dim3(256), 0, st, a,
+                         fp8_rows_per_wave(a.k));
             return hipGetLastError();
         }
     }

@@ -86,12 +86,12 @@ __global__ __launch_bounds__(64) void k_router_topk(const RouterArgs a) {
 
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st) {
     const uint32_t rows = a.experts + a.shared;
-    hipLaunchKernelGGL(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_router_topk(const RouterArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_router_topk, dim3(1), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_router_topk, dim3(1), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

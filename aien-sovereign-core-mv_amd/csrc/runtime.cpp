@@ -112,6 +112,11 @@ bool ensure_scratch(Family f, Ctx *c, size_t bytes) {
     return true;
 }
 
+LaunchStamp &launch_stamp() {
+    static thread_local LaunchStamp s;
+    return s;
+}
+
 uint64_t event_ns(Ctx *c) {
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, c->ev0, c->ev1) != hipSuccess) return 0;

@@ -3,6 +3,7 @@
 // the object layouts shared by the entry points and the decode graph.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -63,6 +64,25 @@ inline uint64_t now_ns() {
                std::chrono::steady_clock::now().time_since_epoch())
         .count();
 }
+
+// Per-launch GPU timestamps (the decode graph's stamp mode): when armed, the next launch made
+// through OMEGA_LAUNCH has its start and end recorded by the dispatch itself
+// (hipExtLaunchKernel), which is what a kernel-trace profiler reports as its duration.
+struct LaunchStamp {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchStamp &launch_stamp();  // per thread
+
+#define OMEGA_LAUNCH(kern, grid, block, shm, st, ...)                                            \
+    do {                                                                                         \
+        ::omega::LaunchStamp &ls_ = ::omega::launch_stamp();                                     \
+        if (ls_.start) {                                                                         \
+            hipExtLaunchKernelGGL(kern, grid, block, shm, st, ls_.start, ls_.stop, 0, __VA_ARGS__); \
+            ls_.start = ls_.stop = nullptr;                                                      \
+        } else {                                                                                 \
+            hipLaunchKernelGGL(kern, grid, block, shm, st, __VA_ARGS__);                         \
+        }                                                                                        \
+    } while (0)
 
 // elapsed of the last ev0 -> ev1 pair, ns
 uint64_t event_ns(Ctx *c);

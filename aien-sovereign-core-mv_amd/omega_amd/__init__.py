@@ -198,6 +198,7 @@ SIGNATURES = {
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
+    "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),
     "omega_gpu_decode_graph_token_id": (i32, [P, u32, u32, U32P, C.POINTER(GraphStats)]),
     "omega_gpu_stream": (P, []),
@@ -672,6 +673,15 @@ class DecodeGraph:
         if n < 0:
             self._rc(n, "stamps")
         return st[:n + 1], kinds[:n]
+
+    def kernel_ns(self):
+        """Per-launch durations (ns) of the last stamped token, as the dispatch recorded them."""
+        cap = DGRAPH_MAX_LAYERS * 16 + 16
+        ns = np.zeros(cap, np.uint64)
+        n = lib().omega_gpu_decode_graph_kernel_ns(self.h, ns.ctypes.data_as(U64P), cap)
+        if n < 0:
+            self._rc(n, "kernel_ns")
+        return ns[:n]
 
     def set_flush_each(self, on):
         lib().omega_gpu_decode_graph_set_flush_each(self.h, int(on))

@@ -10,9 +10,10 @@ generates). A seeded 512-token prompt runs through the decode graph first (untim
 hipGraph replay (token id in, greedy token out). value = tokens / second.
 
 The JSON line also carries:
-  roofline: the dominant kernel's algorithmic bytes per launch over its average duration, the
-            durations measured with HIP events on the library stream over a stamped pass of
-            the same decode steps; peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
+  roofline: the dominant kernel's algorithmic bytes per launch over its average duration; the
+            durations come from a stamped pass of the same decode steps in which every launch's
+            start and end are recorded by its own dispatch (hipExtLaunchKernel events on the
+            library stream); peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
             summary for that kernel when one exists (profiles/), else null.
   cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
             host cores: a bounded sample of 2 of the 48 layers x 4 tokens plus one full-vocab
@@ -41,22 +42,30 @@ def tid(layer, kind):
 
 
 def algorithmic_bytes(kind, ctx):
-    """HBM bytes one launch of a decode-graph kernel must move (weights, scales, activations)."""
-    if kind == "qkv":      # 5120 x 2048 e4m3 + f32 scales + x in + q out + K/V rows
-        return 5120 * 2048 + 40 * 16 * 4 + H * 4 + 4096 * 4 + 2 * 512 * 2
-    if kind == "attn":     # K and V of 4 heads over ctx positions + q + out
-        return 2 * KVH * ctx * HD * 2 + 2 * 4096 * 4
-    if kind == "o_proj":   # 2048 x 4096 e4m3 + scales + attn in + residual read/write
+    """HBM bytes one launch of a decode-graph kernel must move at context `ctx` (weights,
+    scales, activations in and out; the KV rows the attention must read)."""
+    splits = min(64, max(1, -(-(ctx - 1) // 64)))
+    if kind == "qkv":          # 5120 x 2048 e4m3 + scales + x + norm weights + q|k|v out
+        return 5120 * 2048 + 40 * 16 * 4 + 2 * H * 4 + 5120 * 4
+    if kind == "attn":         # K and V of 4 heads over ctx positions + q|k|v in + partials out
+        return 2 * KVH * ctx * HD * 2 + 5120 * 4 + QH * splits * 132 * 4
+    if kind == "attn_combine":  # the split partials in, the attention row out
+        return QH * splits * 132 * 4 + 4096 * 4
+    if kind == "o_proj":       # 2048 x 4096 e4m3 + scales + attention row + residual read/write
         return 2048 * 4096 + 16 * 32 * 4 + 4096 * 4 + 2 * H * 4
-    if kind == "router":   # bf16 gate + norm + x in + x' out
-        return E * H * 2 + 3 * H * 4
-    if kind == "gate_up":  # 8 experts x 1536 x 2048 e4m3 + scales + x' + activation out
-        return TOPK * (1536 * 2048 + 12 * 16 * 4) + H * 4 + TOPK * I * 4
-    if kind == "down":     # 8 experts x 2048 x 768 e4m3 + scales + activations + residual
+    if kind == "router":       # bf16 gate + norm weights + x in + x' out + logits
+        return E * H * 2 + 3 * H * 4 + E * 4
+    if kind == "gate_up":      # 8 experts x 1536 x 2048 e4m3 + scales + logits + x' + activations
+        return TOPK * (1536 * 2048 + 12 * 16 * 4) + E * 4 + H * 4 + TOPK * I * 4
+    if kind == "down":         # 8 experts x 2048 x 768 e4m3 + scales + activations + residual
         return TOPK * (2048 * 768 + 16 * 6 * 4) + TOPK * I * 4 + 2 * H * 4
-    if kind == "lm_head":  # 151936 x 2048 bf16 + final norm + logits
+    if kind == "lm_head":      # 151936 x 2048 bf16 + x + final norm + logits
         return V * H * 2 + 2 * H * 4 + V * 4
     return 0
+
+
+# the decode graph's launches per layer, in order, then the lm_head
+LAYER_KINDS = ["qkv", "attn", "attn_combine", "o_proj", "router", "gate_up", "down"]
 
 
 def build_model(om, max_pos):
@@ -123,6 +132,24 @@ def committed_traffic(kind):
     return None
 
 
+def copy_probe(nbytes):
+    """One device-to-device copy of `nbytes` (the runtime's copy kernel): the calibration run of
+    the HBM byte counters, whose FETCH_SIZE / WRITE_SIZE should read nbytes each."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    src, dst = C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(src), C.c_size_t(nbytes)) == 0
+    assert hip.hipMalloc(C.byref(dst), C.c_size_t(nbytes)) == 0
+    assert hip.hipMemset(src, 1, C.c_size_t(nbytes)) == 0
+    for _ in range(3):
+        assert hip.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +161,8 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run device-to-device copies of BYTES (byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs on a single MI355X and this build "
@@ -145,6 +174,9 @@ def main():
     if om.gpu_count() == 0:
         print("bench.py needs an MI355X", file=sys.stderr)
         sys.exit(3)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     total = args.prompt + args.warmup + args.steps + 8
     max_pos = om.round_max_pos(total)
     model = build_model(om, max_pos)
@@ -176,7 +208,8 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
 
-    # per-kernel durations: the same decode steps with HIP events between the launches
+    # per-kernel durations: the same decode steps once more with every launch's start and end
+    # recorded by its dispatch (what a kernel-trace profiler reports), on the library's stream
     g.set_stamps(True)
     per_kind = {}
     stamp_tokens = 4
@@ -184,15 +217,15 @@ def main():
     for _ in range(stamp_tokens):
         tok, _ = g.token_id(tok, pos)
         pos += 1
-        st, kinds = g.stamps()
-        d = np.diff(st.astype(np.int64))
-        for k, dt in zip(kinds, d):
-            name = om.KIND_NAMES[int(k)]
+        ns = g.kernel_ns()
+        assert len(ns) == len(LAYER_KINDS) * L + 1, len(ns)
+        for i, dt in enumerate(ns):
+            name = LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head"
             per_kind.setdefault(name, []).append(int(dt))
     g.set_stamps(False)
     kernels = {}
     for name, ds in per_kind.items():
-        n_launch = len(ds) / stamp_tokens
+        n_launch = len(ds) // stamp_tokens
         avg_ns = float(np.mean(ds))
         b = algorithmic_bytes(name, ctx_mid)
         kernels[name] = dict(launches_per_token=n_launch, avg_us=round(avg_ns / 1e3, 3),
@@ -201,8 +234,9 @@ def main():
     dom = max(kernels, key=lambda k: kernels[k]["us_per_token"])
     dk = kernels[dom]
     achieved = dk["algorithmic_bytes"] / (dk["avg_us"] * 1e3)
-    step_bytes = sum(algorithmic_bytes(k, ctx_mid) * int(v["launches_per_token"])
+    step_bytes = sum(algorithmic_bytes(k, ctx_mid) * v["launches_per_token"]
                      for k, v in kernels.items())
+    busy_us = sum(v["us_per_token"] for v in kernels.values())
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads)
     line = {
@@ -241,6 +275,8 @@ def main():
             "algorithmic_bytes_per_token": step_bytes,
             "achieved_GBs": round(step_bytes / (ms_per_step * 1e6), 1),
             "frac": round(step_bytes / (ms_per_step * 1e6) / PEAK_GBS, 4),
+            "kernel_busy_us_per_token": round(busy_us, 1),
+            "launches_per_token": len(LAYER_KINDS) * L + 1,
         },
         "kernels": kernels,
         "cpu_baseline": cpu,

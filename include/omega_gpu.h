@@ -498,13 +498,16 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
                                         uint32_t num_q_heads, uint32_t num_kv_heads,
                                         uint32_t head_dim, float *out_dev);
 /* the decode graph with the embedding row gathered on the device: set a [vocab][2048] bf16
- * tensor once, then each token passes only its id (8 bytes go up, 4 come back) */
+ * tensor once, then each token passes only its id */
 int omega_gpu_decode_graph_set_embedding(OmegaGpuDecodeGraph *g, const void *embed_bf16);
 int omega_gpu_decode_graph_token_id(OmegaGpuDecodeGraph *g, uint32_t token_in, uint32_t pos,
                                     uint32_t *token, OmegaGpuDecodeGraphStats *st);
 /* the routed expert ids and weights of every layer of the decode graph's last token
  * ([layers][8] each; either pointer may be NULL) — a trace for parity checks */
 int omega_gpu_decode_graph_read_routes(OmegaGpuDecodeGraph *g, uint32_t *ids, float *weights);
+/* with stamps on: the duration (ns) of every launch of the last token, start to end of the
+ * dispatch as the hardware recorded it (no launch gaps); returns launches or rc<0 */
+int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap);
 /* the library's HIP stream (hipStream_t) and a full synchronisation of it */
 void *omega_gpu_stream(void);
 int omega_gpu_sync(void);

@@ -151,7 +151,10 @@ def test_stamps_time_every_launch(omega, small):
     g.graph.set_stamps(True)
     g.graph.token(g.x_embed(9), 0)
     st, kinds = g.graph.stamps()
+    ns = g.graph.kernel_ns()
     g.graph.set_stamps(False)
+    # every launch's own duration, inside the token's span
+    assert len(ns) == len(kinds) and (ns > 0).all() and ns.sum() <= st[-1]
     assert len(kinds) == 7 * m.cfg.layers + 1
     assert (np.diff(st.astype(np.int64)) >= 0).all()
     names = [omega.kind_name(int(k)) for k in kinds[:7]]
