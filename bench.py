@@ -16,8 +16,8 @@ The JSON line also carries:
             library stream); peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
             summary for that kernel when one exists (profiles/), else null.
   cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
-            host cores: a bounded sample of 2 of the 48 layers x 4 tokens plus one full-vocab
-            lm_head, scaled to the 48-layer step.
+            host cores: a bounded sample of 4 of the 48 layers x 128 tokens plus 4 full-vocab
+            lm_heads (about 10 s of CPU work), scaled to the 48-layer step.
 """
 import argparse
 import json
@@ -100,25 +100,27 @@ def cpu_baseline(threads):
     """The oracle engine on a bounded sample, scaled to the 48-layer step (see module doc)."""
     import pyoracle as orc
 
-    cfg = dict(layers=2, hidden=H, q_heads=QH, kv_heads=KVH, head_dim=HD, experts=E, top_k=TOPK,
-               inter=I, vocab=V, eps=1e-6, rope_theta=1e6)
+    layers, tokens, heads = 4, 128, 4
+    cfg = dict(layers=layers, hidden=H, q_heads=QH, kv_heads=KVH, head_dim=HD, experts=E,
+               top_k=TOPK, inter=I, vocab=V, eps=1e-6, rope_theta=1e6)
     m = orc.Model(cfg, SEED, sigma=0.02, norm_sigma=0.0, threads=threads)
     eng = orc.Engine(m, 256, refined_router=True, threads=threads)
-    tokens = 4
     hid = eng.step(1)   # first touch of every weight page
     t0 = time.perf_counter()
     for t in range(tokens):
         hid = eng.step(2 + t)
-    t_layers = (time.perf_counter() - t0) / tokens / cfg["layers"]
+    t_layers = (time.perf_counter() - t0) / tokens / layers
     t1 = time.perf_counter()
-    eng.logits(hid)
-    t_lm = time.perf_counter() - t1
+    for _ in range(heads):
+        eng.logits(hid)
+    t_lm = (time.perf_counter() - t1) / heads
     step = t_layers * L + t_lm
     return {"value": round(1.0 / step, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"C oracle engine (oracle/oracle.c, {threads} threads, per-output-row "
-                      f"parallel GEMV): 2 of 48 layers x {tokens} tokens at positions 1-4 "
-                      f"({t_layers * 1e3:.1f} ms/layer) + one 151936-row lm_head "
-                      f"({t_lm * 1e3:.1f} ms), scaled to 48 layers: {step:.3f} s/token"}
+                      f"parallel GEMV): {layers} of 48 layers x {tokens} tokens at positions "
+                      f"2-{tokens + 1} ({t_layers * 1e3:.1f} ms/layer) + {heads} 151936-row "
+                      f"lm_heads ({t_lm * 1e3:.1f} ms each), scaled to 48 layers: "
+                      f"{step:.3f} s/token"}
 
 
 def committed_traffic(kind):
