@@ -218,13 +218,11 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         psum += __shfl_xor(psum, 32, 64);
         l_l = l_l * alpha + psum;
         m_l = m_new;
-        // rescale the accumulators: rows 4 g + i hold head (4 g + i) % 8
-        float ah[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) ah[r] = readlane_f32(alpha, r);
+        // rescale the accumulators: rows 4 g + i hold head (4 g + i) % 8, whose alpha lane
+        // (4 g + i) % 8 holds
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float ai = (g & 1) ? ah[4 + i] : ah[i];
+            const float ai = __shfl(alpha, (4 * g + i) & 7, 64);
 #pragma unroll
             for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
         }
@@ -252,27 +250,25 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) O[nb][i] += __shfl_xor(O[nb][i], 32, 64);
-    float mh[8], lh[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        mh[r] = readlane_f32(m_l, r);
-        lh[r] = readlane_f32(l_l, r);
-    }
     if (s == 0) {
-        // this token: one more online-softmax step with score spos and value vs
-        float aold[8], pp[8];
+        // this token: one more online-softmax step with score spos and value vs, done per head
+        // column (lane n holds head n % 8) and gathered into the accumulator rows
+        __shared__ float sp_sh[8];
+        if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const float m_new = fmaxf(mh[r], spos[r]);
-            aold[r] = expf(mh[r] - m_new);
-            pp[r] = expf(spos[r] - m_new);
-            lh[r] = lh[r] * aold[r] + pp[r];
-            mh[r] = m_new;
+            for (int r = 0; r < 8; ++r) sp_sh[r] = spos[r];
         }
+        __syncthreads();
+        const float sp = sp_sh[n & 7];
+        const float m_new = fmaxf(m_l, sp);
+        const float aold = expf(m_l - m_new);
+        const float pnow = expf(sp - m_new);
+        l_l = l_l * aold + pnow;
+        m_l = m_new;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float ai = (g & 1) ? aold[4 + i] : aold[i];
-            const float pi = (g & 1) ? pp[4 + i] : pp[i];
+            const float ai = __shfl(aold, (4 * g + i) & 7, 64);
+            const float pi = __shfl(pnow, (4 * g + i) & 7, 64);
 #pragma unroll
             for (int nb = 0; nb < 8; ++nb) O[nb][i] = fmaf(pi, vs[16 * nb + n], O[nb][i] * ai);
         }
@@ -286,17 +282,10 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
             for (int nb = 0; nb < 8; ++nb) pp[4 + 16 * nb + n] = O[nb][i];
         }
     }
-    if (lane < 8) {
-        float mm = 0.f, ll = 0.f;
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-            if (lane == (uint32_t)r) {
-                mm = mh[r];
-                ll = lh[r];
-            }
+    if (lane < 8) {  // lane r holds head r's running max and sum
         float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
-        pp[0] = mm;
-        pp[1] = ll;
+        pp[0] = m_l;
+        pp[1] = l_l;
     }
 }
 
@@ -431,22 +420,54 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 // Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l); fused partials are
 // dims in order. Either way partial dim d sits at 4 + d, so one combine serves both.
 __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
+    __shared__ float wsh[64];
     const uint32_t head = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     uint32_t tiles;
     if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + kAttnTile - 1) / kAttnTile;
     else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + kAttnTile - 1) / kAttnTile;
     uint32_t active, tps;
-    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);
+    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= 64
     const float *pp = a.part + ((size_t)b * a.qh + head) * a.splits * kPartStride;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < active; ++s) M = fmaxf(M, pp[s * kPartStride]);
-    float L = 0.f, O0 = 0.f, O1 = 0.f;
-    for (uint32_t s = 0; s < active; ++s) {
-        const float *q = pp + s * kPartStride;
-        const float w = a.mutant == 4 ? 1.0f : expf(q[0] - M);
-        L = fmaf(q[1], w, L);
-        O0 = fmaf(q[4 + lane], w, O0);
-        O1 = fmaf(q[68 + lane], w, O1);
+    // lane s holds split s's (m, l); the first 16 splits' o rows are loaded with them, so a
+    // short context costs one round trip
+    const bool mine = lane < active;
+    const float m = mine ? *as_global_f32(pp + lane * kPartStride) : -INFINITY;
+    const float l = mine ? *as_global_f32(pp + lane * kPartStride + 1) : 0.f;
+    constexpr uint32_t kFirst = 16;
+    float f0[kFirst], f1[kFirst];
+#pragma unroll
+    for (uint32_t j = 0; j < kFirst; ++j) {
+        const bool ok = j < active;
+        f0[j] = ok ? *as_global_f32(pp + j * kPartStride + 4 + lane) : 0.f;
+        f1[j] = ok ? *as_global_f32(pp + j * kPartStride + 68 + lane) : 0.f;
+    }
+    float M = row16_max(m);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    const float w = mine ? (a.mutant == 4 ? 1.0f : expf(m - M)) : 0.f;
+    const float L = wave_sum(w * l);
+    wsh[lane] = w;
+    __syncthreads();
+    float O0 = 0.f, O1 = 0.f;
+#pragma unroll
+    for (uint32_t j = 0; j < kFirst; ++j) {
+        O0 = fmaf(f0[j], wsh[j], O0);
+        O1 = fmaf(f1[j], wsh[j], O1);
+    }
+    for (uint32_t s0 = kFirst; s0 < active; s0 += 8) {
+        float o0[8], o1[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool ok = s0 + j < active;
+            const float *q = pp + (size_t)(s0 + j) * kPartStride;
+            o0[j] = ok ? *as_global_f32(q + 4 + lane) : 0.f;
+            o1[j] = ok ? *as_global_f32(q + 68 + lane) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (s0 + j >= active) break;
+            O0 = fmaf(o0[j], wsh[s0 + j], O0);
+            O1 = fmaf(o1[j], wsh[s0 + j], O1);
+        }
     }
     const float inv = a.out_scale / L;
     float *op = a.out + ((size_t)b * a.qh + head) * 128;

@@ -52,18 +52,21 @@ __global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
     float nw[P][8];
     S::load_x(a.x, lane, xr);
     if (NORM) S::load_x(a.norm_w, lane, nw);
+    // the final RMSNorm as one scale on the row sums (the sum of squares runs beside the stream)
+    float scale = 1.0f;
     if (NORM) {
-        const float scale = rms_scale(phases_sumsq(xr), kLmK, a.eps);
+        const double ss = phases_sumsq(xr);
 #pragma unroll
         for (int ph = 0; ph < P; ++ph)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xr[ph][i] = xr[ph][i] * scale * nw[ph][i];
+            for (int i = 0; i < 8; ++i) xr[ph][i] = xr[ph][i] * nw[ph][i];
+        scale = rms_scale(ss, kLmK, a.eps);
         if (a.hidden_out && blockIdx.x == 0 && wid == 0) {
 #pragma unroll
             for (int ph = 0; ph < P; ++ph) {
                 float4 *o = reinterpret_cast<float4 *>(a.hidden_out + S::col(ph, lane));
-                o[0] = make_float4(xr[ph][0], xr[ph][1], xr[ph][2], xr[ph][3]);
-                o[1] = make_float4(xr[ph][4], xr[ph][5], xr[ph][6], xr[ph][7]);
+                o[0] = make_float4(xr[ph][0] * scale, xr[ph][1] * scale, xr[ph][2] * scale, xr[ph][3] * scale);
+                o[1] = make_float4(xr[ph][4] * scale, xr[ph][5] * scale, xr[ph][6] * scale, xr[ph][7] * scale);
             }
         }
     }
@@ -80,7 +83,9 @@ __global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
             slab.v[c] = (two || c < S::CH / 2) ? __builtin_nontemporal_load(p + c * 64) : u32x4{0u, 0u, 0u, 0u};
         float acc[kLmRows] = {0.f, 0.f};
         slab.dot(xr, acc, lane);
-        float v = reduce_rows(acc, lane);
+        float v = reduce_rows(acc, lane) * scale;
+        acc[0] *= scale;
+        acc[1] *= scale;
         if (a.mutant == 1) {
             v = -v;
             acc[0] = -acc[0];

@@ -14,8 +14,8 @@
 //   3. the combine of the attention splits,
 //   4. o GEMV whose epilogue adds into the residual row,
 //   5. router logits (post-attention RMSNorm, exact f64 dot products),
-//   6. gate|up GEMV of the 8 routed experts: the top-8 ranking in its prologue, SwiGLU in its
-//      epilogue,
+//   6. gate|up GEMV of the 8 routed experts: the top-8 ranking in its prologue (one wavefront
+//      per workgroup ranks, LDS shares), SwiGLU in its epilogue,
 //   7. down GEMV: one workgroup = the 8 experts' wavefronts for 8 rows, combined in slot order
 //      in LDS and added into the residual,
 // then the lm_head with the final RMSNorm in its prologue and the argmax folded in: 7L + 1
@@ -66,35 +66,27 @@ constexpr uint32_t kGuPairs = 2;  // gate/up row pairs per wavefront
 __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     using S = Fp8Slab<kHidden, kGuPairs>;
     constexpr int P = S::P;
-    const uint32_t lane = lane_id();
-    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    __shared__ uint32_t sh_id[kTopK];
+    __shared__ float sh_w[kTopK];
+    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
+    const uint32_t item = blockIdx.x * 4 + wid;
     const uint32_t slot = item / (kInter / kGuPairs), j0 = (item % (kInter / kGuPairs)) * kGuPairs;
     float xr[P][16];
     S::load_x(a.xn, lane, xr);
-    Route r;
-    route_topk(a.logits, kExperts, 0, a.norm_topk, a.route_mutant, r);
-    if (item == 0 && lane < (uint32_t)kTopK) {
-        uint32_t id = 0;
-        float wt = 0.f;
+    // wavefront 0 ranks the logits for the workgroup
+    if (wid == 0) {
+        Route r;
+        route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
+        if (lane == 0) {
 #pragma unroll
-        for (int s = 0; s < kTopK; ++s)
-            if (lane == (uint32_t)s) {
-                id = r.id[s];
-                wt = r.w[s];
+            for (int s = 0; s < kTopK; ++s) {
+                sh_id[s] = r.id[s];
+                sh_w[s] = r.w[s];
             }
-        a.ids[lane] = id;
-        a.weights[lane] = wt;
-        if (a.log_ids) a.log_ids[lane] = id;
-        if (a.log_w) a.log_w[lane] = wt;
-        a.tab_gu[2 * lane] = a.dir_gu[2 * id];
-        a.tab_gu[2 * lane + 1] = a.dir_gu[2 * id + 1];
-        a.tab_dn[2 * lane] = a.dir_dn[2 * id];
-        a.tab_dn[2 * lane + 1] = a.dir_dn[2 * id + 1];
+        }
     }
-    uint32_t e = r.id[0];
-#pragma unroll
-    for (int s = 1; s < kTopK; ++s)
-        if (slot == (uint32_t)s) e = r.id[s];
+    __syncthreads();
+    const uint32_t e = sh_id[slot];
     const uint8_t *we = a.w + (size_t)e * 2 * kInter * kHidden;
     const float *se = a.s + (size_t)e * (2 * kInter / 128) * (kHidden / 128);
     S gate, up;
@@ -103,6 +95,21 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     float scg[P], scu[P];
     S::load_scales(se + (size_t)(j0 >> 7) * (kHidden / 128), lane, 1.0f, 0, scg);
     S::load_scales(se + (size_t)((kInter + j0) >> 7) * (kHidden / 128), lane, 1.0f, 0, scu);
+    // workgroup 0 publishes the route once its own weight stream is in flight
+    if (blockIdx.x == 0 && wid == 0 && lane < (uint32_t)kTopK) {
+        const uint32_t id = sh_id[lane];
+        const float wt = sh_w[lane];
+        const uint64_t gu0 = a.dir_gu[2 * id], gu1 = a.dir_gu[2 * id + 1];
+        const uint64_t dn0 = a.dir_dn[2 * id], dn1 = a.dir_dn[2 * id + 1];
+        a.ids[lane] = id;
+        a.weights[lane] = wt;
+        if (a.log_ids) a.log_ids[lane] = id;
+        if (a.log_w) a.log_w[lane] = wt;
+        a.tab_gu[2 * lane] = gu0;
+        a.tab_gu[2 * lane + 1] = gu1;
+        a.tab_dn[2 * lane] = dn0;
+        a.tab_dn[2 * lane + 1] = dn1;
+    }
     float ag[kGuPairs], au[kGuPairs];
 #pragma unroll
     for (uint32_t j = 0; j < kGuPairs; ++j) ag[j] = au[j] = 0.f;

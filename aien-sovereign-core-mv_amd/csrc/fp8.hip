@@ -65,6 +65,9 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     float sc[P];
     S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, a.x_scale, a.mutant, sc);
 
+    // RMSNorm is one scale per row: dot with x * w and scale the row sums at the end, so the
+    // f64 sum of squares runs beside the weight stream instead of ahead of it
+    float scale = 1.0f;
     if (XSRC != XS_F32) {
         static_assert(XSRC == XS_F32 || P * 16 * 64 == K, "the phases must partition the row");
         if (XSRC == XS_EMBED_NORM && blockIdx.x == 0 && threadIdx.x < 64) {
@@ -76,17 +79,18 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
                     o[i] = make_float4(xr[ph][4 * i], xr[ph][4 * i + 1], xr[ph][4 * i + 2], xr[ph][4 * i + 3]);
             }
         }
-        const float scale = rms_scale(phases_sumsq(xr), K, a.eps);
+        const double ss = phases_sumsq(xr);
 #pragma unroll
         for (int ph = 0; ph < P; ++ph)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xr[ph][i] = xr[ph][i] * scale * nw[ph][i];
+            for (int i = 0; i < 16; ++i) xr[ph][i] = xr[ph][i] * nw[ph][i];
+        scale = rms_scale(ss, K, a.eps);
     }
     float acc[RPW];
 #pragma unroll
     for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
     slab.dot(xr, sc, acc, lane);
-    const float v = reduce_rows(acc, lane);
+    const float v = reduce_rows(acc, lane) * scale;
     if (lane < (uint32_t)RPW) {
         const size_t row = (size_t)g * a.n + row0 + lane;
         if (EPI == EPI_STORE) a.y[row] = v;

@@ -6,9 +6,10 @@
 // the lower id; weight = exp(l - max) / sum over the selected of exp(l - max) (norm_topk), or
 // over every expert; the optional shared expert takes the last slot with sigmoid(logit).
 //
-// Every lane ends with the same result. Each of the 8 rounds finds the best remaining
-// (key, id) inside every 16-lane row with DPP exchanges, then across the four rows with
-// readlane, so a round is a few dozen instructions with no LDS traffic.
+// Each candidate becomes one 64-bit key, (total-order value << 32) | ~id, whose unsigned maximum
+// is the next pick (larger logit first, then the lower id). A round is one 64-bit max inside
+// every 16-lane row (DPP), two cross-row exchanges and a mask of the pick, so the 8 rounds stay
+// a few hundred instructions; every lane ends with the same result.
 #pragma once
 
 #include "device.hpp"
@@ -29,69 +30,56 @@ __device__ __forceinline__ int32_t total_key(float f) {
 __device__ __forceinline__ float key_value(int32_t k) {
     return __int_as_float(k < 0 ? (k ^ 0x7fffffff) : k);
 }
-// (ok, oi) beats (bk, bi): a real candidate with a larger key, or an equal key and lower id
-__device__ __forceinline__ bool key_beats(int32_t ok, uint32_t oi, int32_t bk, uint32_t bi) {
-    return oi != 0xffffffffu && (bi == 0xffffffffu || ok > bk || (ok == bk && oi < bi));
+__device__ __forceinline__ uint64_t route_key(float v, uint32_t id) {
+    const uint32_t ord = (uint32_t)total_key(v) ^ 0x80000000u;
+    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - id);
 }
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 template <int CTRL>
-__device__ __forceinline__ void key_step(int32_t &bk, uint32_t &bi) {
-    const int32_t ok = dpp_i32<CTRL>(bk);
-    const uint32_t oi = (uint32_t)dpp_i32<CTRL>((int32_t)bi);
-    if (key_beats(ok, oi, bk, bi)) {
-        bk = ok;
-        bi = oi;
-    }
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+// the maximum over the wavefront, in every lane
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t b) {
+    b = max_u64(b, dpp_u64<DPP_XOR1>(b));
+    b = max_u64(b, dpp_u64<DPP_XOR2>(b));
+    b = max_u64(b, dpp_u64<DPP_HALF_MIRROR>(b));
+    b = max_u64(b, dpp_u64<DPP_MIRROR>(b));
+    b = max_u64(b, shfl_xor_u64(b, 16));
+    return max_u64(b, shfl_xor_u64(b, 32));
 }
 
-// logits: experts (+1 shared) values in global memory; experts 128 or 256.
+// logits: Q * 64 expert values (+1 shared) in global memory.
 // mutant 2: the mask after a pick hits id ^ 1; mutant 4: weights not normalised.
-__device__ __forceinline__ void route_topk(const float *logits, uint32_t experts, uint32_t shared,
-                                           int norm_topk, int mutant, Route &r) {
+template <int Q>
+__device__ __forceinline__ void route_topk(const float *logits, uint32_t shared, int norm_topk,
+                                           int mutant, Route &r) {
+    constexpr uint32_t experts = 64 * Q;
     const uint32_t lane = lane_id();
-    float lv[4];
-    int32_t key[4];
-    bool taken[4];
+    uint64_t pk[Q];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t id = lane + 64 * q;
-        taken[q] = id >= experts;
-        lv[q] = taken[q] ? 0.f : *as_global_f32(logits + id);
-        key[q] = total_key(lv[q]);
-    }
+    for (int q = 0; q < Q; ++q) pk[q] = route_key(*as_global_f32(logits + lane + 64 * q), lane + 64 * q);
     float v[kTopK];
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
-        int32_t bk = INT32_MIN;
-        uint32_t bi = 0xffffffffu;
+        uint64_t b = pk[0];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t id = lane + 64 * q;
-            if (!taken[q] && (bi == 0xffffffffu || key[q] > bk)) {
-                bk = key[q];
-                bi = id;
-            }
-        }
-        key_step<DPP_XOR1>(bk, bi);
-        key_step<DPP_XOR2>(bk, bi);
-        key_step<DPP_HALF_MIRROR>(bk, bi);
-        key_step<DPP_MIRROR>(bk, bi);
-        int32_t k0 = __builtin_amdgcn_readlane(bk, 0);
-        uint32_t i0 = (uint32_t)__builtin_amdgcn_readlane((int32_t)bi, 0);
+        for (int q = 1; q < Q; ++q) b = max_u64(b, pk[q]);
+        b = wave_max_u64(b);
+        const uint32_t id = 0xffffffffu - (uint32_t)b;
+        r.id[s] = id;
+        v[s] = key_value((int32_t)((uint32_t)(b >> 32) ^ 0x80000000u));
+        const uint32_t mask_id = mutant == 2 ? (id ^ 1u) : id;
 #pragma unroll
-        for (int row = 1; row < 4; ++row) {
-            const int32_t kr = __builtin_amdgcn_readlane(bk, 16 * row);
-            const uint32_t ir = (uint32_t)__builtin_amdgcn_readlane((int32_t)bi, 16 * row);
-            if (key_beats(kr, ir, k0, i0)) {
-                k0 = kr;
-                i0 = ir;
-            }
-        }
-        r.id[s] = i0;
-        v[s] = key_value(k0);
-        const uint32_t mask_id = mutant == 2 ? (i0 ^ 1u) : i0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (lane + 64 * q == mask_id) taken[q] = true;
+        for (int q = 0; q < Q; ++q)
+            if (lane + 64 * q == mask_id) pk[q] = 0;
     }
     const float mx = v[0];
     float p[kTopK];

@@ -65,7 +65,8 @@ __global__ __launch_bounds__(256) void k_router_logits(const RouterArgs a) {
 
 __global__ __launch_bounds__(64) void k_router_topk(const RouterArgs a) {
     Route r;
-    route_topk(a.logits, a.experts, a.shared, a.norm_topk, a.mutant, r);
+    if (a.experts == 256) route_topk<4>(a.logits, a.shared, a.norm_topk, a.mutant, r);
+    else route_topk<2>(a.logits, a.shared, a.norm_topk, a.mutant, r);
     const uint32_t lane = lane_id();
     const uint32_t slots = kTopK + (a.shared ? 1 : 0);
 #pragma unroll
