@@ -10,14 +10,16 @@
 // (tensor.rs:164-190) and the bf16 append of aien-kv-cache write_token_kv.
 //
 // Fused kernel (k_dattn): per (split, kv head) one wavefront. The tokens before `pos` are cut
-// into tiles of 64 spread over the splits. Both products run on the bf16 matrix cores
-// (v_mfma_f32_16x16x32_bf16) with the f32 operand split into a bf16 (hi, lo) pair: the 16
-// B-columns of S^T = K q^T are the 8 q heads' hi and lo halves, the 16 A-rows of O = P V are
-// the 8 heads' probability hi and lo halves, and hi + lo rows are added at the end — products
-// with the bf16 K / V are exact, so the result carries about 2^-16 relative error per operand
-// instead of bf16's 2^-8. Token order inside a tile is permuted (tau below) so that every lane
-// reads K as 64 contiguous bytes per row and V as 16 contiguous bytes per (dim, 8 tokens), which
-// is why the cache stores each page's V plane transposed ([head][dim][16 tokens]). Split 0 also
+// into 16-token pages spread over up to 64 splits, so a short context already spreads its page
+// reads over many CUs (a CU's own loads share one queue: four wavefronts' pages on one CU arrive
+// about twice as late as the same pages spread over four CUs). Both products run on the bf16
+// matrix cores with the f32 operand split into a bf16 (hi, lo) pair: the 16 B-columns of
+// S^T = K q^T (v_mfma_f32_16x16x32_bf16) are the 8 q heads' hi and lo halves, the 16 A-rows of
+// O = P V (v_mfma_f32_16x16x16_bf16) the 8 heads' probability hi and lo halves, and hi + lo
+// rows are added at the end — products with the bf16 K / V are exact, so the result carries
+// about 2^-16 relative error per operand instead of bf16's 2^-8. The cache stores each page's V
+// plane transposed ([head][dim][16 tokens]) so that a lane's 4 tokens of one dim are 8
+// contiguous bytes. The 8 heads' RMSNorm scales come from one transposed f64 reduction. Split 0
 // appends this token's K/V and folds it in as one more online-softmax step. A second small
 // launch combines the splits (k_attn_combine); nothing is exchanged between workgroups inside a
 // launch.
@@ -36,44 +38,31 @@ constexpr uint32_t kVtHead = 4096;  // bytes per kv head of a transposed V plane
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// token of row m of block b in a 64-token tile
-__device__ __forceinline__ uint32_t tile_token(uint32_t b, uint32_t m) {
-    return 16 * (m / 4) + 8 * (b / 2) + 4 * (b % 2) + (m % 4);
-}
+typedef short s16x4 __attribute__((ext_vector_type(4)));  // a 16x16x16 bf16 operand
 
-struct DattnTile {
-    u32x4 k[4][4];  // [block][k-step]: K[token][32 g + 8 ks .. +8]
-    u32x4 v[2][8];  // [pv step][n-block]: V^T[dim 16 nb + n][tokens 8 p .. +8] of page g
+// one 16-token page: lane (g = lane / 16, n = lane % 16) holds token n's K dims 32 ks + 8 g .. +8
+// for k-step ks (the four lane groups of a k-step read 64 contiguous bytes of each K row), and
+// V^T[dim 16 nb + n][tokens 4 g .. +4] for n-block nb
+struct DattnPage {
+    u32x4 k[4];
+    u32x2 v[8];
 };
 
-__device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint32_t tile, uint32_t lane,
-                                           DattnTile &T) {
+__device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint32_t page, uint32_t lane,
+                                           DattnPage &T) {
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t tok0 = tile * kAttnTile;
-    const uint8_t *lay = a.pool + (uint64_t)a.layer * a.g.layer_stride;
+    const uint8_t *pg = a.pool + (uint64_t)a.layer * a.g.layer_stride + (uint64_t)page * a.g.block_stride;
+    const gu32x4 *kp = as_global(pg + (uint64_t)n * a.g.token_stride + (uint64_t)h * a.g.head_stride + 16 * g);
 #pragma unroll
-    for (uint32_t b = 0; b < 4; ++b) {
-        const uint32_t tok = tok0 + tile_token(b, n);
-        const gu32x4 *kp = as_global(lay + (uint64_t)(tok >> 4) * a.g.block_stride +
-                                     (uint64_t)(tok & 15) * a.g.token_stride +
-                                     (uint64_t)h * a.g.head_stride + 64 * g);
+    for (int ks = 0; ks < 4; ++ks) T.k[ks] = __builtin_nontemporal_load(kp + 4 * ks);
+    const uint8_t *vp = pg + a.g.plane_stride + (uint64_t)h * kVtHead + n * 32 + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) T.k[b][ks] = __builtin_nontemporal_load(kp + ks);
-    }
-    const uint8_t *vp = lay + (uint64_t)((tok0 >> 4) + g) * a.g.block_stride + a.g.plane_stride +
-                        (uint64_t)h * kVtHead + n * 32;
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-            T.v[p][nb] = __builtin_nontemporal_load(as_global(vp + nb * 16 * 32 + p * 16));
+    for (int nb = 0; nb < 8; ++nb) T.v[nb] = __builtin_nontemporal_load(as_global_u32x2(vp + nb * 16 * 32));
 }
 
-// RMSNorm of one head held as (dims lane, lane + 64), f64 sum of squares, then RoPE
-__device__ __forceinline__ void head_norm_rope(float &v0, float &v1, float w0, float w1, float rc,
-                                               float rs, float eps, bool rope) {
-    const double ss = wave_sum_f64((double)v0 * (double)v0 + (double)v1 * (double)v1);
-    const float scale = rms_scale(ss, 128, eps);
+// RMSNorm (given the head's scale) then RoPE of one head held as (dims lane, lane + 64)
+__device__ __forceinline__ void head_scale_rope(float &v0, float &v1, float scale, float w0, float w1, float rc,
+                                                float rs, bool rope) {
     float n0 = v0 * scale * w0;
     float n1 = v1 * scale * w1;
     if (rope) {
@@ -86,19 +75,75 @@ __device__ __forceinline__ void head_norm_rope(float &v0, float &v1, float w0, f
     v1 = n1;
 }
 
+// One online-softmax step over a page whose first token is tok0 (< pos). The online state of
+// head n % 8 (m, l) sits in every lane of column n; O[nb][i] is row 4 g + i (head (4 g + i) % 8,
+// hi half for g < 2, lo half otherwise), dim 16 nb + n.
+template <bool FIRST>  // FIRST: no earlier page, so the running state starts here (nothing to rescale)
+__device__ __forceinline__ void dattn_page(const DattnPage &T, const bf16x8 (&qop)[4], uint32_t tok0,
+                                           uint32_t pos, uint32_t g, uint32_t n, float &m_l, float &l_l,
+                                           f32x4 (&O)[8]) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), qop[ks], acc, 0, 0, 0);
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float full = acc[i] + dpp_f32<DPP_ROR8>(acc[i]);  // hi + lo columns
+        sc[i] = tok0 + 4 * g + i < pos ? full * kInvSqrt128 : -INFINITY;
+    }
+    // max and sum over the four lane groups (rows) of a column: row swaps, no LDS
+    const float mx = xor_max<32>(xor_max<16>(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))));
+    const float m_new = FIRST ? mx : fmaxf(m_l, mx);  // finite: token tok0 is valid
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pr[i] = expf(sc[i] - m_new);
+        psum += pr[i];
+    }
+    psum = xor_sum<32>(xor_sum<16>(psum));
+    if (FIRST) {
+        l_l = psum;
+    } else {
+        const float alpha = expf(m_l - m_new);
+        l_l = l_l * alpha + psum;
+        // accumulator row 4 g + i belongs to head (4 g + i) % 8: head i for even g, 4 + i for
+        // odd g, whose alpha every row's lane (head) holds
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a_lo = readlane_f32(alpha, i), a_hi = readlane_f32(alpha, 4 + i);
+            const float ai = (g & 1) ? a_hi : a_lo;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
+        }
+    }
+    m_l = m_new;
+    // A operand of O = P V: row n = head n % 8 (hi or lo half), k = tokens 4 g .. +4
+    s16x4 pop;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pop[i] = (short)(n < 8 ? bf16_split_hi(pr[i]) : bf16_split_lo(pr[i]));
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+        O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pop, __builtin_bit_cast(s16x4, T.v[nb]), O[nb], 0, 0, 0);
+}
+
 __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
-    __shared__ float qs[8][128];
-    __shared__ float vs[128];
-    const uint32_t lane = threadIdx.x, s = blockIdx.x, h = blockIdx.y;
+    __shared__ __align__(16) uint16_t qhl[2][8][128];  // the prepared q heads: bf16 hi, lo halves
+    __shared__ float vs[128];        // split 0: this token's V as stored (bf16 values)
+    __shared__ float sp_sh[8];       // split 0: this token's score per head
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint32_t pos = a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host;
-    const uint32_t tiles = (pos + kAttnTile - 1) / kAttnTile;
-    uint32_t active, tps;
-    attn_split_plan(tiles, gridDim.x, a.tiles_per_split, active, tps);
+    const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
+    uint32_t active, pps;
+    attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
     if (s >= active) return;
-    const uint32_t t_begin = s * tps, t_end = min(tiles, t_begin + tps);
+    const uint32_t p_begin = s * pps, p_end = min(pages, p_begin + pps);
 
-    // prologue loads: the 8 q heads (dims lane, lane + 64), norms and the RoPE row at pos
+    // Every load below is issued unconditionally, the page stream last: vector-memory waits
+    // complete in issue order and merge conservatively at branch joins, so a conditional load
+    // here would make the preparation math wait on the page stream.
     const float *qraw = a.qkv + h * 8 * 128;
     float q0[8], q1[8];
 #pragma unroll
@@ -109,29 +154,35 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
     const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
     const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
-    float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f, kw0 = 0.f, kw1 = 0.f;
-    if (s == 0) {
-        k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
-        k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
-        v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
-        v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
-        kw0 = *as_global_f32(a.k_norm + lane);
-        kw1 = *as_global_f32(a.k_norm + 64 + lane);
-    }
-    // the first tile's K/V stream starts before the preparation math
-    DattnTile T;
-    if (t_begin < t_end) dattn_load(a, h, t_begin, lane, T);
+    float k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
+    float k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
+    const float v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
+    const float v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
+    const float kw0 = *as_global_f32(a.k_norm + lane);
+    const float kw1 = *as_global_f32(a.k_norm + 64 + lane);
+    // the first page's K/V stream starts before the preparation math (page 0 stands in when the
+    // split has no page: pos == 0)
+    DattnPage T;
+    dattn_load(a, h, p_begin < p_end ? p_begin : 0, lane, T);
+    __builtin_amdgcn_sched_barrier(0);  // all of the above is issued before any arithmetic
 
+    // the 8 heads' f64 sums of squares in one reduction; lane l then holds head l / 8's scale
     const bool rope = a.mutant != 1;
+    double ss[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ss[r] = (double)q0[r] * (double)q0[r] + (double)q1[r] * (double)q1[r];
+    const float scale_l = rms_scale(head_sums8(ss, lane), 128, a.eps);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-        head_norm_rope(q0[r], q1[r], qw0, qw1, rc, rs, a.eps, rope);
-        qs[r][lane] = q0[r];
-        qs[r][lane + 64] = q1[r];
+        head_scale_rope(q0[r], q1[r], readlane_f32(scale_l, 8 * r), qw0, qw1, rc, rs, rope);
+        qhl[0][r][lane] = bf16_split_hi(q0[r]);
+        qhl[1][r][lane] = bf16_split_lo(q0[r]);
+        qhl[0][r][lane + 64] = bf16_split_hi(q1[r]);
+        qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
     }
-    float spos[8];
     if (s == 0) {
-        head_norm_rope(k0, k1, kw0, kw1, rc, rs, a.eps, rope);
+        const float kscale = rms_scale(wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1), 128, a.eps);
+        head_scale_rope(k0, k1, kscale, kw0, kw1, rc, rs, rope);
         const uint16_t kb0 = bf16_rne(k0), kb1 = bf16_rne(k1);
         const uint16_t vb0 = bf16_rne(v0), vb1 = bf16_rne(v1);
         if (a.mutant != 3) {
@@ -149,116 +200,54 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         const float kf0 = bf16_to_f32(kb0), kf1 = bf16_to_f32(kb1);
         vs[lane] = bf16_to_f32(vb0);
         vs[lane + 64] = bf16_to_f32(vb1);
+        float d[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) spos[r] = wave_sum(fmaf(q0[r], kf0, q1[r] * kf1)) * kInvSqrt128;
+        for (int r = 0; r < 8; ++r) d[r] = fmaf(q0[r], kf0, q1[r] * kf1);
+        const float sp = head_sums8(d, lane) * kInvSqrt128;
+        if ((lane & 7) == 0) sp_sh[lane >> 3] = sp;
     }
-    __syncthreads();  // qs / vs complete (waits on LDS only: the K/V stream stays in flight)
+    __syncthreads();  // qhl / vs / sp_sh complete (waits on LDS only: the page stream stays in flight)
 
     // B operand of S^T = K q^T: head column n is head n % 8, its hi (n < 8) or lo (n >= 8) half;
-    // k-step ks of lane group g covers dims 32 g + 8 ks .. +8
+    // k-step ks of lane group g covers dims 32 ks + 8 g .. +8 (16 bytes of LDS)
     bf16x8 qop[4];
-    {
-        const uint32_t r = n & 7;
-        const bool hi = n < 8;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const float *qq = &qs[r][32 * g + 8 * ks];
-            u32x4 w;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float a0 = qq[2 * j], a1 = qq[2 * j + 1];
-                const uint32_t b0 = hi ? bf16_split_hi(a0) : bf16_split_lo(a0);
-                const uint32_t b1 = hi ? bf16_split_hi(a1) : bf16_split_lo(a1);
-                w[j] = b0 | (b1 << 16);
-            }
-            qop[ks] = as_bf16x8(w);
-        }
-    }
+    for (int ks = 0; ks < 4; ++ks)
+        qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[n >> 3][n & 7][32 * ks + 8 * g]));
 
-    float m_l = -INFINITY, l_l = 0.f;  // online-softmax state of head n % 8
+    float m_l = -INFINITY, l_l = 0.f;
     f32x4 O[8];
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t t = t_begin; t < t_end; ++t) {
-        if (t != t_begin) dattn_load(a, h, t, lane, T);
-        const uint32_t tok0 = t * kAttnTile;
-        float sc[4][4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[b][ks]), qop[ks], acc, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float full = acc[i] + dpp_f32<DPP_ROR8>(acc[i]);  // hi + lo columns
-                const uint32_t tok = tok0 + tile_token(b, 4 * g + i);
-                sc[b][i] = tok < pos ? full * kInvSqrt128 : -INFINITY;
-            }
+    if (p_begin + 1 == p_end) {
+        dattn_page<true>(T, qop, p_begin * kDattnPage, pos, g, n, m_l, l_l, O);
+    } else if (p_begin < p_end) {
+        // each page computed with the next page's loads in flight
+        DattnPage nx;
+        dattn_load(a, h, p_begin + 1, lane, nx);
+        dattn_page<true>(T, qop, p_begin * kDattnPage, pos, g, n, m_l, l_l, O);
+        T = nx;
+        uint32_t p = p_begin + 1;
+        for (; p + 1 < p_end; ++p) {
+            dattn_load(a, h, p + 1, lane, nx);
+            dattn_page<false>(T, qop, p * kDattnPage, pos, g, n, m_l, l_l, O);
+            T = nx;
         }
-        float mx = sc[0][0];
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[b][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_l, mx);
-        const float alpha = expf(m_l - m_new);
-        float pr[4][4];
-        float psum = 0.f;
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pr[b][i] = expf(sc[b][i] - m_new);
-                psum += pr[b][i];
-            }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
-        l_l = l_l * alpha + psum;
-        m_l = m_new;
-        // rescale the accumulators: rows 4 g + i hold head (4 g + i) % 8, whose alpha lane
-        // (4 g + i) % 8 holds
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float ai = __shfl(alpha, (4 * g + i) & 7, 64);
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
-        }
-        // A operand of O = P V: row n = head n % 8, its hi or lo half; k = 8 g + j is token
-        // 16 g + 8 p + j of the tile (blocks 2p and 2p + 1 of the scores)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            u32x4 w;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float a0 = j < 2 ? pr[2 * p][2 * j] : pr[2 * p + 1][2 * j - 4];
-                const float a1 = j < 2 ? pr[2 * p][2 * j + 1] : pr[2 * p + 1][2 * j - 3];
-                const uint32_t b0 = n < 8 ? bf16_split_hi(a0) : bf16_split_lo(a0);
-                const uint32_t b1 = n < 8 ? bf16_split_hi(a1) : bf16_split_lo(a1);
-                w[j] = b0 | (b1 << 16);
-            }
-            const bf16x8 pop = as_bf16x8(w);
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb)
-                O[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, as_bf16x8(T.v[p][nb]), O[nb], 0, 0, 0);
-        }
+        dattn_page<false>(T, qop, p * kDattnPage, pos, g, n, m_l, l_l, O);
     }
-    // hi rows (lane groups 0, 1) + lo rows (groups 2, 3)
+    // Output. Row 4 g + i holds the hi half of head 4 g + i for g < 2 and the lo half for g >= 2,
+    // so a pair sum over lanes {l, l ^ 32} gives the full value; one swap serves two accumulators:
+    // lanes 0-31 get O[nb] (head 4 g + i, dims 16 nb + n), lanes 32-63 get O[nb + 4] (head
+    // 4 (g - 2) + i, dims 16 (nb + 4) + n), so every lane stores 16 values.
+    const uint32_t hg = g & 1, nb_off = (g >> 1) * 4;
+    float ov[4][4];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
+    for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) O[nb][i] += __shfl_xor(O[nb][i], 32, 64);
+        for (int i = 0; i < 4; ++i) ov[nb][i] = pair_sum<32>(O[nb][i], O[nb + 4][i]);
     if (s == 0) {
-        // this token: one more online-softmax step with score spos and value vs, done per head
-        // column (lane n holds head n % 8) and gathered into the accumulator rows
-        __shared__ float sp_sh[8];
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < 8; ++r) sp_sh[r] = spos[r];
-        }
-        __syncthreads();
+        // this token: one more online-softmax step with score sp and value vs; lane n of every
+        // row holds head n % 8's state, so the head of row i is gathered by readlane
         const float sp = sp_sh[n & 7];
         const float m_new = fmaxf(m_l, sp);
         const float aold = expf(m_l - m_new);
@@ -267,20 +256,20 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         m_l = m_new;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float ai = __shfl(aold, (4 * g + i) & 7, 64);
-            const float pi = __shfl(pnow, (4 * g + i) & 7, 64);
+            const float a_lo = readlane_f32(aold, i), a_hi = readlane_f32(aold, 4 + i);
+            const float p_lo = readlane_f32(pnow, i), p_hi = readlane_f32(pnow, 4 + i);
+            const float ai = hg ? a_hi : a_lo;
+            const float pi = hg ? p_hi : p_lo;
 #pragma unroll
-            for (int nb = 0; nb < 8; ++nb) O[nb][i] = fmaf(pi, vs[16 * nb + n], O[nb][i] * ai);
+            for (int nb = 0; nb < 4; ++nb) ov[nb][i] = fmaf(pi, vs[16 * (nb + nb_off) + n], ov[nb][i] * ai);
         }
     }
     float *part = a.part + ((size_t)h * 8 * kDattnSplits + s) * kPartStride;
-    if (g < 2) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float *pp = part + (size_t)(4 * g + i) * kDattnSplits * kPartStride;
+    for (int i = 0; i < 4; ++i) {
+        float *pp = part + (size_t)(4 * hg + i) * kDattnSplits * kPartStride;
 #pragma unroll
-            for (int nb = 0; nb < 8; ++nb) pp[4 + 16 * nb + n] = O[nb][i];
-        }
+        for (int nb = 0; nb < 4; ++nb) pp[4 + 16 * (nb + nb_off) + n] = ov[nb][i];
     }
     if (lane < 8) {  // lane r holds head r's running max and sum
         float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
@@ -290,7 +279,7 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_dattn, dim3(kDattnSplits, 4), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_dattn, dim3(4, kDattnSplits), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -419,64 +408,52 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 // ------------------------------------------------------------------------ split combine
 // Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l); fused partials are
 // dims in order. Either way partial dim d sits at 4 + d, so one combine serves both.
+// One wavefront per (seq, q head, quarter of the dims): lane l covers dim 32 q + l % 32 of the
+// slots of parity l / 32, so a workgroup reads 8 KiB of partials (a CU's loads share one queue).
 __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
-    __shared__ float wsh[64];
-    const uint32_t head = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    uint32_t tiles;
-    if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + kAttnTile - 1) / kAttnTile;
-    else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + kAttnTile - 1) / kAttnTile;
-    uint32_t active, tps;
-    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= 64
+    __shared__ float wsh[kDattnSplits];
+    const uint32_t head = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y, lane = threadIdx.x;
+    const uint32_t d = 32 * quarter + (lane & 31), half = lane >> 5;
     const float *pp = a.part + ((size_t)b * a.qh + head) * a.splits * kPartStride;
-    // lane s holds split s's (m, l); the first 16 splits' o rows are loaded with them, so a
-    // short context costs one round trip
-    const bool mine = lane < active;
-    const float m = mine ? *as_global_f32(pp + lane * kPartStride) : -INFINITY;
-    const float l = mine ? *as_global_f32(pp + lane * kPartStride + 1) : 0.f;
-    constexpr uint32_t kFirst = 16;
-    float f0[kFirst], f1[kFirst];
+    // Every slot's (m, l) and o values are loaded before the split count is known (the stale
+    // slots past it are dropped below), so the context length and the partials share one round
+    // trip.
+    const uint32_t mslot = min(lane, a.splits - 1);
+    const float m_raw = *as_global_f32(pp + mslot * kPartStride);
+    const float l_raw = *as_global_f32(pp + mslot * kPartStride + 1);
+    constexpr uint32_t kPer = kDattnSplits / 2;
+    float f[kPer];
 #pragma unroll
-    for (uint32_t j = 0; j < kFirst; ++j) {
-        const bool ok = j < active;
-        f0[j] = ok ? *as_global_f32(pp + j * kPartStride + 4 + lane) : 0.f;
-        f1[j] = ok ? *as_global_f32(pp + j * kPartStride + 68 + lane) : 0.f;
-    }
+    for (uint32_t k = 0; k < kPer; ++k)
+        f[k] = *as_global_f32(pp + min(2 * k + half, a.splits - 1) * kPartStride + 4 + d);
+    uint32_t tiles;
+    if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + a.tile_tokens - 1) / a.tile_tokens;
+    else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + a.tile_tokens - 1) / a.tile_tokens;
+    uint32_t active, tps;
+    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= splits <= 64
+    // lane s holds split s's (m, l)
+    const bool mine = lane < active;
+    const float m = mine ? m_raw : -INFINITY;
+    const float l = mine ? l_raw : 0.f;
     float M = row16_max(m);
     M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
     const float w = mine ? (a.mutant == 4 ? 1.0f : expf(m - M)) : 0.f;
     const float L = wave_sum(w * l);
     wsh[lane] = w;
     __syncthreads();
-    float O0 = 0.f, O1 = 0.f;
+    // slots past `active` are selected out, not weighted by 0 (their contents may not be finite)
+    float O = 0.f;
 #pragma unroll
-    for (uint32_t j = 0; j < kFirst; ++j) {
-        O0 = fmaf(f0[j], wsh[j], O0);
-        O1 = fmaf(f1[j], wsh[j], O1);
+    for (uint32_t k = 0; k < kPer; ++k) {
+        const uint32_t j = 2 * k + half;
+        O = j < active ? fmaf(f[k], wsh[j], O) : O;
     }
-    for (uint32_t s0 = kFirst; s0 < active; s0 += 8) {
-        float o0[8], o1[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const bool ok = s0 + j < active;
-            const float *q = pp + (size_t)(s0 + j) * kPartStride;
-            o0[j] = ok ? *as_global_f32(q + 4 + lane) : 0.f;
-            o1[j] = ok ? *as_global_f32(q + 68 + lane) : 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (s0 + j >= active) break;
-            O0 = fmaf(o0[j], wsh[s0 + j], O0);
-            O1 = fmaf(o1[j], wsh[s0 + j], O1);
-        }
-    }
-    const float inv = a.out_scale / L;
-    float *op = a.out + ((size_t)b * a.qh + head) * 128;
-    op[lane] = O0 * inv;
-    op[lane + 64] = O1 * inv;
+    O = xor_sum<32>(O);  // even + odd slots
+    if (lane < 32) a.out[((size_t)b * a.qh + head) * 128 + d] = O * (a.out_scale / L);
 }
 
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_attn_combine, dim3(a.qh, a.seqs), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_attn_combine, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -541,7 +518,7 @@ DattnArgs cache_dattn(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, con
     a.rope_cos = c->rope_cos;
     a.rope_sin = c->rope_sin;
     a.eps = eps;
-    a.tiles_per_split = knobs().dattn_per_split / kAttnTile;
+    a.tiles_per_split = knobs().dattn_per_split / kDattnPage;
     a.part = part;
     a.mutant = knobs().dattn_mutant;
     return a;
@@ -666,6 +643,7 @@ int omega_gpu_decode_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t p
     cb.splits = kDattnSplits;
     cb.pos_host = pos;
     cb.tiles_per_split = a.tiles_per_split;
+    cb.tile_tokens = kDattnPage;
     cb.qh = 32;
     cb.out_scale = out_scale;
     cb.out = c->out;
@@ -679,15 +657,15 @@ int omega_gpu_decode_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t p
     memcpy(out, cx->pin, 4096 * 4);
     if (info) {
         uint32_t active, tps;
-        attn_split_plan((pos + kAttnTile - 1) / kAttnTile, kDattnSplits, a.tiles_per_split, active, tps);
+        attn_split_plan((pos + kDattnPage - 1) / kDattnPage, kDattnSplits, a.tiles_per_split, active, tps);
         memset(info, 0, sizeof(*info));
         info->layer = layer;
         info->pos = pos;
         info->splits = active;
-        info->per_split = tps * kAttnTile;
+        info->per_split = tps * kDattnPage;
         info->depth = 32;
-        info->grid_x = kDattnSplits;
-        info->grid_y = 4;
+        info->grid_x = 4;
+        info->grid_y = kDattnSplits;
         info->threads = 64;
         info->kv_bytes = 2ull * 4 * (pos + 1) * 256;
         info->elapsed_ns = event_ns(cx);

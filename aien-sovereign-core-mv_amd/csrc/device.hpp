@@ -113,6 +113,80 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
 }
 
+// ------------------------------------------------------------------ cross-row exchanges
+// gfx950's row swaps move data between 16-lane rows (v_permlane16_swap: rows 0<->1, 2<->3) or
+// halves (v_permlane32_swap) on the VALU, where __shfl would take an LDS round trip. swap32(x, y)
+// returns r0 = (x of lanes 0-31 | y of lanes 0-31) and r1 = (x of lanes 32-63 | y of lanes
+// 32-63); swap16 does the same per pair of rows. So with x = y = v, r0 + r1 is v + v[lane ^ 32]
+// (v[lane ^ 16]) in every lane, bitwise the same in both lanes of a pair (the two operands are
+// the same, in either order); with x, y two different values, lanes 0-31 get x summed over the
+// pair and lanes 32-63 get y summed over the pair.
+__device__ __forceinline__ void swap32(uint32_t x, uint32_t y, uint32_t &r0, uint32_t &r1) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    r0 = r[0];
+    r1 = r[1];
+}
+__device__ __forceinline__ void swap16(uint32_t x, uint32_t y, uint32_t &r0, uint32_t &r1) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    r0 = r[0];
+    r1 = r[1];
+}
+template <int W>
+__device__ __forceinline__ void swapw(uint32_t x, uint32_t y, uint32_t &r0, uint32_t &r1) {
+    if (W == 32) swap32(x, y, r0, r1);
+    else swap16(x, y, r0, r1);
+}
+// x summed over lanes {l, l ^ W} in the lower lane of each pair, y in the upper (W = 16, 32)
+template <int W>
+__device__ __forceinline__ float pair_sum(float x, float y) {
+    uint32_t r0, r1;
+    swapw<W>(__float_as_uint(x), __float_as_uint(y), r0, r1);
+    return __uint_as_float(r0) + __uint_as_float(r1);
+}
+template <int W>
+__device__ __forceinline__ double pair_sum(double x, double y) {
+    const uint64_t bx = (uint64_t)__double_as_longlong(x), by = (uint64_t)__double_as_longlong(y);
+    uint32_t l0, l1, h0, h1;
+    swapw<W>((uint32_t)bx, (uint32_t)by, l0, l1);
+    swapw<W>((uint32_t)(bx >> 32), (uint32_t)(by >> 32), h0, h1);
+    return __longlong_as_double((long long)(((uint64_t)h0 << 32) | l0)) +
+           __longlong_as_double((long long)(((uint64_t)h1 << 32) | l1));
+}
+template <int W>
+__device__ __forceinline__ float xor_sum(float v) { return pair_sum<W>(v, v); }
+template <int W>
+__device__ __forceinline__ float xor_max(float v) {
+    uint32_t r0, r1;
+    swapw<W>(__float_as_uint(v), __float_as_uint(v), r0, r1);
+    return fmaxf(__uint_as_float(r0), __uint_as_float(r1));
+}
+
+// Eight per-head values summed over the wavefront by one transposed reduction: lane l ends with
+// the total of head l / 8. Three halving exchanges (lanes ^32, ^16, ^8) each keep half of the
+// heads, then the 8 lanes of a head add up by DPP; every lane of a head holds the same bits.
+template <typename T>
+__device__ __forceinline__ T head_sums8(const T (&v)[8], uint32_t lane) {
+    T t4[4], t2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t4[i] = pair_sum<32>(v[i], v[i + 4]);     // heads 4 b5 + i
+#pragma unroll
+    for (int i = 0; i < 2; ++i) t2[i] = pair_sum<16>(t4[i], t4[i + 2]);   // heads 4 b5 + 2 b4 + i
+    const bool b3 = (lane >> 3) & 1;
+    T t;
+    if constexpr (sizeof(T) == 8) {
+        t = (b3 ? t2[1] : t2[0]) + dpp_f64<DPP_ROR8>(b3 ? t2[0] : t2[1]);
+        t += dpp_f64<DPP_XOR1>(t);
+        t += dpp_f64<DPP_XOR2>(t);
+        t += dpp_f64<DPP_HALF_MIRROR>(t);
+    } else {
+        t = (b3 ? t2[1] : t2[0]) + dpp_f32<DPP_ROR8>(b3 ? t2[0] : t2[1]);
+        t += dpp_f32<DPP_XOR1>(t);
+        t += dpp_f32<DPP_XOR2>(t);
+        t += dpp_f32<DPP_HALF_MIRROR>(t);
+    }
+    return t;
+}
+
 // ------------------------------------------------------------------ widening dot products
 // 16 e4m3 bytes (one lane's 16 B) times 16 activations; the native OCP-fp8 convert.
 __device__ __forceinline__ void dot4_fp8(uint32_t w, const float *xx, float &p) {

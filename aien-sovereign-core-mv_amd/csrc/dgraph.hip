@@ -290,6 +290,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         cb.splits = kDattnSplits;
         cb.pos_dev = pos_dev;
         cb.tiles_per_split = da.tiles_per_split;
+        cb.tile_tokens = kDattnPage;
         cb.qh = 32;
         cb.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
         cb.out = g->attn;

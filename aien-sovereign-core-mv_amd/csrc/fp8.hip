@@ -42,7 +42,9 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     using S = Fp8Slab<K, RPW>;
     constexpr int P = S::P;
     const uint32_t lane = lane_id();
-    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (scalar registers): the group's weight pointer then comes from a scalar
+    // kernel-argument load instead of a vector round trip ahead of the weight stream
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const uint32_t per_group = a.n / RPW;
     if (wave >= a.groups * per_group) return;
     const uint32_t g = wave / per_group, row0 = (wave % per_group) * RPW;
@@ -50,7 +52,9 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     const float *sexp;
     group_tensor(a, g, K, wexp, sexp);
 
-    // activation phases (and norm weights) first: their loads go ahead of the weight stream
+    // every small load (activation phases, norm weights, block scales) goes ahead of the weight
+    // stream: vector-memory waits complete in issue order, so waiting on any of them then never
+    // waits on the weights
     float xr[P][16];
     float nw[P][16];
     if (XSRC == XS_EMBED_NORM) {
@@ -60,14 +64,17 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
         S::load_x(a.x + (size_t)g * a.x_stride, lane, xr);
     }
     if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
+    float sc[P];
+    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc);
     S slab;
     slab.load(wexp + (size_t)row0 * K, lane);
-    float sc[P];
-    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, a.x_scale, a.mutant, sc);
+    // every load is issued before any arithmetic (the scheduler would otherwise sink the weight
+    // loads between the dots, one round trip each)
+    __builtin_amdgcn_sched_barrier(0);
 
     // RMSNorm is one scale per row: dot with x * w and scale the row sums at the end, so the
     // f64 sum of squares runs beside the weight stream instead of ahead of it
-    float scale = 1.0f;
+    float scale = a.x_scale;
     if (XSRC != XS_F32) {
         static_assert(XSRC == XS_F32 || P * 16 * 64 == K, "the phases must partition the row");
         if (XSRC == XS_EMBED_NORM && blockIdx.x == 0 && threadIdx.x < 64) {
@@ -84,7 +91,7 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
         for (int ph = 0; ph < P; ++ph)
 #pragma unroll
             for (int i = 0; i < 16; ++i) xr[ph][i] = xr[ph][i] * nw[ph][i];
-        scale = rms_scale(ss, K, a.eps);
+        scale *= rms_scale(ss, K, a.eps);
     }
     float acc[RPW];
 #pragma unroll
@@ -104,7 +111,7 @@ constexpr uint32_t kAnyRows = 8;
 
 __global__ __launch_bounds__(256) void k_fp8_rows_any(const Fp8RowsArgs a, uint32_t rpw) {
     const uint32_t lane = lane_id();
-    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const uint32_t per_group = a.n / rpw;
     if (wave >= a.groups * per_group) return;
     const uint32_t g = wave / per_group, row0 = (wave % per_group) * rpw;

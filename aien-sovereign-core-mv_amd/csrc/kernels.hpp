@@ -35,7 +35,7 @@ struct Fp8RowsArgs {
     const uint64_t *tab = nullptr;  // device group table {w_va, s_va} x groups, or null
     const float *x = nullptr;
     uint32_t x_stride = 0;
-    float x_scale = 1.0f;           // folded into the block scales (exact power of two)
+    float x_scale = 1.0f;           // applied to the row sums (exact power of two)
     const float *norm_w = nullptr;
     float eps = 1e-6f;
     const uint16_t *embed = nullptr;     // XS_EMBED_NORM
@@ -103,7 +103,8 @@ hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st);
 hipError_t launch_router_topk(const RouterArgs &a, hipStream_t st);
 
 // ---------------------------------------------------------------- attention
-constexpr uint32_t kAttnTile = 64;       // tokens per tile (one wavefront)
+constexpr uint32_t kAttnTile = 64;       // tokens per tile of the paged kernel (one wavefront)
+constexpr uint32_t kDattnPage = 16;      // tokens per split unit of the fused kernel (one page)
 constexpr uint32_t kDattnSplits = 64;    // split workgroups per kv head of the fused kernel
 constexpr uint32_t kPartStride = 132;    // floats per (head, split) partial: m, l, -, -, o[128]
 
@@ -135,7 +136,7 @@ struct DattnArgs {
     float eps = 1e-6f;
     const uint32_t *pos_dev = nullptr;
     uint32_t pos_host = 0;
-    uint32_t tiles_per_split = 0;    // 0: spread over every split
+    uint32_t tiles_per_split = 0;    // pages per split; 0: spread over every split
     float *part = nullptr;           // [32][kDattnSplits][kPartStride]
     int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written
 };
@@ -166,6 +167,7 @@ struct CombineArgs {
     const uint32_t *pos_dev = nullptr;      // fused: tiles before pos, plus the token itself
     uint32_t pos_host = 0;
     uint32_t tiles_per_split = 0;           // as the fused kernel's
+    uint32_t tile_tokens = kAttnTile;       // tokens per split unit (kDattnPage for the fused kernel)
     const int32_t *context_lens = nullptr;  // paged: tiles of the context
     uint32_t seqs = 1, qh = 32;
     float out_scale = 1.0f;

@@ -8,8 +8,8 @@
 //
 // Each candidate becomes one 64-bit key, (total-order value << 32) | ~id, whose unsigned maximum
 // is the next pick (larger logit first, then the lower id). A round is one 64-bit max inside
-// every 16-lane row (DPP), two cross-row exchanges and a mask of the pick, so the 8 rounds stay
-// a few hundred instructions; every lane ends with the same result.
+// every 16-lane row (DPP), two cross-row row swaps and a mask of the pick, all on the VALU, so
+// the 8 rounds stay a few hundred instructions; every lane ends with the same result.
 #pragma once
 
 #include "device.hpp"
@@ -41,10 +41,14 @@ __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
     const uint32_t hi = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)(v >> 32));
     return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
-    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
-    return ((uint64_t)hi << 32) | lo;
+// max of the key in lanes {l, l ^ W} (W = 16, 32) by row swaps: r0 of both dword swaps is the
+// lower lane's key, r1 the upper lane's
+template <int W>
+__device__ __forceinline__ uint64_t xor_max_u64(uint64_t v) {
+    uint32_t l0, l1, h0, h1;
+    swapw<W>((uint32_t)v, (uint32_t)v, l0, l1);
+    swapw<W>((uint32_t)(v >> 32), (uint32_t)(v >> 32), h0, h1);
+    return max_u64(((uint64_t)h0 << 32) | l0, ((uint64_t)h1 << 32) | l1);
 }
 // the maximum over the wavefront, in every lane
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t b) {
@@ -52,8 +56,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t b) {
     b = max_u64(b, dpp_u64<DPP_XOR2>(b));
     b = max_u64(b, dpp_u64<DPP_HALF_MIRROR>(b));
     b = max_u64(b, dpp_u64<DPP_MIRROR>(b));
-    b = max_u64(b, shfl_xor_u64(b, 16));
-    return max_u64(b, shfl_xor_u64(b, 32));
+    b = xor_max_u64<16>(b);
+    return xor_max_u64<32>(b);
 }
 
 // logits: Q * 64 expert values (+1 shared) in global memory.

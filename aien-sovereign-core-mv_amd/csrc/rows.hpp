@@ -95,14 +95,16 @@ struct Fp8Slab : Slab<K, RPW> {
             }
         }
     }
-    // scale of each phase for the rows' 128-row block: srow[col / 128] * x_scale
+    // scale of each phase for the rows' 128-row block: srow[col / 128] * x_scale. The loads are
+    // unconditional (the test mutants select after them): a conditional load would leave a
+    // branch join whose conservative wait covers every load issued before it.
     __device__ static void load_scales(const float *srow, uint32_t lane, float x_scale, int mutant,
                                        float (&sc)[P]) {
 #pragma unroll
         for (int ph = 0; ph < P; ++ph) {
             const uint32_t cb = mutant == 2 ? 0u : B::col_bytes(ph, lane) / 128u;
-            const float s = mutant == 1 ? 1.0f : *as_global_f32(srow + cb);
-            sc[ph] = s * x_scale;
+            const float s = *as_global_f32(srow + cb);
+            sc[ph] = (mutant == 1 ? 1.0f : s) * x_scale;
         }
     }
     __device__ __forceinline__ void dot(const float (&xr)[P][16], const float (&sc)[P],
