@@ -89,12 +89,14 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     const uint32_t e = sh_id[slot];
     const uint8_t *we = a.w + (size_t)e * 2 * kInter * kHidden;
     const float *se = a.s + (size_t)e * (2 * kInter / 128) * (kHidden / 128);
-    S gate, up;
-    gate.load(we + (size_t)j0 * kHidden, lane);
-    up.load(we + (size_t)(kInter + j0) * kHidden, lane);
+    // block scales ahead of the weight stream: waits complete in issue order
     float scg[P], scu[P];
     S::load_scales(se + (size_t)(j0 >> 7) * (kHidden / 128), lane, 1.0f, 0, scg);
     S::load_scales(se + (size_t)((kInter + j0) >> 7) * (kHidden / 128), lane, 1.0f, 0, scu);
+    S gate, up;
+    gate.load(we + (size_t)j0 * kHidden, lane);
+    up.load(we + (size_t)(kInter + j0) * kHidden, lane);
+    __builtin_amdgcn_sched_barrier(0);
     // workgroup 0 publishes the route once its own weight stream is in flight
     if (blockIdx.x == 0 && wid == 0 && lane < (uint32_t)kTopK) {
         const uint32_t id = sh_id[lane];
@@ -142,15 +144,25 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
     using S = Fp8Slab<kInter, kDnRows>;
     constexpr int P = S::P;
     __shared__ float red[kTopK][kDnRows];
-    const uint32_t lane = lane_id(), slot = threadIdx.x >> 6;
+    const uint32_t lane = lane_id();
+    const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: e by s_load
     const uint32_t row0 = blockIdx.x * kDnRows;
+    int graph_mutant = a.graph_mutant;
+    asm volatile("" : "+s"(graph_mutant));  // read with the other arguments, not after the dot
+    // every small load goes ahead of the weight stream (the route weights and the residual rows
+    // of the epilogue included), so no round trip is left after the dot
+    const uint32_t e = a.ids[slot];
     float xr[P][16];
     S::load_x(a.act + slot * kInter, lane, xr);
-    const uint32_t e = *as_global_u32(a.ids + slot);
-    S slab;
-    slab.load(a.w + ((size_t)e * kHidden + row0) * kInter, lane);
+    const float wraw = *as_global_f32(a.weights + (lane & (kTopK - 1)));  // lane s: slot s's weight
+    const float xres = *as_global_f32(a.x + row0 + (lane & (kDnRows - 1)));
     float sc[P];
     S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f, 0, sc);
+    S slab;
+    slab.load(a.w + ((size_t)e * kHidden + row0) * kInter, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // graph mutant 2 drops slot 7 from the combine (decided here, not after the dot)
+    const float wgt = (graph_mutant == 2 && (lane & (kTopK - 1)) == 7) ? 0.f : wraw;
     float acc[kDnRows];
 #pragma unroll
     for (uint32_t j = 0; j < kDnRows; ++j) acc[j] = 0.f;
@@ -162,10 +174,9 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
         float moe = 0.f;
 #pragma unroll
         for (int s = 0; s < kTopK; ++s) {
-            const float wgt = (a.graph_mutant == 2 && s == 7) ? 0.f : *as_global_f32(a.weights + s);
-            moe += wgt * red[s][threadIdx.x];
+            moe += readlane_f32(wgt, s) * red[s][threadIdx.x];
         }
-        a.x[row0 + threadIdx.x] += moe;
+        a.x[row0 + threadIdx.x] = xres + moe;
     }
 }
 

@@ -66,6 +66,9 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
     float sc[P];
     S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc);
+    // the residual row of the epilogue, read now rather than after the dot
+    const size_t yrow = (size_t)g * a.n + row0 + (lane & (RPW - 1));
+    const float yres = EPI == EPI_RESID ? *as_global_f32(a.y + yrow) : 0.f;
     S slab;
     slab.load(wexp + (size_t)row0 * K, lane);
     // every load is issued before any arithmetic (the scheduler would otherwise sink the weight
@@ -98,11 +101,7 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
     slab.dot(xr, sc, acc, lane);
     const float v = reduce_rows(acc, lane) * scale;
-    if (lane < (uint32_t)RPW) {
-        const size_t row = (size_t)g * a.n + row0 + lane;
-        if (EPI == EPI_STORE) a.y[row] = v;
-        else a.y[row] += v;
-    }
+    if (lane < (uint32_t)RPW) a.y[yrow] = EPI == EPI_STORE ? v : yres + v;
 }
 
 // Any k (a multiple of 128 up to 32768): rows per wavefront rpw = 1024 / gcd(k, 1024) <= 8,
