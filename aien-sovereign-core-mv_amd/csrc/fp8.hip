@@ -64,10 +64,13 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
         S::load_x(a.x + (size_t)g * a.x_stride, lane, xr);
     }
     if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
-    float sc[P];
-    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc);
+    // block scales of row0's 128-row block, and of the last row's when RPW does not divide 128
+    float sc[2][P];
+    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc[0]);
+    if constexpr (!S::kOneBlock)
+        S::load_scales(sexp + (size_t)((row0 + RPW - 1) >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc[1]);
     // the residual row of the epilogue, read now rather than after the dot
-    const size_t yrow = (size_t)g * a.n + row0 + (lane & (RPW - 1));
+    const size_t yrow = (size_t)g * a.n + row0 + min(lane, (uint32_t)RPW - 1);
     const float yres = EPI == EPI_RESID ? *as_global_f32(a.y + yrow) : 0.f;
     S slab;
     slab.load(wexp + (size_t)row0 * K, lane);
@@ -99,7 +102,8 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     float acc[RPW];
 #pragma unroll
     for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
-    slab.dot(xr, sc, acc, lane);
+    if constexpr (S::kOneBlock) slab.dot(xr, sc[0], acc, lane);
+    else slab.dot2(xr, sc, row0, acc);
     const float v = reduce_rows(acc, lane) * scale;
     if (lane < (uint32_t)RPW) a.y[yrow] = EPI == EPI_STORE ? v : yres + v;
 }
@@ -180,7 +184,8 @@ uint32_t fp8_rows_blocks(const Fp8RowsArgs &a) {
 
 template <int K, int RPW, int EPI, int XSRC>
 static hipError_t launch_k(const Fp8RowsArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC>), dim3(fp8_rows_blocks(a)), dim3(256), 0, st, a);
+    const uint32_t waves = a.groups * (a.n / RPW);
+    OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -197,8 +202,14 @@ hipError_t launch_fp8_rows(const Fp8RowsArgs &a, int epi, int xsrc, hipStream_t 
             return hipGetLastError();
         }
     }
-    if (epi == EPI_STORE && xsrc == XS_NORM) return launch_k<2048, 4, EPI_STORE, XS_NORM>(a, st);
-    if (epi == EPI_STORE && xsrc == XS_EMBED_NORM) return launch_k<2048, 4, EPI_STORE, XS_EMBED_NORM>(a, st);
+    // the normed GEMVs are the q|k|v projection (n = 5120): 5 rows per wavefront make 1024
+    // wavefronts, one per SIMD, where 4 rows would leave a quarter of the SIMDs with two
+    if (epi == EPI_STORE && xsrc == XS_NORM)
+        return a.n % 5 == 0 && a.groups == 1 ? launch_k<2048, 5, EPI_STORE, XS_NORM>(a, st)
+                                              : launch_k<2048, 4, EPI_STORE, XS_NORM>(a, st);
+    if (epi == EPI_STORE && xsrc == XS_EMBED_NORM)
+        return a.n % 5 == 0 && a.groups == 1 ? launch_k<2048, 5, EPI_STORE, XS_EMBED_NORM>(a, st)
+                                              : launch_k<2048, 4, EPI_STORE, XS_EMBED_NORM>(a, st);
     if (epi == EPI_RESID && xsrc == XS_F32 && a.k == 4096) return launch_k<4096, 2, EPI_RESID, XS_F32>(a, st);
     return hipErrorInvalidValue;
 }

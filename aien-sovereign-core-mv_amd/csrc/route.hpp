@@ -6,10 +6,12 @@
 // the lower id; weight = exp(l - max) / sum over the selected of exp(l - max) (norm_topk), or
 // over every expert; the optional shared expert takes the last slot with sigmoid(logit).
 //
-// Each candidate becomes one 64-bit key, (total-order value << 32) | ~id, whose unsigned maximum
-// is the next pick (larger logit first, then the lower id). A round is one 64-bit max inside
-// every 16-lane row (DPP), two cross-row row swaps and a mask of the pick, all on the VALU, so
-// the 8 rounds stay a few hundred instructions; every lane ends with the same result.
+// Each candidate becomes its 32-bit total-order key (unsigned order = the float total order).
+// A round takes the wavefront maximum of the keys (DPP inside 16-lane rows, then two row swaps,
+// all on the VALU) and the lowest expert id holding it (a ballot of the lanes equal to the
+// maximum): exactly the order "larger logit first, then the lower id". The pick's key is then
+// cleared to 0, below every real key, and the 8 rounds stay about 20 instructions each; every
+// lane ends with the same result.
 #pragma once
 
 #include "device.hpp"
@@ -30,34 +32,21 @@ __device__ __forceinline__ int32_t total_key(float f) {
 __device__ __forceinline__ float key_value(int32_t k) {
     return __int_as_float(k < 0 ? (k ^ 0x7fffffff) : k);
 }
-__device__ __forceinline__ uint64_t route_key(float v, uint32_t id) {
-    const uint32_t ord = (uint32_t)total_key(v) ^ 0x80000000u;
-    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - id);
-}
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-    const uint32_t lo = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)v);
-    const uint32_t hi = (uint32_t)dpp_i32<CTRL>((int)(uint32_t)(v >> 32));
-    return ((uint64_t)hi << 32) | lo;
-}
-// max of the key in lanes {l, l ^ W} (W = 16, 32) by row swaps: r0 of both dword swaps is the
-// lower lane's key, r1 the upper lane's
+__device__ __forceinline__ uint32_t ord_key(float v) { return (uint32_t)total_key(v) ^ 0x80000000u; }
 template <int W>
-__device__ __forceinline__ uint64_t xor_max_u64(uint64_t v) {
-    uint32_t l0, l1, h0, h1;
-    swapw<W>((uint32_t)v, (uint32_t)v, l0, l1);
-    swapw<W>((uint32_t)(v >> 32), (uint32_t)(v >> 32), h0, h1);
-    return max_u64(((uint64_t)h0 << 32) | l0, ((uint64_t)h1 << 32) | l1);
+__device__ __forceinline__ uint32_t xor_max_u32(uint32_t v) {
+    uint32_t r0, r1;
+    swapw<W>(v, v, r0, r1);
+    return r0 > r1 ? r0 : r1;
 }
 // the maximum over the wavefront, in every lane
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t b) {
-    b = max_u64(b, dpp_u64<DPP_XOR1>(b));
-    b = max_u64(b, dpp_u64<DPP_XOR2>(b));
-    b = max_u64(b, dpp_u64<DPP_HALF_MIRROR>(b));
-    b = max_u64(b, dpp_u64<DPP_MIRROR>(b));
-    b = xor_max_u64<16>(b);
-    return xor_max_u64<32>(b);
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i32<DPP_XOR1>((int)v));
+    v = max(v, (uint32_t)dpp_i32<DPP_XOR2>((int)v));
+    v = max(v, (uint32_t)dpp_i32<DPP_HALF_MIRROR>((int)v));
+    v = max(v, (uint32_t)dpp_i32<DPP_MIRROR>((int)v));
+    v = xor_max_u32<16>(v);
+    return xor_max_u32<32>(v);
 }
 
 // logits: Q * 64 expert values (+1 shared) in global memory.
@@ -67,23 +56,29 @@ __device__ __forceinline__ void route_topk(const float *logits, uint32_t shared,
                                            int mutant, Route &r) {
     constexpr uint32_t experts = 64 * Q;
     const uint32_t lane = lane_id();
-    uint64_t pk[Q];
+    uint32_t k[Q];  // expert lane + 64 q
 #pragma unroll
-    for (int q = 0; q < Q; ++q) pk[q] = route_key(*as_global_f32(logits + lane + 64 * q), lane + 64 * q);
+    for (int q = 0; q < Q; ++q) k[q] = ord_key(*as_global_f32(logits + lane + 64 * q));
     float v[kTopK];
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
-        uint64_t b = pk[0];
+        uint32_t m = k[0];
 #pragma unroll
-        for (int q = 1; q < Q; ++q) b = max_u64(b, pk[q]);
-        b = wave_max_u64(b);
-        const uint32_t id = 0xffffffffu - (uint32_t)b;
+        for (int q = 1; q < Q; ++q) m = max(m, k[q]);
+        m = wave_max_u32(m);
+        // the lowest id whose key is the maximum: quarter q holds ids 64 q .. 64 q + 63
+        uint32_t id = 0xffffffffu;
+#pragma unroll
+        for (int q = Q - 1; q >= 0; --q) {
+            const uint64_t b = __ballot(k[q] == m);
+            if (b) id = 64 * q + (uint32_t)(__ffsll((long long)b) - 1);
+        }
         r.id[s] = id;
-        v[s] = key_value((int32_t)((uint32_t)(b >> 32) ^ 0x80000000u));
+        v[s] = key_value((int32_t)(m ^ 0x80000000u));
         const uint32_t mask_id = mutant == 2 ? (id ^ 1u) : id;
 #pragma unroll
         for (int q = 0; q < Q; ++q)
-            if (lane + 64 * q == mask_id) pk[q] = 0;
+            if (lane + 64 * q == mask_id) k[q] = 0;
     }
     const float mx = v[0];
     float p[kTopK];

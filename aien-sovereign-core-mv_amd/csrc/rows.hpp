@@ -111,6 +111,21 @@ struct Fp8Slab : Slab<K, RPW> {
                                         float (&acc)[RPW], uint32_t lane) const {
         this->accumulate(sc, acc, lane, [&](const u32x4 w, int ph) { return fp8_dot16(w, xr[ph]); });
     }
+    // RPW rows starting at row0 may reach into the next 128-row scale block when RPW does not
+    // divide 128: sc[0] holds the scales of row0's block, sc[1] those of the last row's block, and
+    // each chunk (one row, KB >= 1024) takes the block of its row.
+    static constexpr bool kOneBlock = 128 % RPW == 0;
+    __device__ __forceinline__ void dot2(const float (&xr)[P][16], const float (&sc)[2][P], uint32_t row0,
+                                         float (&acc)[RPW]) const {
+        static_assert(K >= 1024, "one row per chunk");
+#pragma unroll
+        for (int c = 0; c < B::CH; ++c) {
+            const int ph = c % P;
+            const int r = B::row_lo(c);
+            const bool upper = ((row0 + r) >> 7) != (row0 >> 7);
+            acc[r] = fmaf(fp8_dot16(this->v[c], xr[ph]), upper ? sc[1][ph] : sc[0][ph], acc[r]);
+        }
+    }
 };
 
 // bf16 slab of RPW rows of K columns (rows of 2K bytes)
