@@ -68,12 +68,15 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     constexpr int P = S::P;
     __shared__ uint32_t sh_id[kTopK];
     __shared__ float sh_w[kTopK];
+    __shared__ __align__(16) float xs[kHidden];  // the normed row, staged once per workgroup
     const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
     const uint32_t item = blockIdx.x * 4 + wid;
     const uint32_t slot = item / (kInter / kGuPairs), j0 = (item % (kInter / kGuPairs)) * kGuPairs;
-    float xr[P][16];
-    S::load_x(a.xn, lane, xr);
-    // wavefront 0 ranks the logits for the workgroup
+    static_assert(kHidden == 8 * 256, "two float4 of the row per thread");
+    const f32x4 xt0 = *as_global_f32x4(a.xn + 4 * threadIdx.x);
+    const f32x4 xt1 = *as_global_f32x4(a.xn + 1024 + 4 * threadIdx.x);
+    // wavefront 0 ranks the logits for the workgroup (its logits load goes out right behind the
+    // row's: the row is written to LDS after the ranking)
     if (wid == 0) {
         Route r;
         route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
@@ -85,7 +88,11 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
             }
         }
     }
-    __syncthreads();
+    reinterpret_cast<f32x4 *>(xs)[threadIdx.x] = xt0;
+    reinterpret_cast<f32x4 *>(xs)[threadIdx.x + 256] = xt1;
+    __syncthreads();  // route and staged row complete
+    float xr[P][16];
+    S::load_x_lds(xs, lane, xr);
     const uint32_t e = sh_id[slot];
     const uint8_t *we = a.w + (size_t)e * 2 * kInter * kHidden;
     const float *se = a.s + (size_t)e * (2 * kInter / 128) * (kHidden / 128);

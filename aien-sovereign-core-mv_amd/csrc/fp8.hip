@@ -37,33 +37,62 @@ __device__ __forceinline__ void group_tensor(const Fp8RowsArgs &a, uint32_t g, u
     }
 }
 
-template <int K, int RPW, int EPI, int XSRC>
+// XL: the workgroup's four wavefronts share one group (groups == 1 or n / RPW a multiple of 4),
+// so the activation row (and the norm weights) is staged once per workgroup in LDS instead of
+// once per wavefront — a CU's loads share one path, and the replicated activation bytes would
+// otherwise double its traffic.
+template <int K, int RPW, int EPI, int XSRC, bool XL>
 __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     using S = Fp8Slab<K, RPW>;
     constexpr int P = S::P;
+    constexpr int NX = (K / 4 + 255) / 256;  // float4 of the row per thread when staged
+    __shared__ __align__(16) float xs[XL ? K : 4];
+    __shared__ __align__(16) float ws[XL && XSRC != XS_F32 ? K : 4];
     const uint32_t lane = lane_id();
     // wave-uniform (scalar registers): the group's weight pointer then comes from a scalar
     // kernel-argument load instead of a vector round trip ahead of the weight stream
     const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const uint32_t per_group = a.n / RPW;
-    if (wave >= a.groups * per_group) return;
-    const uint32_t g = wave / per_group, row0 = (wave % per_group) * RPW;
+    const bool live = wave < a.groups * per_group;
+    if (!XL && !live) return;  // with XL every thread takes part in the staging and its barrier
+    const uint32_t wv = live ? wave : 0;  // a wavefront past the end streams row 0, unused
+    const uint32_t g = wv / per_group, row0 = (wv % per_group) * RPW;
     const uint8_t *wexp;
     const float *sexp;
     group_tensor(a, g, K, wexp, sexp);
 
-    // every small load (activation phases, norm weights, block scales) goes ahead of the weight
-    // stream: vector-memory waits complete in issue order, so waiting on any of them then never
-    // waits on the weights
+    // every small load (activation row or phases, norm weights, block scales) goes ahead of the
+    // weight stream: vector-memory waits complete in issue order, so waiting on any of them then
+    // never waits on the weights
     float xr[P][16];
     float nw[P][16];
-    if (XSRC == XS_EMBED_NORM) {
-        const uint32_t tok = *as_global_u32(a.embed_tok) % a.embed_rows;
-        S::load_x_bf16(a.embed + (size_t)tok * K, lane, xr);
+    f32x4 xt[NX], wt[NX];
+    u32x4 et;
+    if constexpr (XL) {
+        if (XSRC == XS_EMBED_NORM) {
+            static_assert(XSRC != XS_EMBED_NORM || K == 2048, "one 8-value piece of the row per thread");
+            const uint32_t tok = *as_global_u32(a.embed_tok) % a.embed_rows;
+            et = *as_global(a.embed + (size_t)tok * K + 8 * threadIdx.x);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NX; ++i)
+                xt[i] = *as_global_f32x4(a.x + (size_t)g * a.x_stride + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
+        }
+        if (XSRC != XS_F32) {
+#pragma unroll
+            for (int i = 0; i < NX; ++i)
+                wt[i] = *as_global_f32x4(a.norm_w + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
+        }
     } else {
-        S::load_x(a.x + (size_t)g * a.x_stride, lane, xr);
+        if (XSRC == XS_EMBED_NORM) {
+            const uint32_t tok = *as_global_u32(a.embed_tok) % a.embed_rows;
+            S::load_x_bf16(a.embed + (size_t)tok * K, lane, xr);
+        } else {
+            S::load_x(a.x + (size_t)g * a.x_stride, lane, xr);
+        }
+        if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
     }
-    if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
+    __builtin_amdgcn_sched_barrier(0);  // the activation loads stay ahead of everything below
     // block scales of row0's 128-row block, and of the last row's when RPW does not divide 128
     float sc[2][P];
     S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc[0]);
@@ -77,6 +106,26 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     // every load is issued before any arithmetic (the scheduler would otherwise sink the weight
     // loads between the dots, one round trip each)
     __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (XL) {
+        if (XSRC == XS_EMBED_NORM) {
+            f32x4 *d = reinterpret_cast<f32x4 *>(xs + 8 * threadIdx.x);
+            d[0] = f32x4{bf16_lo(et[0]), bf16_hi(et[0]), bf16_lo(et[1]), bf16_hi(et[1])};
+            d[1] = f32x4{bf16_lo(et[2]), bf16_hi(et[2]), bf16_lo(et[3]), bf16_hi(et[3])};
+        } else {
+#pragma unroll
+            for (int i = 0; i < NX; ++i)
+                if (threadIdx.x + 256 * i < (uint32_t)K / 4) reinterpret_cast<f32x4 *>(xs)[threadIdx.x + 256 * i] = xt[i];
+        }
+        if (XSRC != XS_F32) {
+#pragma unroll
+            for (int i = 0; i < NX; ++i)
+                if (threadIdx.x + 256 * i < (uint32_t)K / 4) reinterpret_cast<f32x4 *>(ws)[threadIdx.x + 256 * i] = wt[i];
+        }
+        __syncthreads();  // LDS only: the weight stream stays in flight
+        S::load_x_lds(xs, lane, xr);
+        if (XSRC != XS_F32) S::load_x_lds(ws, lane, nw);
+    }
 
     // RMSNorm is one scale per row: dot with x * w and scale the row sums at the end, so the
     // f64 sum of squares runs beside the weight stream instead of ahead of it
@@ -105,7 +154,7 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     if constexpr (S::kOneBlock) slab.dot(xr, sc[0], acc, lane);
     else slab.dot2(xr, sc, row0, acc);
     const float v = reduce_rows(acc, lane) * scale;
-    if (lane < (uint32_t)RPW) a.y[yrow] = EPI == EPI_STORE ? v : yres + v;
+    if (live && lane < (uint32_t)RPW) a.y[yrow] = EPI == EPI_STORE ? v : yres + v;
 }
 
 // Any k (a multiple of 128 up to 32768): rows per wavefront rpw = 1024 / gcd(k, 1024) <= 8,
@@ -185,7 +234,10 @@ uint32_t fp8_rows_blocks(const Fp8RowsArgs &a) {
 template <int K, int RPW, int EPI, int XSRC>
 static hipError_t launch_k(const Fp8RowsArgs &a, hipStream_t st) {
     const uint32_t waves = a.groups * (a.n / RPW);
-    OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    // the activation row is staged per workgroup when the workgroup's wavefronts share a group
+    const bool xl = a.groups == 1 || (a.n / RPW) % 4 == 0;
+    if (xl) OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, true>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    else OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, false>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -79,6 +79,21 @@ struct Fp8Slab : Slab<K, RPW> {
             }
         }
     }
+    // the phases from a row staged in LDS
+    __device__ static void load_x_lds(const float *xs, uint32_t lane, float (&xr)[P][16]) {
+#pragma unroll
+        for (int ph = 0; ph < P; ++ph) {
+            const f32x4 *q = reinterpret_cast<const f32x4 *>(xs + B::col_bytes(ph, lane));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 t = q[i];
+                xr[ph][4 * i] = t.x;
+                xr[ph][4 * i + 1] = t.y;
+                xr[ph][4 * i + 2] = t.z;
+                xr[ph][4 * i + 3] = t.w;
+            }
+        }
+    }
     // the phases of a bf16 row (an embedding row as the activation)
     __device__ static void load_x_bf16(const uint16_t *x, uint32_t lane, float (&xr)[P][16]) {
 #pragma unroll
