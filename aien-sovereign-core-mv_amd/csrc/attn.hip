@@ -283,6 +283,150 @@ hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------ paged (matrix cores)
+// GQA group 8 over 16-token pages of the reference layout, one wavefront per (split, kv head,
+// seq), the same bf16 hi/lo matrix-core products as the fused kernel. The K rows of a page go
+// straight into the A operand of S^T = K q^T (lane (g, n): token n, 16 contiguous bytes of each
+// 64-byte k-step, so every load instruction reads whole 64-byte segments of 16 rows). V rows are
+// token-major in the pool while the B operand of O = P V wants four tokens of one dim per lane,
+// so each page's V tile is read coalesced (16 lanes per 256-byte row), staged in LDS and read
+// back transposed. Tokens at or past the context in the last page may hold anything (unwritten
+// slots): their scores are selected to -inf and their V rows to zero before staging, so neither
+// reaches the result. The page table of the split is read 64 entries at a time into one VGPR
+// and the page ids taken by readlane, so no page load waits on a table load.
+constexpr uint32_t kVtRow = 272;  // bytes per staged V row: 256 + 16 (rows 4 g apart on distinct banks)
+
+struct PagedRegs {
+    u32x4 k[4];  // A operand of the four k-steps
+    u32x4 v[4];  // V rows: piece j is token 4 j + lane / 16, dims 8 (lane % 16) .. +8
+};
+
+template <int MUT>
+__device__ __forceinline__ void paged_load(const AttnArgs &a, const int32_t *tab, uint32_t blk, uint32_t h,
+                                           uint32_t page, uint32_t ctx, uint32_t lane, PagedRegs &R) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint8_t *pg = a.pool + (uint64_t)blk * a.g.block_stride + (uint64_t)a.layer * a.g.layer_stride;
+    const gu32x4 *kp = as_global(pg + (uint64_t)n * a.g.token_stride + (uint64_t)h * a.g.head_stride + 16 * g);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) R.k[ks] = __builtin_nontemporal_load(kp + 4 * ks);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t t = 4 * j + g;
+        const uint8_t *vpg = pg;
+        if (MUT == 2) {  // test mutant: V one position late (clamped to the last token)
+            const uint32_t tv = min(page * 16 + t + 1, ctx - 1);
+            t = tv & 15;
+            vpg = a.pool + (uint64_t)(uint32_t)tab[tv >> 4] * a.g.block_stride +
+                  (uint64_t)a.layer * a.g.layer_stride;
+        }
+        R.v[j] = __builtin_nontemporal_load(as_global(vpg + a.g.plane_stride + (uint64_t)t * a.g.token_stride +
+                                                      (uint64_t)h * a.g.head_stride + 16 * n));
+    }
+}
+
+// V tile -> LDS (invalid tokens zeroed) -> the B operands of the 8 n-blocks
+__device__ __forceinline__ void paged_stage_v(const PagedRegs &R, uint32_t tok0, uint32_t ctx, uint32_t lane,
+                                              uint8_t *vt, DattnPage &T) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    __syncthreads();  // the previous page's reads are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t t = 4 * j + g;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4 *>(vt + t * kVtRow + 16 * n) = tok0 + t < ctx ? R.v[j] : z;
+    }
+    __syncthreads();
+    const uint16_t *v16 = reinterpret_cast<const uint16_t *>(vt);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        const uint32_t col = 16 * nb + n;
+        const uint32_t e0 = v16[(4 * g + 0) * (kVtRow / 2) + col];
+        const uint32_t e1 = v16[(4 * g + 1) * (kVtRow / 2) + col];
+        const uint32_t e2 = v16[(4 * g + 2) * (kVtRow / 2) + col];
+        const uint32_t e3 = v16[(4 * g + 3) * (kVtRow / 2) + col];
+        T.v[nb] = u32x2{e0 | (e1 << 16), e2 | (e3 << 16)};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) T.k[ks] = R.k[ks];
+}
+
+template <int MUT>
+__global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
+    __shared__ __align__(16) uint16_t qhl[2][8][128];  // the 8 q heads: bf16 hi, lo halves
+    __shared__ __align__(16) uint8_t vt[16 * kVtRow];  // one staged V tile
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t ctx = (uint32_t)a.context_lens[b];
+    const uint32_t pages = (ctx + 15) / 16;
+    uint32_t active, pps;
+    attn_split_plan(pages, a.splits, 0, active, pps);
+    if (c >= active) return;
+    const uint32_t p_begin = c * pps, p_end = min(pages, p_begin + pps);
+    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
+    // the split's page ids, 64 at a time (lane i: page base + i)
+    uint32_t tbase = p_begin;
+    int32_t tl = tab[min(tbase + lane, pages - 1)];
+    const float *q = a.q + ((size_t)b * a.qh + h * 8) * 128;
+    float q0[8], q1[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        q0[r] = *as_global_f32(q + r * 128 + lane);
+        q1[r] = *as_global_f32(q + r * 128 + 64 + lane);
+    }
+    PagedRegs R;
+    paged_load<MUT>(a, tab, (uint32_t)__builtin_amdgcn_readfirstlane(tl), h, p_begin, ctx, lane, R);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        qhl[0][r][lane] = bf16_split_hi(q0[r]);
+        qhl[1][r][lane] = bf16_split_lo(q0[r]);
+        qhl[0][r][lane + 64] = bf16_split_hi(q1[r]);
+        qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
+    }
+    __syncthreads();
+    bf16x8 qop[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[n >> 3][n & 7][32 * ks + 8 * g]));
+
+    float m_l = -INFINITY, l_l = 0.f;
+    f32x4 O[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    DattnPage T;
+    for (uint32_t p = p_begin; p < p_end; ++p) {
+        // the next page's loads go out before this page's math
+        PagedRegs nx;
+        const bool more = p + 1 < p_end;
+        if (more) {
+            if (p + 1 - tbase >= 64) {
+                tbase += 64;
+                tl = tab[min(tbase + lane, pages - 1)];
+            }
+            const uint32_t nblk = (uint32_t)__builtin_amdgcn_readlane(tl, p + 1 - tbase);
+            paged_load<MUT>(a, tab, nblk, h, p + 1, ctx, lane, nx);
+        }
+        paged_stage_v(R, p * 16, ctx, lane, vt, T);
+        if (p == p_begin) dattn_page<true>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        else dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        if (more) R = nx;
+    }
+    // rows 4 g + i: hi half of head 4 g + i (g < 2) or lo half (g >= 2); see k_dattn
+    const uint32_t hg = g & 1, nb_off = (g >> 1) * 4;
+    float *part = a.part + (((size_t)b * a.qh + h * 8) * a.splits + c) * kPartStride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float *pp = part + (size_t)(4 * hg + i) * a.splits * kPartStride;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) pp[4 + 16 * (nb + nb_off) + n] = pair_sum<32>(O[nb][i], O[nb + 4][i]);
+    }
+    if (lane < 8) {  // lane r holds head r's running max and sum
+        float *pp = part + (size_t)lane * a.splits * kPartStride;
+        pp[0] = m_l;
+        pp[1] = l_l;
+    }
+}
+
 // ------------------------------------------------------------------------ paged (VALU)
 // One wavefront per (split, kv head, seq): lane = token for Q K (K row per lane, q read
 // wave-uniformly), lane = dim pair for P V.
@@ -395,6 +539,14 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const dim3 grid(a.splits, a.kvh, a.seqs);
+    if (paged_mfma(a.qh, a.kvh, a.g.block_size)) {
+        // kv head fastest: the heads of one split are dispatched together and read the same
+        // pages' 1 KiB token rows at about the same time
+        const dim3 hgrid(a.kvh, a.splits, a.seqs);
+        if (a.mutant == 2) hipLaunchKernelGGL(k_paged<2>, hgrid, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(k_paged<0>, hgrid, dim3(64), 0, st, a);
+        return hipGetLastError();
+    }
     switch (a.qh / a.kvh) {
     case 1: hipLaunchKernelGGL(k_attn<1>, grid, dim3(64), 0, st, a); break;
     case 2: hipLaunchKernelGGL(k_attn<2>, grid, dim3(64), 0, st, a); break;
@@ -406,22 +558,29 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------------ split combine
-// Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l); fused partials are
-// dims in order. Either way partial dim d sits at 4 + d, so one combine serves both.
-// One wavefront per (seq, q head, quarter of the dims): lane l covers dim 32 q + l % 32 of the
-// slots of parity l / 32, so a workgroup reads 8 KiB of partials (a CU's loads share one queue).
+// Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l) for the VALU kernel
+// and dims in order for the matrix-core kernels; either way partial dim d sits at 4 + d, so one
+// combine serves all. One wavefront per (seq, q head, quarter of the dims): lane l covers dim
+// 32 q + l % 32 of the slots of parity l / 32, so a workgroup reads 8 KiB of partials per 64
+// slots (a CU's loads share one queue). CH chunks of 64 slots: 1 for up to 64 splits, 4 for up
+// to 256.
+template <int CH>
 __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
-    __shared__ float wsh[kDattnSplits];
+    __shared__ float wsh[64 * CH];
     const uint32_t head = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y, lane = threadIdx.x;
     const uint32_t d = 32 * quarter + (lane & 31), half = lane >> 5;
     const float *pp = a.part + ((size_t)b * a.qh + head) * a.splits * kPartStride;
     // Every slot's (m, l) and o values are loaded before the split count is known (the stale
     // slots past it are dropped below), so the context length and the partials share one round
     // trip.
-    const uint32_t mslot = min(lane, a.splits - 1);
-    const float m_raw = *as_global_f32(pp + mslot * kPartStride);
-    const float l_raw = *as_global_f32(pp + mslot * kPartStride + 1);
-    constexpr uint32_t kPer = kDattnSplits / 2;
+    float m_raw[CH], l_raw[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const uint32_t mslot = min(64 * c + lane, a.splits - 1);
+        m_raw[c] = *as_global_f32(pp + mslot * kPartStride);
+        l_raw[c] = *as_global_f32(pp + mslot * kPartStride + 1);
+    }
+    constexpr uint32_t kPer = 32 * CH;
     float f[kPer];
 #pragma unroll
     for (uint32_t k = 0; k < kPer; ++k)
@@ -430,16 +589,21 @@ __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
     if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + a.tile_tokens - 1) / a.tile_tokens;
     else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + a.tile_tokens - 1) / a.tile_tokens;
     uint32_t active, tps;
-    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= splits <= 64
-    // lane s holds split s's (m, l)
-    const bool mine = lane < active;
-    const float m = mine ? m_raw : -INFINITY;
-    const float l = mine ? l_raw : 0.f;
-    float M = row16_max(m);
+    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= splits <= 64 CH
+    // lane s of chunk c holds split 64 c + s's (m, l)
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) M = fmaxf(M, 64 * c + lane < active ? m_raw[c] : -INFINITY);
+    M = row16_max(M);
     M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
-    const float w = mine ? (a.mutant == 4 ? 1.0f : expf(m - M)) : 0.f;
-    const float L = wave_sum(w * l);
-    wsh[lane] = w;
+    float L = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const bool mine = 64 * c + lane < active;
+        const float w = mine ? (a.mutant == 4 ? 1.0f : expf(m_raw[c] - M)) : 0.f;
+        L += wave_sum(w * (mine ? l_raw[c] : 0.f));
+        wsh[64 * c + lane] = w;
+    }
     __syncthreads();
     // slots past `active` are selected out, not weighted by 0 (their contents may not be finite)
     float O = 0.f;
@@ -453,7 +617,8 @@ __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
 }
 
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_attn_combine, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
+    if (a.splits > 64) OMEGA_LAUNCH(k_attn_combine<4>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
+    else OMEGA_LAUNCH(k_attn_combine<1>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -470,10 +635,22 @@ void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out
         }
 }
 
-// splits of a paged launch: one tile of 64 tokens per item up to 64 items per (seq, kv head)
-uint32_t paged_splits(uint32_t max_ctx) {
-    const uint32_t t = (max_ctx + kAttnTile - 1) / kAttnTile;
-    return t < 1 ? 1 : (t > 64 ? 64 : t);
+bool paged_mfma(uint32_t qh, uint32_t kvh, uint32_t block_size) { return qh == 8 * kvh && block_size == 16; }
+
+// Splits of a paged launch and the tokens of its split unit. Matrix-core kernel: 16-token pages,
+// splits chosen so that the launch holds about 2048 wavefronts (8 per CU) when the pages allow,
+// at least two pages per split and at most 256 splits per (seq, kv head). VALU kernel: tiles of
+// 64 tokens, one per item up to 64 items.
+uint32_t paged_splits(uint32_t max_ctx, uint32_t seqs, uint32_t kvh, bool mfma, uint32_t &unit) {
+    unit = mfma ? 16u : kAttnTile;
+    const uint32_t units = (max_ctx + unit - 1) / unit;
+    if (!mfma) return units < 1 ? 1 : (units > 64 ? 64 : units);
+    // at least two pages per split (the page stream stays double-buffered), at most 256 splits
+    const uint32_t pairs = seqs * kvh;
+    uint32_t s = pairs >= 2048 ? 1u : (2048u + pairs - 1) / pairs;
+    const uint32_t cap = units / 2 > 256 ? 256 : units / 2;
+    s = s < cap ? s : cap;
+    return s < 1 ? 1 : s;
 }
 
 KvGeom geom_of(const OmegaGpuKvLayout &l) {
@@ -854,7 +1031,8 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
         g.layer_stride = 0;
         lay = 0;
     }
-    const uint32_t splits = paged_splits(max_ctx);
+    uint32_t unit = kAttnTile;
+    const uint32_t splits = paged_splits(max_ctx, seqs, kvh, paged_mfma(qh, kvh, layout->block_size), unit);
     const size_t part_bytes = (size_t)seqs * qh * splits * kPartStride * 4;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
     // device scratch: q | out | table | lens | partials | staged pages
@@ -906,6 +1084,7 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
     CombineArgs cb;
     cb.part = pd;
     cb.splits = splits;
+    cb.tile_tokens = unit;
     cb.context_lens = lens_dev;
     cb.seqs = seqs;
     cb.qh = qh;
@@ -1014,7 +1193,9 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     Ctx *cx = ctx(F_ATTN);
     if (!cx) return OMEGA_GPU_ATTN_CHIP_FAIL;
     // every context must fit max_context: the split count is planned from it
-    const uint32_t splits = paged_splits(max_context);
+    uint32_t unit = kAttnTile;
+    const uint32_t splits = paged_splits(max_context, num_seqs, num_kv_heads,
+                                         paged_mfma(num_q_heads, num_kv_heads, layout->block_size), unit);
     if (!ensure_scratch(F_ATTN, cx, (size_t)num_seqs * num_q_heads * splits * kPartStride * 4))
         return OMEGA_GPU_ATTN_CHIP_FAIL;
     AttnArgs a;
@@ -1034,6 +1215,7 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     CombineArgs cb;
     cb.part = a.part;
     cb.splits = splits;
+    cb.tile_tokens = unit;
     cb.context_lens = context_lens_dev;
     cb.seqs = num_seqs;
     cb.qh = num_q_heads;

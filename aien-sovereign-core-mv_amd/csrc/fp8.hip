@@ -382,6 +382,13 @@ hipError_t launch_bf16_synth(uint16_t *w, uint32_t n, uint32_t k, uint64_t seed,
     return hipGetLastError();
 }
 
+hipError_t launch_bf16_synth_count(uint16_t *w, size_t count, uint64_t seed, uint64_t tensor, float sigma,
+                                   hipStream_t st) {
+    const float c = sigma * (1.0f / 65536.0f);
+    hipLaunchKernelGGL(k_bf16_synth, dim3(8192), dim3(256), 0, st, w, count, synth_base(seed, tensor), c);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- host-side checks
 static int check_tensor_shape(Family f, uint32_t experts, uint32_t n, uint32_t k) {
     if (experts == 0 || n == 0 || n % 128 != 0 || k % 128 != 0 || k < 128 || k > 32768) {
@@ -530,6 +537,20 @@ void omega_gpu_synth_bf16_host(uint64_t seed, uint64_t tensor_id, size_t count, 
         memcpy(&u, &v, 4);
         out[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
     }
+}
+
+int omega_gpu_synth_bf16_dev(void *dst, uint64_t count, uint64_t seed, uint64_t tensor_id, float sigma) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_BF16);
+    if (!dst) {
+        set_error(F_BF16, "bf16 synth dev: NULL buffer");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    Ctx *c = ctx(F_BF16);
+    if (!c) return OMEGA_GPU_CHIP_FAIL;
+    if (count == 0) return OMEGA_GPU_OK;
+    OMEGA_HIP(F_BF16, launch_bf16_synth_count(static_cast<uint16_t *>(dst), count, seed, tensor_id, sigma, c->stream));
+    return OMEGA_GPU_OK;
 }
 
 int omega_gpu_fp8_tensor_synth(uint32_t experts, uint32_t n, uint32_t k, uint64_t seed,

@@ -72,6 +72,9 @@ constexpr uint32_t kArgmaxSlots = 64;
 hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st);
 hipError_t launch_bf16_synth(uint16_t *w, uint32_t n, uint32_t k, uint64_t seed, uint64_t tensor,
                              float sigma, hipStream_t st);
+// `count` bf16 values of the same generator into any device buffer
+hipError_t launch_bf16_synth_count(uint16_t *w, size_t count, uint64_t seed, uint64_t tensor, float sigma,
+                                   hipStream_t st);
 // sets *flag when any element is NaN or infinite
 hipError_t launch_bf16_scan(const uint16_t *w, size_t count, uint32_t *flag, hipStream_t st);
 // host side of the argmax: the greedy token from the slots (lowest index of the maximum)
@@ -158,6 +161,9 @@ struct AttnArgs {
     int mutant = 0;                         // 2: V one position late
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+// GQA group 8 over 16-token pages runs on the matrix cores (k_paged), other shapes on the VALU
+bool paged_mfma(uint32_t qh, uint32_t kvh, uint32_t block_size);
+uint32_t paged_splits(uint32_t max_ctx, uint32_t seqs, uint32_t kvh, bool mfma, uint32_t &unit);
 
 // Combines the split partials of every (seq, q head): out = sum w_s o_s / sum w_s l_s with
 // w_s = exp(m_s - max m), times out_scale.

@@ -194,6 +194,7 @@ SIGNATURES = {
     "omega_gpu_fp8_tensor_synth": (i32, [u32, u32, u32, u64, u64, f32, C.POINTER(P)]),
     "omega_gpu_bf16_tensor_synth": (i32, [u32, u32, u64, u64, f32, C.POINTER(P)]),
     "omega_gpu_synth_bf16_host": (None, [u64, u64, C.c_size_t, f32, i32, P]),
+    "omega_gpu_synth_bf16_dev": (i32, [P, u64, u64, u64, f32]),
     "omega_gpu_fp8_gemv_dev": (i32, [P, u32, P, P]),
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
@@ -699,6 +700,99 @@ class DecodeGraph:
             self.free()
         except Exception:
             pass
+
+
+_hip = None
+
+
+def hip():
+    """libamdhip64 for the device buffers and events of the device-pointer entry points."""
+    global _hip
+    if _hip is None:
+        h = C.CDLL("libamdhip64.so")
+        h.hipMalloc.argtypes = [C.POINTER(P), C.c_size_t]
+        h.hipFree.argtypes = [P]
+        h.hipMemcpy.argtypes = [P, P, C.c_size_t, C.c_int]
+        h.hipMemsetAsync.argtypes = [P, C.c_int, C.c_size_t, P]
+        h.hipEventCreate.argtypes = [C.POINTER(P)]
+        h.hipEventRecord.argtypes = [P, P]
+        h.hipEventSynchronize.argtypes = [P]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), P, P]
+        h.hipEventDestroy.argtypes = [P]
+        _hip = h
+    return _hip
+
+
+class DeviceBuffer:
+    """A device allocation (hipMalloc) with host copies; `.ptr` is the device address."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = P()
+        rc = hip().hipMalloc(C.byref(p), C.c_size_t(max(self.nbytes, 1)))
+        if rc != 0:
+            raise OmegaGpuError(-4, f"hipMalloc({self.nbytes}) failed: {rc}")
+        self.ptr = p
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        sync()
+        assert hip().hipMemcpy(self.ptr, a.ctypes.data_as(P), C.c_size_t(a.nbytes), 1) == 0
+
+    def download(self, dtype, count):
+        out = np.empty(count, dtype)
+        sync()
+        assert hip().hipMemcpy(out.ctypes.data_as(P), self.ptr, C.c_size_t(out.nbytes), 2) == 0
+        return out
+
+    def free(self):
+        if self.ptr:
+            sync()
+            hip().hipFree(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class StreamTimer:
+    """HIP events on the library's stream: the GPU time between start() and stop()."""
+
+    def __init__(self):
+        self.a, self.b = P(), P()
+        assert hip().hipEventCreate(C.byref(self.a)) == 0
+        assert hip().hipEventCreate(C.byref(self.b)) == 0
+
+    def start(self):
+        assert hip().hipEventRecord(self.a, lib().omega_gpu_stream()) == 0
+
+    def stop(self):
+        assert hip().hipEventRecord(self.b, lib().omega_gpu_stream()) == 0
+
+    def ms(self):
+        assert hip().hipEventSynchronize(self.b) == 0
+        v = C.c_float()
+        assert hip().hipEventElapsedTime(C.byref(v), self.a, self.b) == 0
+        return v.value
+
+
+def synth_bf16_dev(buf, count, seed, tensor_id, sigma=1.0, offset_bytes=0):
+    """Fill `count` bf16 values of the library's generator into a device buffer."""
+    dst = P((buf.ptr.value or 0) + offset_bytes)
+    rc = lib().omega_gpu_synth_bf16_dev(dst, count, seed, tensor_id, sigma)
+    if rc:
+        raise OmegaGpuError(rc, _s(lib().omega_gpu_bf16_last_error()))
 
 
 def synth_bf16_host(seed, tensor_id, shape, sigma, one_plus=False):

@@ -152,6 +152,113 @@ def copy_probe(nbytes):
     print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
 
 
+# ---------------------------------------------------------------- configuration 3: paged attention
+PAGED_POINTS = [(b, l) for b in (1, 8, 32) for l in (2048, 8192, 32768)]
+
+
+def paged_bytes(seqs, ctx):
+    """Algorithmic HBM bytes of one paged-attention call: the K and V rows of the 4 kv heads over
+    every context token (2 x 4 x 256 B per token), q and out f32, the page tables and lengths."""
+    return seqs * ctx * 2 * KVH * HD * 2 + 2 * seqs * QH * HD * 4 + seqs * (ctx // 16) * 4 + seqs * 4
+
+
+def paged_cpu_baseline(om_unused=None):
+    """The oracle's paged attention (f64 SDPA over the bf16 rows) on one host thread, batch 1 at
+    context 2048, on a host pool of the same layout."""
+    import ctypes as C
+
+    import pyoracle as orc
+
+    rng = np.random.default_rng(1)
+    lay = orc.kv_layout(128, 16, 1, KVH, HD)
+    pool = orc.f32_to_bf16(rng.standard_normal(lay.pool_bytes // 2).astype(np.float32)).view(np.uint8)
+    tab = rng.permutation(128).astype(np.int32)
+    q = rng.standard_normal(QH * HD).astype(np.float32)
+    out = np.zeros(QH * HD, np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        orc.lib().oref_paged_attention(orc.ptr(q), orc.ptr(pool), C.byref(lay), orc.ptr(tab), 2048, 0,
+                                       QH, KVH, HD, orc.ptr(out))
+        reps += 1
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return {"value": round(us, 1), "unit": "us/call", "cores": 1, "kind": "port",
+            "sample": f"oracle oref_paged_attention (oracle/oracle.c), batch 1 at context 2048, "
+                      f"{reps} calls in about 10 s on one host thread"}
+
+
+def bench_paged(om, args):
+    """Configuration 3: GQA 32/4 x 128 decode attention over 16-token pages of the 30B pool
+    geometry (48 layers, one layer read), page tables random permutations of the free pages,
+    bf16 K/V ~ N(0,1); each point timed cold (the Infinity Cache and L2 flushed by a 1 GiB fill
+    before every call) with HIP events on the library stream: the attention launch and its split
+    combine."""
+    import ctypes as C
+
+    max_pages = max(b * l // 16 for b, l in PAGED_POINTS)
+    layers = L
+    import pyoracle as orc
+
+    lay = orc.kv_layout(max_pages, 16, layers, KVH, HD)
+    L_ = om.KvLayout(lay.block_stride_bytes, lay.layer_stride_bytes, lay.kv_plane_stride_bytes,
+                     lay.token_stride_bytes, lay.head_stride_bytes, lay.pool_bytes, lay.num_blocks,
+                     lay.num_layers, lay.block_size)
+    pool = om.DeviceBuffer(lay.pool_bytes)
+    om.synth_bf16_dev(pool, lay.pool_bytes // 2, SEED, 77, 1.0)
+    flush = om.DeviceBuffer(1 << 30)
+    om.sync()
+    lib = om.lib()
+    hip = om.hip()
+    stream = lib.omega_gpu_stream()
+    timer = om.StreamTimer()
+    rng = np.random.default_rng(SEED)
+    layer = 7
+    lines = []
+    for seqs, ctx in PAGED_POINTS:
+        pages = ctx // 16
+        perm = rng.permutation(max_pages)[: seqs * pages].astype(np.int32).reshape(seqs, pages)
+        q = rng.standard_normal((seqs, QH * HD)).astype(np.float32)
+        qd = om.DeviceBuffer.from_array(q)
+        td = om.DeviceBuffer.from_array(perm)
+        ld = om.DeviceBuffer.from_array(np.full(seqs, ctx, np.int32))
+        od = om.DeviceBuffer(q.nbytes)
+
+        def call():
+            rc = lib.omega_gpu_paged_attention_batch_dev(qd.ptr, pool.ptr, C.byref(L_), td.ptr, ld.ptr,
+                                                         pages, seqs, ctx, layer, QH, KVH, HD, od.ptr)
+            assert rc == 0, om._s(lib.omega_gpu_attention_last_error())
+
+        for _ in range(2):
+            call()
+        times = []
+        for _ in range(args.paged_reps):
+            assert hip.hipMemsetAsync(flush.ptr, 1, C.c_size_t(flush.nbytes), stream) == 0
+            timer.start()
+            call()
+            timer.stop()
+            times.append(timer.ms() * 1e3)
+        us = float(np.median(times))
+        b = paged_bytes(seqs, ctx)
+        line = {"workload": "paged_attention", "seqs": seqs, "ctx": ctx, "us_per_call": round(us, 2),
+                "algorithmic_bytes": b, "GBs": round(b / (us * 1e3), 1),
+                "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times)}
+        print(json.dumps(line), flush=True)
+        lines.append(line)
+        for buf in (qd, td, ld, od):
+            buf.free()
+    cpu = None if args.no_cpu else paged_cpu_baseline()
+    big = lines[-1]
+    print(json.dumps({
+        "metric": "paged GQA decode attention (configuration 3), achieved HBM GB/s vs peak",
+        "value": big["GBs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "bf16 KV, f32 q/out, fp32 accumulate", "data": "synthetic N(0,1) K/V, random page tables",
+        "config": {"workload": "paged attention 32q/4kv x 128, 16-token pages, 48-layer pool geometry",
+                   "points": [[p["seqs"], p["ctx"]] for p in lines]},
+        "roofline": {"bound": "hbm", "kernel": "k_paged + k_attn_combine", "achieved": big["GBs"],
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": big["frac"], "traffic": None},
+        "points": lines, "cpu_baseline": cpu}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,6 +270,10 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--workload", choices=["decode", "paged"], default="decode",
+                    help="decode: the bs=1 decode step (configuration 4, the headline line); "
+                         "paged: the paged-attention sweep (configuration 3)")
+    ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES (byte-counter calibration)")
     args = ap.parse_args()
@@ -178,6 +289,9 @@ def main():
         sys.exit(3)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.workload == "paged":
+        bench_paged(om, args)
         return
     total = args.prompt + args.warmup + args.steps + 8
     max_pos = om.round_max_pos(total)

@@ -483,6 +483,9 @@ int omega_gpu_bf16_tensor_synth(uint32_t n, uint32_t k, uint64_t seed, uint64_t 
 /* the same generator on the host: count bf16 values of N(0, sigma) (or 1 + N(0, sigma)) */
 void omega_gpu_synth_bf16_host(uint64_t seed, uint64_t tensor_id, size_t count, float sigma,
                                int one_plus, uint16_t *out);
+/* the same generator into a caller's device buffer: count bf16 values of N(0, sigma), enqueued
+ * on the library's stream (no synchronisation) */
+int omega_gpu_synth_bf16_dev(void *dst, uint64_t count, uint64_t seed, uint64_t tensor_id, float sigma);
 /* device-pointer GEMV: x_dev f32[k], y_dev f32[n]; no host copies, no synchronisation
  * (stream = the library's stream) */
 int omega_gpu_fp8_gemv_dev(const OmegaGpuFp8Tensor *t, uint32_t expert, const float *x_dev,

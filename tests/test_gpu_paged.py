@@ -1,0 +1,161 @@
+"""GPU parity of the matrix-core paged decode attention (GQA 32 q / 4 kv heads of 128 over
+16-token pages of the aien-kv-cache layout) against the CPU oracle's f64 attention.
+
+Cases: the configuration-3 shapes (batch 1, 8, 32 at contexts up to 32768, page tables drawn
+from a free-page pool), ragged contexts that end inside a page whose unwritten slots hold NaN
+and infinity, splits longer than 64 pages (the page-table window moves), and the test mutants
+(V one position late, the split combine without its maxima) that the parity bar must catch.
+Bar: max abs error over max abs value <= 2e-3 (attention_out in fp32 accumulate).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+QH, KVH, HD = 32, 4, 128
+
+
+def rel_err(a, e):
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def _omega_layout(omega, lay):
+    return omega.KvLayout(lay.block_stride_bytes, lay.layer_stride_bytes, lay.kv_plane_stride_bytes,
+                          lay.token_stride_bytes, lay.head_stride_bytes, lay.pool_bytes,
+                          lay.num_blocks, lay.num_layers, lay.block_size)
+
+
+class Pool:
+    """A host pool of N(0,1) bf16 rows and its device copy."""
+
+    def __init__(self, omega, oracle, rng, nb, layers):
+        self.lay = oracle.kv_layout(nb, 16, layers, KVH, HD)
+        self.host = oracle.f32_to_bf16(
+            rng.standard_normal(self.lay.pool_bytes // 2).astype(np.float32)).view(np.uint8)
+        self.L = _omega_layout(omega, self.lay)
+        self.dev = omega.DeviceBuffer.from_array(self.host)
+
+    def poison_tail(self, oracle, table, ctx, layer):
+        """NaN / inf bf16 in the slots past `ctx` of the sequence's last page (every head, K and
+        V), in the host pool and the device copy."""
+        last = int(table[(ctx - 1) // 16])
+        lay = self.lay
+        for t in range(ctx % 16 or 16, 16):
+            for plane in (0, 1):
+                off = (last * lay.block_stride_bytes + layer * lay.layer_stride_bytes +
+                       plane * lay.kv_plane_stride_bytes + t * lay.token_stride_bytes)
+                row = self.host[off:off + KVH * 256].view(np.uint16)
+                row[0::2] = 0x7FC0  # NaN
+                row[1::2] = 0x7F80  # +inf
+        self.dev.upload(self.host)
+
+
+def run_dev(omega, pool, q, tabs, lens, layer):
+    lib = omega.lib()
+    seqs, maxb = tabs.shape
+    qd = omega.DeviceBuffer.from_array(q)
+    td = omega.DeviceBuffer.from_array(tabs.astype(np.int32))
+    ld = omega.DeviceBuffer.from_array(lens.astype(np.int32))
+    od = omega.DeviceBuffer(q.nbytes)
+    rc = lib.omega_gpu_paged_attention_batch_dev(qd.ptr, pool.dev.ptr, C.byref(pool.L), td.ptr,
+                                                 ld.ptr, maxb, seqs, int(lens.max()), layer, QH,
+                                                 KVH, HD, od.ptr)
+    assert rc == 0, omega._s(lib.omega_gpu_attention_last_error())
+    return od.download(np.float32, q.size)
+
+
+def oracle_out(oracle, pool, q, table, ctx, layer):
+    want = np.zeros(QH * HD, np.float32)
+    oracle.lib().oref_paged_attention(oracle.ptr(np.ascontiguousarray(q)), oracle.ptr(pool.host),
+                                      C.byref(pool.lay), oracle.ptr(table.astype(np.int32)), int(ctx),
+                                      layer, QH, KVH, HD, oracle.ptr(want))
+    return want
+
+
+@pytest.mark.parametrize("seqs,ctx,check", [(1, 2048, None), (1, 32768, None), (8, 8192, None),
+                                            (32, 32768, (0, 17, 31))])
+def test_config3_shapes(omega, oracle, seqs, ctx, check):
+    rng = np.random.default_rng(seqs * 7 + ctx)
+    nb = 4096
+    pool = Pool(omega, oracle, rng, nb, 2)
+    pages = ctx // 16
+    # every sequence's table is a random permutation of free pages while the pool lasts, then
+    # pages are reused (the kernel never assumes distinct pages)
+    tabs = np.stack([rng.permutation(nb)[:pages] if pages <= nb else rng.integers(0, nb, pages)
+                     for _ in range(seqs)]).astype(np.int32)
+    lens = np.full(seqs, ctx, np.int32)
+    q = rng.standard_normal((seqs, QH * HD)).astype(np.float32)
+    out = run_dev(omega, pool, q, tabs, lens, 1).reshape(seqs, QH * HD)
+    assert np.isfinite(out).all()
+    for b in (range(seqs) if check is None else check):
+        e = rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], ctx, 1))
+        assert e <= TOL, (b, e)
+
+
+def test_ragged_contexts_ignore_unwritten_slots(omega, oracle):
+    rng = np.random.default_rng(31)
+    nb = 512
+    pool = Pool(omega, oracle, rng, nb, 3)
+    lens = np.array([1, 5, 16, 17, 333, 1000, 2047, 4099], np.int32)
+    maxb = int((lens.max() + 15) // 16) + 3
+    tabs = np.full((lens.size, maxb), -1, np.int32)
+    free = rng.permutation(nb)  # disjoint pages: a poisoned tail belongs to its sequence only
+    used = 0
+    for b, cl in enumerate(lens):
+        n_b = (cl + 15) // 16
+        tabs[b, :n_b] = free[used:used + n_b]
+        used += n_b
+    for b, cl in enumerate(lens):
+        if cl % 16:
+            pool.poison_tail(oracle, tabs[b], int(cl), 2)
+    q = rng.standard_normal((lens.size, QH * HD)).astype(np.float32)
+    out = run_dev(omega, pool, q, tabs, lens, 2).reshape(lens.size, QH * HD)
+    assert np.isfinite(out).all()
+    for b, cl in enumerate(lens):
+        e = rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], cl, 2))
+        assert e <= TOL, (b, int(cl), e)
+    # ctx 1: the output of every head is the single V row
+    lay = pool.lay
+    off = int(tabs[0, 0]) * lay.block_stride_bytes + 2 * lay.layer_stride_bytes + lay.kv_plane_stride_bytes
+    v0 = oracle.bf16_to_f32(pool.host[off:off + KVH * 256].view(np.uint16).copy()).reshape(KVH, HD)
+    np.testing.assert_allclose(out[0].reshape(QH, HD), np.repeat(v0, QH // KVH, axis=0), rtol=1e-6, atol=1e-6)
+
+
+def test_splits_longer_than_the_table_window(omega, oracle):
+    # 128 (seq, kv head) pairs -> 16 splits; 2560 pages per sequence -> 160 pages per split, so
+    # each split crosses two 64-entry windows of its page table
+    rng = np.random.default_rng(32)
+    nb = 2048
+    pool = Pool(omega, oracle, rng, nb, 1)
+    seqs, ctx = 32, 40960 - 7
+    pages = (ctx + 15) // 16
+    tabs = rng.integers(0, nb, (seqs, pages)).astype(np.int32)
+    lens = np.full(seqs, ctx, np.int32)
+    lens[5] = 16 * 65 + 3
+    q = rng.standard_normal((seqs, QH * HD)).astype(np.float32)
+    out = run_dev(omega, pool, q, tabs, lens, 0).reshape(seqs, QH * HD)
+    for b in (0, 5, 31):
+        e = rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0))
+        assert e <= TOL, (b, e)
+
+
+@pytest.mark.parametrize("mutant", [2, 4])
+def test_paged_mutants_are_caught(omega, oracle, mutant):
+    rng = np.random.default_rng(33)
+    nb = 256
+    pool = Pool(omega, oracle, rng, nb, 1)
+    lens = np.array([700, 1500], np.int32)
+    tabs = np.stack([rng.permutation(nb)[:(1500 + 15) // 16] for _ in range(2)]).astype(np.int32)
+    q = (3.0 * rng.standard_normal((2, QH * HD))).astype(np.float32)
+    lib = omega.lib()
+    lib.omega_gpu_decode_attn_test_set_mutant(mutant)
+    try:
+        out = run_dev(omega, pool, q, tabs, lens, 0).reshape(2, QH * HD)
+    finally:
+        lib.omega_gpu_decode_attn_test_set_mutant(0)
+    errs = [rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) for b in range(2)]
+    assert max(errs) > TOL, errs
+    clean = run_dev(omega, pool, q, tabs, lens, 0).reshape(2, QH * HD)
+    assert max(rel_err(clean[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) for b in range(2)) <= TOL
