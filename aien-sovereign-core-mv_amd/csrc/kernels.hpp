@@ -182,6 +182,45 @@ struct CombineArgs {
 };
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st);
 
+// ---------------------------------------------------------------- batched MoE block
+// T tokens (<= kMoeMaxTokens) through RMSNorm, router logits, top-8 and grouping, the grouped
+// gate|up (SwiGLU) and down FP8 GEMMs on the matrix cores, and the slot-order combine.
+constexpr uint32_t kMoeMaxTokens = 64;
+struct MoeArgs {
+    const float *h = nullptr;          // [T][2048] residual rows
+    const float *norm_w = nullptr;     // post-attention RMSNorm weights [2048]
+    const uint16_t *gate = nullptr;    // router [128][2048] bf16
+    float eps = 1e-6f;
+    int norm_topk = 1;
+    uint32_t tokens = 0;
+    const uint8_t *gu_w = nullptr;     // [128][1536][2048] e4m3
+    const float *gu_s = nullptr;       // [128][12][16]
+    const uint8_t *dn_w = nullptr;     // [128][2048][768] e4m3
+    const float *dn_s = nullptr;       // [128][16][6]
+    const float *resid = nullptr;      // optional: out = resid + moe
+    uint32_t *ids = nullptr;           // [T][8]
+    float *weights = nullptr;          // [T][8]
+    float *out = nullptr;              // [T][2048]
+    // workspace (moe_work_carve)
+    float *xn = nullptr;               // [T][2048] x'
+    uint8_t *xq = nullptr;             // [T][16][3][128] e4m3 terms of x'
+    float *xs = nullptr;               // [T][16][4] their scales
+    float *logits = nullptr;           // [T][128]
+    uint32_t *plan = nullptr;          // [0]: segments
+    uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
+    uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
+    uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row
+    float *act = nullptr;              // [T * 8][768] SwiGLU rows
+    uint8_t *aq = nullptr;             // [T * 8][6][3][128]
+    float *as = nullptr;               // [T * 8][6][4]
+    float *ydn = nullptr;              // [T * 8][2048] down rows
+    int mutant = 0;  // 1: rank mask id^1; 2: weights not normalised; 5: gate/up swapped;
+                     // 6: slot 7 dropped; 7: one activation term
+};
+hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st);
+size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens);
+size_t moe_work_bytes(uint32_t tokens);
+
 // RoPE table of one position range (host twin of the oracle's rope_cos_sin)
 void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out);
 

@@ -95,6 +95,7 @@ struct Knobs {
     int fp8_sealed = 0;
     uint32_t fp8_cta_budget = 0;
     int gemm_mutant = 0;
+    int moe_mutant = 0;
     int router_mutant = 0;
     int dattn_mutant = 0;
     uint32_t dattn_per_split = 0;

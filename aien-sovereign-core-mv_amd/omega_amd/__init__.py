@@ -195,6 +195,9 @@ SIGNATURES = {
     "omega_gpu_bf16_tensor_synth": (i32, [u32, u32, u64, u64, f32, C.POINTER(P)]),
     "omega_gpu_synth_bf16_host": (None, [u64, u64, C.c_size_t, f32, i32, P]),
     "omega_gpu_synth_bf16_dev": (i32, [P, u64, u64, u64, f32]),
+    "omega_gpu_moe_batch_f32": (i32, [P, u32, P, P, u32, P, f32, i32, P, P, P]),
+    "omega_gpu_moe_batch_dev": (i32, [P, u32, P, P, u32, P, f32, i32, P, P, P, P]),
+    "omega_gpu_moe_test_set_mutant": (None, [i32]),
     "omega_gpu_fp8_gemv_dev": (i32, [P, u32, P, P]),
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
@@ -785,6 +788,21 @@ class StreamTimer:
         v = C.c_float()
         assert hip().hipEventElapsedTime(C.byref(v), self.a, self.b) == 0
         return v.value
+
+
+def moe_batch(router, layer, gate_up, down, h, eps, norm_topk=True):
+    """The batched MoE block (omega_gpu_moe_batch_f32): h [T][2048] -> (moe_out [T][2048] without
+    the residual, ids [T][8], weights [T][8])."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    T = h.shape[0]
+    out = np.empty((T, 2048), np.float32)
+    ids = np.empty((T, 8), np.uint32)
+    w = np.empty((T, 8), np.float32)
+    rc = lib().omega_gpu_moe_batch_f32(router.as_raw(), layer, gate_up.as_raw(), down.as_raw(), T,
+                                       ptr(h), eps, int(norm_topk), ptr(ids), ptr(w), ptr(out))
+    if rc:
+        raise OmegaGpuError(rc, _s(lib().omega_gpu_fp8gemm_last_error()))
+    return out, ids, w
 
 
 def synth_bf16_dev(buf, count, seed, tensor_id, sigma=1.0, offset_bytes=0):

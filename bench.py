@@ -259,6 +259,93 @@ def bench_paged(om, args):
         "points": lines, "cpu_baseline": cpu}), flush=True)
 
 
+# ---------------------------------------------------------------- configuration 2: batched MoE block
+def moe_bytes(T, distinct):
+    """Algorithmic HBM bytes of one MoE block: the bf16 router, the e4m3 gate|up and down weights
+    and block scales of every distinct routed expert, h in, ids / weights / moe_out out."""
+    per_expert = 1536 * 2048 + 12 * 16 * 4 + 2048 * 768 + 16 * 6 * 4
+    return E * H * 2 + H * 4 + distinct * per_expert + T * H * 4 * 2 + T * TOPK * 8
+
+
+def moe_cpu_baseline(T, threads):
+    """The oracle's per-token route + FP8 MoE arm over T tokens (synthetic weights)."""
+    import pyoracle as orc
+
+    rng = np.random.default_rng(3)
+    gu_w, gu_s = orc.synth_fp8(SEED, 2, E, 2 * I, H)
+    dn_w, dn_s = orc.synth_fp8(SEED, 3, E, H, I)
+    gate = orc.f32_to_bf16((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    norm = np.ones(H, np.float32)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    t0 = time.perf_counter()
+    for t in range(T):
+        ids, w, post, _ = orc.route(gate, norm, h[t], 1e-6)
+        orc.moe_block(gu_w, gu_s, dn_w, dn_s, ids, w, post)
+    ms = (time.perf_counter() - t0) * 1e3
+    return {"value": round(ms, 2), "unit": "ms/block", "cores": 1, "kind": "port",
+            "sample": f"oracle route + oref_moe_block (oracle/oracle.c) for {T} tokens, one host "
+                      f"thread, synthetic weights of the same shapes"}
+
+
+def bench_moe(om, args):
+    """Configuration 2: one Qwen3-30B-A3B MoE block at token batch 1 and 32 (h ~ N(0,1) bf16,
+    router N(0, 0.02) bf16, experts e4m3 with 128x128 block scales), timed with HIP events on the
+    library stream over `moe_reps` calls with fresh inputs each (so the routed experts change)."""
+    import ctypes as C
+
+    router = om.Router(1)
+    rng = np.random.default_rng(SEED)
+    gate = om.synth_bf16_host(SEED, 9, (E, H), 0.02)
+    router.set_layer(0, gate, np.ones(H, np.float32))
+    router.set_directory(0, np.zeros(2 * E, np.uint64), np.zeros(2 * E, np.uint64))
+    gu = om.Fp8Tensor.synth(E, 2 * I, H, SEED, 2)
+    dn = om.Fp8Tensor.synth(E, H, I, SEED, 3)
+    lib = om.lib()
+    timer = om.StreamTimer()
+    lines = []
+    for T in (1, 32):
+        reps = args.moe_reps
+        hs = [om.DeviceBuffer.from_array(
+            om.synth_bf16_host(SEED, 500 + r, (T, H), 1.0).astype(np.uint32) << 16) for r in range(reps + 2)]
+        od = om.DeviceBuffer(T * H * 4)
+        idd = om.DeviceBuffer(T * TOPK * 4)
+        wd = om.DeviceBuffer(T * TOPK * 4)
+        times, distinct = [], []
+        for r in range(reps + 2):
+            timer.start()
+            rc = lib.omega_gpu_moe_batch_dev(router.as_raw(), 0, gu.as_raw(), dn.as_raw(), T, hs[r].ptr,
+                                             1e-6, 1, None, idd.ptr, wd.ptr, od.ptr)
+            assert rc == 0, om._s(lib.omega_gpu_fp8gemm_last_error())
+            timer.stop()
+            ms = timer.ms()
+            if r >= 2:
+                times.append(ms * 1e3)
+                distinct.append(len(np.unique(idd.download(np.uint32, T * TOPK))))
+        us = float(np.median(times))
+        d = float(np.mean(distinct))
+        b = moe_bytes(T, d)
+        line = {"workload": "moe_block", "tokens": T, "us_per_block": round(us, 2),
+                "distinct_experts": d, "algorithmic_bytes": int(b), "GBs": round(b / (us * 1e3), 1),
+                "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times),
+                "launches": 7}
+        print(json.dumps(line), flush=True)
+        lines.append(line)
+        for buf in hs + [od, idd, wd]:
+            buf.free()
+    cpu = None if args.no_cpu else moe_cpu_baseline(32, 1)
+    big = lines[-1]
+    print(json.dumps({
+        "metric": "Qwen3-30B-A3B MoE block (configuration 2) at token batch 32, achieved HBM GB/s vs peak",
+        "value": big["GBs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "fp8 (e4m3 weights, 3-term e4m3 activations, fp32 accumulate)",
+        "data": "synthetic random-init weights and bf16 N(0,1) rows",
+        "config": {"workload": "MoE block, 128 experts top-8, hidden 2048, intermediate 768",
+                   "tokens": [1, 32]},
+        "roofline": {"bound": "hbm", "kernel": "moe block (7 launches)", "achieved": big["GBs"],
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": big["frac"], "traffic": None},
+        "points": lines, "cpu_baseline": cpu}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -270,10 +357,12 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "paged"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "paged", "moe"], default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
-                         "paged: the paged-attention sweep (configuration 3)")
+                         "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
+                         "at token batch 1 and 32 (configuration 2)")
     ap.add_argument("--paged-reps", type=int, default=10)
+    ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES (byte-counter calibration)")
     args = ap.parse_args()
@@ -292,6 +381,9 @@ def main():
         return
     if args.workload == "paged":
         bench_paged(om, args)
+        return
+    if args.workload == "moe":
+        bench_moe(om, args)
         return
     total = args.prompt + args.warmup + args.steps + 8
     max_pos = om.round_max_pos(total)

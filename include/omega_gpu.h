@@ -511,6 +511,24 @@ int omega_gpu_decode_graph_read_routes(OmegaGpuDecodeGraph *g, uint32_t *ids, fl
 /* with stamps on: the duration (ns) of every launch of the last token, start to end of the
  * dispatch as the hardware recorded it (no launch gaps); returns launches or rc<0 */
 int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap);
+/* Batched MoE block (not in the reference ABI; the expert FFN of a decode step at token batch
+ * T <= 64, the reference's per-token FP8 arm qwen3_moe_omega.rs:4287-4318 batched): for each of
+ * `tokens` rows of h [T][2048] f32, RMSNorm with the router's layer weights, router logits, top-8
+ * (ids and weights bit-exact with the per-token route), then gate|up, SwiGLU and down of the
+ * routed experts grouped by expert on the FP8 matrix cores, combined in slot order:
+ * moe_out [T][2048] (no residual). Errors are reported by omega_gpu_fp8gemm_last_error. */
+int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const OmegaGpuFp8Tensor *gate_up,
+                            const OmegaGpuFp8Tensor *down, uint32_t tokens, const float *h, float eps,
+                            int norm_topk, uint32_t *ids, float *weights, float *moe_out);
+/* the same on device pointers, enqueued on the library's stream; out = resid + moe when resid_dev
+ * is not NULL (resid_dev may equal out_dev) */
+int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const OmegaGpuFp8Tensor *gate_up,
+                            const OmegaGpuFp8Tensor *down, uint32_t tokens, const float *h_dev, float eps,
+                            int norm_topk, const float *resid_dev, uint32_t *ids_dev, float *weights_dev,
+                            float *out_dev);
+/* test mutants of the batched MoE block: 1 rank mask on id^1, 2 weights not normalised, 5 gate and
+ * up swapped, 6 slot 7 dropped from the combine, 7 one activation term (a plain fp8 cast) */
+void omega_gpu_moe_test_set_mutant(int mutant);
 /* the library's HIP stream (hipStream_t) and a full synchronisation of it */
 void *omega_gpu_stream(void);
 int omega_gpu_sync(void);

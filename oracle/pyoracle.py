@@ -291,6 +291,17 @@ def route(gate_bf16, norm_w, x, eps: float, top_k: int = 8, refined: bool = True
     return ids, w, post, logits
 
 
+def moe_block(gu_w, gu_s, dn_w, dn_s, ids, weights, post, w8a8: bool = False):
+    """The engine's FP8 MoE arm for one token (oref_moe_block): moe_out without the residual."""
+    experts, n2, h = gu_w.shape
+    out = np.zeros(h, dtype=np.float32)
+    lib().oref_moe_block(ptr(gu_w), ptr(gu_s), ptr(dn_w), ptr(dn_s), experts, h, n2 // 2, len(ids),
+                         ptr(np.ascontiguousarray(ids, dtype=np.uint32)),
+                         ptr(np.ascontiguousarray(weights, dtype=np.float32)),
+                         ptr(np.ascontiguousarray(post, dtype=np.float32)), int(w8a8), ptr(out))
+    return out
+
+
 def swiglu(gu, i: int):
     act = np.empty(i, dtype=np.float32)
     lib().oref_swiglu(ptr(np.ascontiguousarray(gu, dtype=np.float32)), i, ptr(act))

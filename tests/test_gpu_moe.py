@@ -1,0 +1,119 @@
+"""GPU parity of the batched MoE block (configuration 2: Qwen3-30B-A3B MoE at token batch 1 and
+32) against the CPU oracle: per token the reference route (RMSNorm, f64-refined router logits,
+top-8 by total order, renormalised weights) and the engine's FP8 MoE arm (gate|up grouped GEMV,
+SwiGLU, down grouped GEMV, slot-order combine).
+
+Bars: expert ids bit-exact, weights within 1e-6 relative, moe_out within 2e-3 relative
+(max abs error over max abs value, per token). The GEMMs run on the FP8 matrix cores with the
+activations split into three e4m3 terms; the one-term mutant (a plain fp8 cast of the
+activations) must fail the 2e-3 bar, which shows the bar resolves the split's precision.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+SEED = 20261202
+E, H, I = 128, 2048, 768
+
+
+def rel_err(a, e):
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def model(omega, oracle):
+    rng = np.random.default_rng(5)
+    gu_w, gu_s = oracle.synth_fp8(SEED, 2, E, 2 * I, H)
+    dn_w, dn_s = oracle.synth_fp8(SEED, 3, E, H, I)
+    gu = omega.Fp8Tensor.synth(E, 2 * I, H, SEED, 2)
+    dn = omega.Fp8Tensor.synth(E, H, I, SEED, 3)
+    gate = oracle.f32_to_bf16((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    norm = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    r = omega.Router(1)
+    r.set_layer(0, gate, norm)
+    r.set_directory(0, np.zeros(2 * E, np.uint64), np.zeros(2 * E, np.uint64))
+    m = dict(gu_w=gu_w, gu_s=gu_s, dn_w=dn_w, dn_s=dn_s, gu=gu, dn=dn, gate=gate, norm=norm, router=r)
+    yield m
+    r.free()
+    gu.free()
+    dn.free()
+
+
+def oracle_block(oracle, m, h, eps=1e-6):
+    outs, ids, ws = [], [], []
+    for t in range(h.shape[0]):
+        i, w, post, _ = oracle.route(m["gate"], m["norm"], h[t], eps, refined=True)
+        outs.append(oracle.moe_block(m["gu_w"], m["gu_s"], m["dn_w"], m["dn_s"], i, w, post))
+        ids.append(i)
+        ws.append(w)
+    return np.stack(outs), np.stack(ids), np.stack(ws)
+
+
+def bf16_rows(oracle, rng, T):
+    return oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32)))
+
+
+@pytest.mark.parametrize("T", [1, 17, 32, 64])
+def test_moe_block_matches_the_oracle(omega, oracle, model, T):
+    h = bf16_rows(oracle, np.random.default_rng(100 + T), T)
+    out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    want, want_ids, want_w = oracle_block(oracle, model, h)
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_allclose(w, want_w, rtol=1e-6, atol=0)
+    errs = [rel_err(out[t], want[t]) for t in range(T)]
+    assert max(errs) <= TOL, (max(errs), int(np.argmax(errs)))
+    # deterministic: the same call again gives the same bits
+    out2, ids2, _ = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    np.testing.assert_array_equal(out2, out)
+    np.testing.assert_array_equal(ids2, ids)
+
+
+def test_crowded_experts_use_several_row_tiles(omega, oracle, model):
+    # 64 near-identical tokens route to the same experts: segments of up to 64 rows (4 MFMA
+    # column tiles of 16)
+    rng = np.random.default_rng(7)
+    base = rng.standard_normal(H).astype(np.float32)
+    h = bf16_rows(oracle, rng, 64) * 0.02 + base
+    h = oracle.bf16_to_f32(oracle.f32_to_bf16(h.astype(np.float32)))
+    out, ids, _ = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    want, want_ids, _ = oracle_block(oracle, model, h)
+    np.testing.assert_array_equal(ids, want_ids)
+    assert np.bincount(ids.reshape(-1), minlength=E).max() > 48
+    assert max(rel_err(out[t], want[t]) for t in range(64)) <= TOL
+
+
+def test_device_entry_adds_the_residual(omega, oracle, model):
+    T = 32
+    h = bf16_rows(oracle, np.random.default_rng(9), T)
+    out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    lib = omega.lib()
+    hd = omega.DeviceBuffer.from_array(h)
+    od = omega.DeviceBuffer(h.nbytes)
+    idd = omega.DeviceBuffer(T * 8 * 4)
+    wd = omega.DeviceBuffer(T * 8 * 4)
+    rc = lib.omega_gpu_moe_batch_dev(model["router"].as_raw(), 0, model["gu"].as_raw(),
+                                     model["dn"].as_raw(), T, hd.ptr, 1e-6, 1, hd.ptr, idd.ptr,
+                                     wd.ptr, od.ptr)
+    assert rc == 0
+    got = od.download(np.float32, T * H).reshape(T, H)
+    np.testing.assert_array_equal(idd.download(np.uint32, T * 8).reshape(T, 8), ids)
+    # the same moe rows, then one f32 add of the residual
+    np.testing.assert_array_equal(got, (h + out).astype(np.float32))
+
+
+@pytest.mark.parametrize("mutant", [1, 2, 5, 6, 7])
+def test_moe_mutants_are_caught(omega, oracle, model, mutant):
+    T = 32
+    h = bf16_rows(oracle, np.random.default_rng(11), T)
+    want, want_ids, want_w = oracle_block(oracle, model, h)
+    lib = omega.lib()
+    lib.omega_gpu_moe_test_set_mutant(mutant)
+    try:
+        out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    finally:
+        lib.omega_gpu_moe_test_set_mutant(0)
+    caught = (not np.array_equal(ids, want_ids) or
+              not np.allclose(w, want_w, rtol=1e-6, atol=0) or
+              max(rel_err(out[t], want[t]) for t in range(T)) > TOL)
+    assert caught
