@@ -389,6 +389,49 @@ hipError_t launch_bf16_synth_count(uint16_t *w, size_t count, uint64_t seed, uin
     return hipGetLastError();
 }
 
+// row-major e4m3 -> the tiled twin (runtime.hpp): one thread per 16 output bytes
+__global__ __launch_bounds__(256) void k_fp8_tile(const uint8_t *w, uint8_t *wt, uint32_t n, uint32_t k,
+                                                  size_t pieces) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    // output piece i: block b = i / 128, lane slot l = i % 64, half h = (i / 64) % 2
+    const size_t b = i >> 7;
+    const uint32_t h = (uint32_t)(i >> 6) & 1u, l = (uint32_t)i & 63u;
+    const uint32_t kbs = k / 128, rts = n / 16;
+    const uint32_t kb = (uint32_t)(b % kbs);
+    const size_t rt_all = b / kbs;  // expert * rts + rt
+    const uint32_t r = l & 15u, gq = l >> 4;
+    const size_t row = (rt_all / rts) * n + (rt_all % rts) * 16 + r;  // expert * n + 16 rt + r
+    const u32x4 v = *as_global(w + row * k + (size_t)kb * 128 + 64 * h + 16 * gq);
+    *reinterpret_cast<u32x4 *>(wt + i * 16) = v;
+}
+
+hipError_t launch_fp8_tile(const uint8_t *w, uint8_t *wt, uint32_t experts, uint32_t n, uint32_t k,
+                           hipStream_t st) {
+    const size_t pieces = (size_t)experts * n * k / 16;
+    hipLaunchKernelGGL(k_fp8_tile, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, w, wt, n, k, pieces);
+    return hipGetLastError();
+}
+
+// the tiled twin of t, built on first use (not while a graph is being captured: callers build
+// it before capture)
+int fp8_ensure_tiled(Family f, OmegaGpuFp8Tensor *t) {
+    if (t->wt) return OMEGA_GPU_OK;
+    Ctx *c = ctx(f);
+    if (!c) return OMEGA_GPU_CHIP_FAIL;
+    const size_t bytes = (size_t)t->experts * t->n * t->k;
+    OMEGA_HIP(f, hipMalloc(&t->wt, bytes));
+    hipError_t e = launch_fp8_tile(t->w, t->wt, t->experts, t->n, t->k, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(t->wt);
+        t->wt = nullptr;
+        set_error(f, "fp8 tiled twin: %s", hipGetErrorString(e));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    return OMEGA_GPU_OK;
+}
+
 // ---------------------------------------------------------------- host-side checks
 static int check_tensor_shape(Family f, uint32_t experts, uint32_t n, uint32_t k) {
     if (experts == 0 || n == 0 || n % 128 != 0 || k % 128 != 0 || k < 128 || k > 32768) {
@@ -591,6 +634,7 @@ void omega_gpu_fp8_tensor_free(OmegaGpuFp8Tensor *t) {
     if (c) (void)hipStreamSynchronize(c->stream);
     if (t->w) (void)hipFree(t->w);
     if (t->s) (void)hipFree(t->s);
+    if (t->wt) (void)hipFree(t->wt);
     delete t;
 }
 

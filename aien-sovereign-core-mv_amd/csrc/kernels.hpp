@@ -51,6 +51,8 @@ hipError_t launch_fp8_rows(const Fp8RowsArgs &a, int epi, int xsrc, hipStream_t 
 uint32_t fp8_rows_per_wave(uint32_t k);
 uint32_t fp8_rows_blocks(const Fp8RowsArgs &a);
 
+hipError_t launch_fp8_tile(const uint8_t *w, uint8_t *wt, uint32_t experts, uint32_t n, uint32_t k,
+                           hipStream_t st);
 hipError_t launch_fp8_synth(uint8_t *w, float *s, uint32_t experts, uint32_t n, uint32_t k,
                             uint64_t seed, uint64_t tensor, float sigma, hipStream_t st);
 // sets *flag when any byte is an e4m3 NaN (0x7f / 0xff)
@@ -193,9 +195,9 @@ struct MoeArgs {
     float eps = 1e-6f;
     int norm_topk = 1;
     uint32_t tokens = 0;
-    const uint8_t *gu_w = nullptr;     // [128][1536][2048] e4m3
+    const uint8_t *gu_wt = nullptr;    // [128][1536][2048] e4m3, tiled twin
     const float *gu_s = nullptr;       // [128][12][16]
-    const uint8_t *dn_w = nullptr;     // [128][2048][768] e4m3
+    const uint8_t *dn_wt = nullptr;    // [128][2048][768] e4m3, tiled twin
     const float *dn_s = nullptr;       // [128][16][6]
     const float *resid = nullptr;      // optional: out = resid + moe
     uint32_t *ids = nullptr;           // [T][8]
@@ -210,10 +212,11 @@ struct MoeArgs {
     uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
     uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row
-    float *act = nullptr;              // [T * 8][768] SwiGLU rows
-    uint8_t *aq = nullptr;             // [T * 8][6][3][128]
+    float *gp = nullptr;               // [8 k-slices][T * 8][1536] gate|up partial sums
+    uint8_t *aq = nullptr;             // [T * 8][6][3][128] split terms of the SwiGLU rows
     float *as = nullptr;               // [T * 8][6][4]
-    float *ydn = nullptr;              // [T * 8][2048] down rows
+    float *dp = nullptr;               // [3 k-slices][T * 8][2048] down partial sums
+    uint32_t nt[2] = {16, 8};          // tiles per wavefront (gate|up, down)
     int mutant = 0;  // 1: rank mask id^1; 2: weights not normalised; 5: gate/up swapped;
                      // 6: slot 7 dropped; 7: one activation term
 };

@@ -30,8 +30,6 @@ namespace omega {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kMH = 2048, kMI = 768, kME = 128, kTerms = 3;
-constexpr uint32_t kGuTiles = kMI / 16;   // 16 gate + 16 up features per wavefront
-constexpr uint32_t kDnTiles = kMH / 32;   // 32 down features per wavefront
 
 // ------------------------------------------------------------------ activation split
 // 2^(floor(log2 amax) - 7): amax / s lies in [128, 256), inside e4m3's range; a zero block gets 1
@@ -143,70 +141,81 @@ __global__ __launch_bounds__(64) void k_moe_router(const MoeArgs a) {
 // ------------------------------------------------------------------ 3. top-8 and the grouping (one workgroup)
 // Rows of the grouped GEMMs are (token, slot) pairs ordered by expert, then by pair index
 // (t * 8 + s) inside an expert; segments are the experts with rows, in ascending id.
-__global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
+__global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
+    constexpr uint32_t kWords = kMoeMaxTokens * kTopK / 32;
     __shared__ uint32_t sid[kMoeMaxTokens * kTopK];
-    __shared__ uint32_t cnt[kME], off[kME], segi[kME];
+    __shared__ uint32_t mask[kME][kWords];  // bit p of expert e: pair p routes to e
+    __shared__ uint32_t scan[2][kME];       // count | (count > 0) << 16, prefix-summed
+    __shared__ float lg[kMoeMaxTokens * kME];
     const uint32_t tid = threadIdx.x, lane = lane_id(), wid = tid >> 6;
     const uint32_t pairs = a.tokens * kTopK;
-    for (uint32_t t = wid; t < a.tokens; t += 4) {
+    for (uint32_t i = tid; i < kME * kWords; i += 1024) (&mask[0][0])[i] = 0u;
+    // every token's logits in one round trip, then the rankings from LDS: sixteen wavefronts (four
+    // per SIMD, so the ranking's dependent VALU chains of about 300 instructions per token
+    // overlap) in a rolled loop (small code)
+    for (uint32_t i = tid; i < a.tokens * kME; i += 1024) lg[i] = a.logits[i];
+    __syncthreads();
+    // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
+    const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
+#pragma unroll 1
+    for (uint32_t t = wid; t < a.tokens; t += 16) {
+        uint32_t k[kME / 64];
+#pragma unroll
+        for (uint32_t q = 0; q < kME / 64; ++q) k[q] = ord_key(lg[t * kME + lane + 64 * q]);
         Route r;
-        // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
-        route_topk<kME / 64>(a.logits + (size_t)t * kME, 0, a.norm_topk,
-                             a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0), r);
+        route_topk_keys<kME / 64>(k, a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
 #pragma unroll
         for (int s = 0; s < kTopK; ++s) {
             if (lane == (uint32_t)s) {
-                sid[t * kTopK + s] = r.id[s];
-                a.ids[t * kTopK + s] = r.id[s];
-                a.weights[t * kTopK + s] = r.w[s];
+                const uint32_t p = t * kTopK + s;
+                sid[p] = r.id[s];
+                a.ids[p] = r.id[s];
+                a.weights[p] = r.w[s];
+                atomicOr(&mask[r.id[s]][p >> 5], 1u << (p & 31));
             }
         }
     }
     __syncthreads();
+    // counts and the two prefix sums (rows, segments) over the experts: a log-step scan
     if (tid < kME) {
         uint32_t c = 0;
-        for (uint32_t p = 0; p < pairs; ++p) c += sid[p] == tid;
-        cnt[tid] = c;
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) c += __popc(mask[tid][w]);
+        scan[0][tid] = c | (c ? 1u << 16 : 0u);
     }
     __syncthreads();
-    if (tid == 0) {  // 128 prefix sums
-        uint32_t o = 0, sg = 0;
-        for (uint32_t e = 0; e < kME; ++e) {
-            off[e] = o;
-            segi[e] = sg;
-            o += cnt[e];
-            sg += cnt[e] ? 1u : 0u;
-        }
-        a.plan[0] = sg;  // segments
+    uint32_t src = 0;
+#pragma unroll
+    for (uint32_t d = 1; d < kME; d <<= 1) {
+        if (tid < kME) scan[src ^ 1][tid] = scan[src][tid] + (tid >= d ? scan[src][tid - d] : 0u);
+        src ^= 1;
+        __syncthreads();
     }
-    __syncthreads();
-    if (tid < kME) {
-        const uint32_t e = tid, c = cnt[e];
+    if (tid < kME) {  // inclusive sums -> this expert's row offset and segment index
+        const uint32_t incl = scan[src][tid];
+        const uint32_t own = scan[src][tid] - (tid ? scan[src][tid - 1] : 0u);
+        const uint32_t c = own & 0xffffu, off = (incl & 0xffffu) - c, sg = (incl >> 16) - (c ? 1u : 0u);
+        if (tid == kME - 1) a.plan[0] = incl >> 16;  // segments
         if (c) {
-            const uint32_t sg = segi[e];
-            a.seg_expert[sg] = e;
-            a.seg_start[sg] = off[e];
+            a.seg_expert[sg] = tid;
+            a.seg_start[sg] = off;
             a.seg_count[sg] = c;
-            uint32_t row = off[e];
-            for (uint32_t p = 0; p < pairs; ++p) {
-                if (sid[p] == e) {
-                    a.pair_row[p] = row;
-                    a.row_token[row] = p / kTopK;
-                    ++row;
-                }
-            }
         }
+    }
+    // every pair's row: its expert's offset plus the pairs before it on that expert
+    for (uint32_t p = tid; p < pairs; p += 1024) {
+        const uint32_t e = sid[p];
+        uint32_t rank = __popc(mask[e][p >> 5] & ((1u << (p & 31)) - 1u));
+        for (uint32_t w = 0; w < (p >> 5); ++w) rank += __popc(mask[e][w]);
+        const uint32_t incl = scan[src][e] & 0xffffu;
+        const uint32_t own = incl - (e ? (scan[src][e - 1] & 0xffffu) : 0u);
+        const uint32_t row = incl - own + rank;
+        a.pair_row[p] = row;
+        a.row_token[row] = p / kTopK;
     }
 }
 
 // ------------------------------------------------------------------ 4/6. grouped FP8 GEMM on the matrix cores
-__device__ __forceinline__ i32x8 ld32(const uint8_t *p) {
-    // bytes [0, 16) and [64, 80) of a 128-byte k-block piece at p: lane group g reads at 16 g, so
-    // every load instruction covers 64 contiguous bytes of each of the 16 rows
-    const u32x4 a = __builtin_nontemporal_load(as_global(p));
-    const u32x4 b = __builtin_nontemporal_load(as_global(p + 64));
-    return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
-}
 __device__ __forceinline__ i32x8 ld32_cached(const uint8_t *p) {
     const u32x4 a = *as_global(p);
     const u32x4 b = *as_global(p + 64);
@@ -216,132 +225,192 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b) {
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
 }
+// acc + A (e4m3) x (2^(sb - 127) B) (e4m3): the B scale is the E8M0 exponent of a power-of-two
+// activation term scale, the same in every lane of a column, so the k-to-lane mapping of the
+// scale blocks does not matter
+__device__ __forceinline__ f32x4 mfma_fp8_sb(const i32x8 &a, const i32x8 &b, const f32x4 &acc, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, sb);
+}
+// the E8M0 exponent of a power-of-two f32 scale (0: a dropped term, 2^-127)
+__device__ __forceinline__ int e8m0_of(float s) { return (int)((__float_as_uint(s) >> 23) & 0xff); }
 
-// tot[R][i] (feature 16 R + 4 g + i of the wavefront's tiles, column n) accumulates, per k-block,
-// ws[R][kb] * sum_t xs_t * (W_R q_t). KB k-blocks; A rows at w[R] (+ n * K, lane's row); the
-// weight scales at wsp[R][kb] (wave-uniform); B rows of the split activations at xq (row, kb,
-// term). One k-block of weights is in flight ahead of the math.
-template <int KB, int R>
-__device__ __forceinline__ void mfma_rows(const uint8_t *const (&w)[R], const float *const (&wsp)[R],
-                                          const uint8_t *xq, const float *xs, uint32_t xrow, uint32_t g,
-                                          f32x4 (&tot)[R]) {
-    const uint8_t *xr = xq + (size_t)xrow * KB * kTerms * 128 + 16 * g;
-    const float *sr = xs + (size_t)xrow * KB * 4;
-    i32x8 A[R];
+// Grouped GEMM on the matrix cores, one independent wavefront per (expert segment, run of NT
+// tiles, k-slice). A tile is 16 gate features j0..j0+15 and their 16 up features (gate|up) or 32
+// down features (down); a k-slice is KBW 128-column blocks. The wavefront loads its slice of the
+// segment's activation terms once per 16-row column tile, then streams its tiles' weights from
+// the tiled twin (each load instruction 1 KiB contiguous: a 16-rows x 64-bytes operand pattern on
+// row-major weights streams at about 4.8 TB/s against 6 TB/s contiguous), the next tile's in flight
+// while the current tile's products run, and stores the slice's partial sums. No wavefront waits for
+// another (HBM's tail latency would set every tile's pace through a barrier); the consumer adds
+// the k-slices in slice order: the SwiGLU + split kernel for gate|up, the combine for down.
+template <int EPI>  // 0: gate|up, 1: down
+struct MoeGemm {
+    static constexpr int KB = EPI == 0 ? kMH / 128 : kMI / 128;
+    static constexpr int KBW = 2;
+    static constexpr uint32_t SPLITS = KB / KBW;
+    static constexpr uint32_t K = KB * 128;
+    static constexpr uint32_t TILES = EPI == 0 ? kMI / 16 : kMH / 32;
+    static constexpr uint32_t NOUT = EPI == 0 ? 2 * kMI : kMH;  // partial row width
+    static_assert(KB % KBW == 0, "whole k-blocks per slice");
+};
+
+// one k-block of a 16-row tile from the tiled twin: the lane's two 16-byte pieces, each load
+// instruction 1 KiB contiguous
+__device__ __forceinline__ i32x8 ld_tile(const uint8_t *blk, uint32_t lane) {
+    const u32x4 a = __builtin_nontemporal_load(as_global(blk + 16 * lane));
+    const u32x4 b = __builtin_nontemporal_load(as_global(blk + 1024 + 16 * lane));
+    return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+}
+
+template <int KBW>
+struct MoeTileA {
+    i32x8 A[2][KBW];
+    // t0, t1: the twin's blocks of the two 16-row halves at the slice's first k-block
+    __device__ __forceinline__ void load(const uint8_t *t0, const uint8_t *t1, uint32_t lane) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) A[r] = ld32(w[r] + 16 * g);
+        for (int j = 0; j < KBW; ++j) {
+            A[0][j] = ld_tile(t0 + 2048 * j, lane);
+            A[1][j] = ld_tile(t1 + 2048 * j, lane);
+        }
+    }
+};
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
+    using G = MoeGemm<EPI>;
+    constexpr int KBW = G::KBW;
+    const uint32_t lane = lane_id(), g = lane >> 4, n = lane & 15;
+    const uint32_t nt = a.nt[EPI], groups = G::TILES / nt;
+    const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const uint32_t split = item % G::SPLITS, rest = item / G::SPLITS;
+    const uint32_t grp = rest % groups, seg = rest / groups;
+    if (seg >= a.plan[0]) return;
+    const uint32_t e = a.seg_expert[seg], r0 = a.seg_start[seg], cnt = a.seg_count[seg];
+    const uint32_t kb0 = split * KBW, t0 = grp * nt;
+    // the expert's tiled twin: (N / 16) row tiles of KB 2 KiB blocks
+    const uint8_t *wb = EPI == 0 ? a.gu_wt + (size_t)e * 2 * kMI * kMH : a.dn_wt + (size_t)e * kMH * kMI;
+    const float *sb = EPI == 0 ? a.gu_s + (size_t)e * (2 * kMI / 128) * G::KB
+                               : a.dn_s + (size_t)e * (kMH / 128) * G::KB;
+    const uint8_t *xq = EPI == 0 ? a.xq : a.aq;
+    const float *xs = EPI == 0 ? a.xs : a.as;
+    // first feature of the tile's two 16-row halves
+    auto f0 = [&](uint32_t t) { return EPI == 0 ? t * 16 : t * 32; };
+    auto f1 = [&](uint32_t t) { return EPI == 0 ? kMI + t * 16 : t * 32 + 16; };
+    // block (row tile of feature f, the slice's first k-block)
+    auto blk = [&](uint32_t f) { return wb + ((size_t)(f >> 4) * G::KB + kb0) * 2048; };
+    float *part = (EPI == 0 ? a.gp : a.dp) + (size_t)split * a.tokens * kTopK * G::NOUT;
+    for (uint32_t m0 = 0; m0 < cnt; m0 += 16) {
+        const bool valid = m0 + n < cnt;
+        const uint32_t row = r0 + (valid ? m0 + n : 0);
+        const uint32_t xrow = EPI == 0 ? a.row_token[row] : row;
+        MoeTileA<KBW> cur;
+        cur.load(blk(f0(t0)), blk(f1(t0)), lane);
+        // the column tile's activation terms for this slice
+        const uint8_t *xr = xq + ((size_t)xrow * G::KB + kb0) * kTerms * 128 + 16 * g;
+        const float *sr = xs + ((size_t)xrow * G::KB + kb0) * 4;
+        i32x8 B[KBW][kTerms];
+        int sbe[KBW][kTerms];  // the terms' E8M0 scales
+#pragma unroll
+        for (int j = 0; j < KBW; ++j) {
+#pragma unroll
+            for (uint32_t t = 0; t < kTerms; ++t) B[j][t] = ld32_cached(xr + (j * kTerms + t) * 128);
+            const f32x4 v = *as_global_f32x4(sr + 4 * j);
+            sbe[j][0] = e8m0_of(v.x);
+            sbe[j][1] = e8m0_of(v.y);
+            sbe[j][2] = e8m0_of(v.z);
+        }
+        float *prow = part + (size_t)row * G::NOUT + 4 * g;
 #pragma unroll 1
-    for (int kb = 0; kb < KB; ++kb) {
-        i32x8 An[R];
-        const int kn = kb + 1 < KB ? kb + 1 : kb;  // the last block reloads itself (in bounds, unused)
+        for (uint32_t i = 0; i < nt; ++i) {
+            const uint32_t tile = t0 + i, tn = i + 1 < nt ? tile + 1 : tile;  // the last reloads itself
+            MoeTileA<KBW> nxt;
+            nxt.load(blk(f0(tn)), blk(f1(tn)), lane);
+            const float *ws0 = sb + (size_t)(f0(tile) >> 7) * G::KB;
+            const float *ws1 = sb + (size_t)(f1(tile) >> 7) * G::KB;
+            f32x4 tot[2];
+            tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < R; ++r) An[r] = ld32(w[r] + 128 * kn + 16 * g);
-        i32x8 B[kTerms];
+            for (int j = 0; j < KBW; ++j) {
+                const float w0 = ws0[kb0 + j], w1 = ws1[kb0 + j];
+                f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (uint32_t t = 0; t < kTerms; ++t) B[t] = ld32_cached(xr + (kb * kTerms + t) * 128);
-        const f32x4 xsc = *as_global_f32x4(sr + kb * 4);
-        const float xsv[kTerms] = {xsc.x, xsc.y, xsc.z};
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float wsc = wsp[r][kb];
-#pragma unroll
-            for (uint32_t t = 0; t < kTerms; ++t) {
-                const f32x4 c = mfma_fp8(A[r], B[t]);
-                const float f = wsc * xsv[t];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) tot[r][i] = fmaf(c[i], f, tot[r][i]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) A[r] = An[r];
-    }
-}
-
-// gate|up: wavefront = (segment, 16 features j0..j0+15); gate rows j0 + n, up rows 768 + j0 + n
-__global__ __launch_bounds__(256) void k_moe_gate_up(const MoeArgs a) {
-    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
-    const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + wid);
-    const uint32_t seg = item / kGuTiles, tile = item % kGuTiles;
-    if (seg >= a.plan[0]) return;
-    const uint32_t e = a.seg_expert[seg], r0 = a.seg_start[seg], cnt = a.seg_count[seg];
-    const uint32_t j0 = tile * 16;
-    const uint8_t *we = a.gu_w + (size_t)e * 2 * kMI * kMH;
-    const uint8_t *w[2] = {we + (size_t)(j0 + n) * kMH, we + (size_t)(kMI + j0 + n) * kMH};
-    const float *se = a.gu_s + (size_t)e * (2 * kMI / 128) * (kMH / 128);
-    const float *ws[2] = {se + (j0 >> 7) * (kMH / 128), se + ((kMI + j0) >> 7) * (kMH / 128)};
-    for (uint32_t m0 = 0; m0 < cnt; m0 += 16) {
-        const bool valid = m0 + n < cnt;
-        const uint32_t row = r0 + (valid ? m0 + n : 0);
-        const uint32_t tok = a.row_token[row];
-        f32x4 tot[2];
-        tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        mfma_rows<kMH / 128, 2>(w, ws, a.xq, a.xs, tok, g, tot);
-        if (valid) {
-            float o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float gv = tot[0][i], uv = tot[1][i];
-                if (a.mutant == 5) {
-                    const float t = gv;
-                    gv = uv;
-                    uv = t;
+                for (uint32_t t = 0; t < kTerms; ++t) {
+                    c0 = mfma_fp8_sb(cur.A[0][j], B[j][t], c0, sbe[j][t]);
+                    c1 = mfma_fp8_sb(cur.A[1][j], B[j][t], c1, sbe[j][t]);
                 }
-                o[i] = gv / (1.0f + expf(-gv)) * uv;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    tot[0][q] = fmaf(c0[q], w0, tot[0][q]);
+                    tot[1][q] = fmaf(c1[q], w1, tot[1][q]);
+                }
             }
-            *reinterpret_cast<f32x4 *>(a.act + (size_t)row * kMI + j0 + 4 * g) = f32x4{o[0], o[1], o[2], o[3]};
+            if (valid) {
+                *reinterpret_cast<f32x4 *>(prow + f0(tile)) = tot[0];
+                *reinterpret_cast<f32x4 *>(prow + f1(tile)) = tot[1];
+            }
+            cur = nxt;
         }
     }
 }
 
-// the SwiGLU rows -> their split terms (one 16-lane row per 128-value block)
+// the gate|up k-slices summed in slice order, SwiGLU, then the split terms of the row (one
+// 16-lane row per 128-value block)
 __global__ __launch_bounds__(256) void k_moe_split_act(const MoeArgs a) {
+    using G = MoeGemm<0>;
     const uint32_t blk = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
+    const uint32_t rows = a.tokens * kTopK;
     const uint32_t row = blk / (kMI / 128), b = blk % (kMI / 128);
-    const bool live = row < a.tokens * kTopK;
-    const float *src = a.act + (size_t)(live ? row : 0) * kMI + 128 * b + 8 * j;
-    const f32x4 x0 = *as_global_f32x4(src), x1 = *as_global_f32x4(src + 4);
-    float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    u32x2 q[kTerms];
-    float s[kTerms];
-    split8(v, q, s, a.mutant == 7);  // every lane of the 16-lane row takes part (the block maximum)
-    if (live) store_split(a.aq, a.as, row, kMI / 128, b, j, q, s);
-}
-
-// down: wavefront = (segment, 32 features d0..d0+31 as two 16-row tiles)
-__global__ __launch_bounds__(256) void k_moe_down(const MoeArgs a) {
-    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
-    const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + wid);
-    const uint32_t seg = item / kDnTiles, tile = item % kDnTiles;
-    if (seg >= a.plan[0]) return;
-    const uint32_t e = a.seg_expert[seg], r0 = a.seg_start[seg], cnt = a.seg_count[seg];
-    const uint32_t d0 = tile * 32;
-    const uint8_t *we = a.dn_w + (size_t)e * kMH * kMI;
-    const uint8_t *w[2] = {we + (size_t)(d0 + n) * kMI, we + (size_t)(d0 + 16 + n) * kMI};
-    const float *se = a.dn_s + ((size_t)e * (kMH / 128) + (d0 >> 7)) * (kMI / 128);
-    const float *ws[2] = {se, se};
-    for (uint32_t m0 = 0; m0 < cnt; m0 += 16) {
-        const bool valid = m0 + n < cnt;
-        const uint32_t row = r0 + (valid ? m0 + n : 0);
-        f32x4 tot[2];
-        tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        mfma_rows<kMI / 128, 2>(w, ws, a.aq, a.as, row, g, tot);
-        if (valid) {
-            float *y = a.ydn + (size_t)row * kMH + d0 + 4 * g;
-            *reinterpret_cast<f32x4 *>(y) = tot[0];
-            *reinterpret_cast<f32x4 *>(y + 16) = tot[1];
+    const bool live = row < rows;
+    const size_t slice = (size_t)rows * G::NOUT;
+    const float *src = a.gp + (size_t)(live ? row : 0) * G::NOUT + 128 * b + 8 * j;
+    float gv[8], uv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) gv[i] = uv[i] = 0.f;
+#pragma unroll
+    for (uint32_t s = 0; s < G::SPLITS; ++s) {
+        const float *p = src + s * slice;
+        const f32x4 g0 = *as_global_f32x4(p), g1 = *as_global_f32x4(p + 4);
+        const f32x4 u0 = *as_global_f32x4(p + kMI), u1 = *as_global_f32x4(p + kMI + 4);
+        const float gs[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float us[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            gv[i] += gs[i];
+            uv[i] += us[i];
         }
     }
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float gg = gv[i], uu = uv[i];
+        if (a.mutant == 5) {
+            const float t = gg;
+            gg = uu;
+            uu = t;
+        }
+        v[i] = gg / (1.0f + expf(-gg)) * uu;
+    }
+    u32x2 q[kTerms];
+    float sc[kTerms];
+    split8(v, q, sc, a.mutant == 7);  // every lane of the 16-lane row takes part (the block maximum)
+    if (live) store_split(a.aq, a.as, row, kMI / 128, b, j, q, sc);
 }
 
 // ------------------------------------------------------------------ 7. combine (slot order from zero) [+ residual]
+// each slot's down row is its k-slices summed in slice order
 __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
+    using G = MoeGemm<1>;
     const uint32_t t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
+    const size_t slice = (size_t)a.tokens * kTopK * kMH;
     float moe = 0.f;
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
         const uint32_t row = a.pair_row[t * kTopK + s];
         const float w = (a.mutant == 6 && s == kTopK - 1) ? 0.f : a.weights[t * kTopK + s];
-        moe += w * a.ydn[(size_t)row * kMH + c];
+        float y = 0.f;
+#pragma unroll
+        for (uint32_t k = 0; k < G::SPLITS; ++k) y += a.dp[k * slice + (size_t)row * kMH + c];
+        moe += w * y;
     }
     const size_t o = (size_t)t * kMH + c;
     a.out[o] = a.resid ? a.resid[o] + moe : moe;
@@ -352,10 +421,12 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
     const uint32_t segs_max = P < kME ? P : kME;
     OMEGA_LAUNCH(k_moe_prep, dim3(T), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_router, dim3(kME, (T + 3) / 4), dim3(64), 0, st, a);
-    OMEGA_LAUNCH(k_moe_plan, dim3(1), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_gate_up, dim3((segs_max * kGuTiles + 3) / 4), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_moe_plan, dim3(1), dim3(1024), 0, st, a);
+    const uint32_t w0 = segs_max * (MoeGemm<0>::TILES / a.nt[0]) * MoeGemm<0>::SPLITS;
+    const uint32_t w1 = segs_max * (MoeGemm<1>::TILES / a.nt[1]) * MoeGemm<1>::SPLITS;
+    OMEGA_LAUNCH(k_moe_gemm<0>, dim3((w0 + 3) / 4), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_split_act, dim3((P * (kMI / 128) + 15) / 16), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_down, dim3((segs_max * kDnTiles + 3) / 4), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_moe_gemm<1>, dim3((w1 + 3) / 4), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -384,10 +455,13 @@ size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens) {
     a.seg_count = reinterpret_cast<uint32_t *>(take(kME * 4));
     a.pair_row = reinterpret_cast<uint32_t *>(take(P * 4));
     a.row_token = reinterpret_cast<uint32_t *>(take(P * 4));
-    a.act = reinterpret_cast<float *>(take(P * kMI * 4));
+    a.gp = reinterpret_cast<float *>(take(MoeGemm<0>::SPLITS * P * MoeGemm<0>::NOUT * 4));
     a.aq = take(P * (kMI / 128) * kTerms * 128);
     a.as = reinterpret_cast<float *>(take(P * (kMI / 128) * 16));
-    a.ydn = reinterpret_cast<float *>(take(P * kMH * 4));
+    a.dp = reinterpret_cast<float *>(take(MoeGemm<1>::SPLITS * P * MoeGemm<1>::NOUT * 4));
+    // tiles per wavefront: long runs once there are segments enough to fill the chip
+    a.nt[0] = tokens >= 8 ? 16 : 2;
+    a.nt[1] = tokens >= 8 ? 8 : 2;
     return o;
 }
 
@@ -436,9 +510,9 @@ MoeArgs moe_args(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tenso
     a.eps = eps;
     a.norm_topk = norm_topk;
     a.tokens = tokens;
-    a.gu_w = gu->w;
+    a.gu_wt = gu->wt;
     a.gu_s = gu->s;
-    a.dn_w = dn->w;
+    a.dn_wt = dn->wt;
     a.dn_s = dn->s;
     a.mutant = knobs().moe_mutant;
     return a;
@@ -455,6 +529,8 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     clear_error(F_GEMM);
     int rc = moe_check(router, layer, gate_up, down, tokens);
+    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
+    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
     if (rc) return rc;
     if (!h_dev || !ids_dev || !weights_dev || !out_dev) {
         set_error(F_GEMM, "moe batch dev: NULL pointer");
@@ -482,6 +558,8 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     clear_error(F_GEMM);
     int rc = moe_check(router, layer, gate_up, down, tokens);
+    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
+    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
     if (rc) return rc;
     if (!h || !ids || !weights || !moe_out) {
         set_error(F_GEMM, "moe batch: NULL pointer");

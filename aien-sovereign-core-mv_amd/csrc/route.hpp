@@ -49,16 +49,22 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return xor_max_u32<32>(v);
 }
 
-// logits: Q * 64 expert values (+1 shared) in global memory.
-// mutant 2: the mask after a pick hits id ^ 1; mutant 4: weights not normalised.
+// the ranking keys of Q * 64 logits: lane l holds experts l + 64 q
 template <int Q>
-__device__ __forceinline__ void route_topk(const float *logits, uint32_t shared, int norm_topk,
-                                           int mutant, Route &r) {
-    constexpr uint32_t experts = 64 * Q;
+__device__ __forceinline__ void route_keys(const float *logits, uint32_t (&k)[Q]) {
     const uint32_t lane = lane_id();
-    uint32_t k[Q];  // expert lane + 64 q
 #pragma unroll
     for (int q = 0; q < Q; ++q) k[q] = ord_key(*as_global_f32(logits + lane + 64 * q));
+}
+
+// logits: Q * 64 expert values (+1 shared) in global memory, their keys already loaded (the
+// keys are consumed).
+// mutant 2: the mask after a pick hits id ^ 1; mutant 4: weights not normalised.
+template <int Q>
+__device__ __forceinline__ void route_topk_keys(uint32_t (&k)[Q], const float *logits, uint32_t shared,
+                                                int norm_topk, int mutant, Route &r) {
+    constexpr uint32_t experts = 64 * Q;
+    const uint32_t lane = lane_id();
     float v[kTopK];
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
@@ -98,6 +104,14 @@ __device__ __forceinline__ void route_topk(const float *logits, uint32_t shared,
         r.id[kTopK] = experts;
         r.w[kTopK] = 1.0f / (1.0f + expf(-*as_global_f32(logits + experts)));
     }
+}
+
+template <int Q>
+__device__ __forceinline__ void route_topk(const float *logits, uint32_t shared, int norm_topk,
+                                           int mutant, Route &r) {
+    uint32_t k[Q];
+    route_keys<Q>(logits, k);
+    route_topk_keys<Q>(k, logits, shared, norm_topk, mutant, r);
 }
 
 }  // namespace omega

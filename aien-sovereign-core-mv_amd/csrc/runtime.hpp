@@ -110,11 +110,22 @@ Knobs &knobs();
 // ---------------------------------------------------------------------------- object layouts
 // Device layout of an FP8 tensor: row-major e4m3 bytes [experts][n][k] (a wavefront streams
 // whole rows), scales f32 [experts][n/128][k/128].
+// The matrix-core kernels of the batched paths read a tiled twin of the same bytes (built once on
+// the device, on first batched use): block (expert, 16-row tile rt, 128-column block kb) is 2 KiB
+// at ((expert * n/16 + rt) * k/128 + kb) * 2048, and inside it byte (row r, column c) sits at
+// (c / 64) * 1024 + ((c % 64) / 16 * 16 + r) * 16 + c % 16 — the FP8 MFMA operand order, so each
+// operand load instruction of a wavefront reads 1 KiB contiguous.
 struct OmegaGpuFp8Tensor {
     uint32_t experts = 0, n = 0, k = 0;
     uint8_t *w = nullptr;
     float *s = nullptr;
+    uint8_t *wt = nullptr;  // tiled twin (batched matrix-core paths), or null until first needed
 };
+
+namespace omega {
+// builds t's tiled twin when it has none (synchronises the library stream; not during capture)
+int fp8_ensure_tiled(Family f, OmegaGpuFp8Tensor *t);
+}  // namespace omega
 
 // Device layout of a bf16 tensor: row-major [n][k] (n_pad == n).
 struct OmegaGpuBf16Tensor {

@@ -14,7 +14,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-LIB_PATH = os.path.join(PKG, "_build", "libomega_gpu.so")
+# OMEGA_GPU_LIB selects another build of the same library (a tuning variant); default: in-tree
+LIB_PATH = os.environ.get("OMEGA_GPU_LIB") or os.path.join(PKG, "_build", "libomega_gpu.so")
 
 _lib = None
 
