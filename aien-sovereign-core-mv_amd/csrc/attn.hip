@@ -29,6 +29,7 @@
 
 #include "device.hpp"
 #include "kernels.hpp"
+#include "mfma.hpp"
 #include "runtime.hpp"
 
 namespace omega {
@@ -36,7 +37,6 @@ namespace omega {
 constexpr float kInvSqrt128 = 0.08838834764831845f;
 constexpr uint32_t kVtHead = 4096;  // bytes per kv head of a transposed V plane (128 dims x 32 B)
 
-__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));  // a 16x16x16 bf16 operand
 
@@ -60,20 +60,6 @@ __device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint3
     for (int nb = 0; nb < 8; ++nb) T.v[nb] = __builtin_nontemporal_load(as_global_u32x2(vp + nb * 16 * 32));
 }
 
-// RMSNorm (given the head's scale) then RoPE of one head held as (dims lane, lane + 64)
-__device__ __forceinline__ void head_scale_rope(float &v0, float &v1, float scale, float w0, float w1, float rc,
-                                                float rs, bool rope) {
-    float n0 = v0 * scale * w0;
-    float n1 = v1 * scale * w1;
-    if (rope) {
-        const float r0 = __fsub_rn(__fmul_rn(n0, rc), __fmul_rn(n1, rs));
-        const float r1 = __fadd_rn(__fmul_rn(n0, rs), __fmul_rn(n1, rc));
-        n0 = r0;
-        n1 = r1;
-    }
-    v0 = n0;
-    v1 = n1;
-}
 
 // One online-softmax step over a page whose first token is tok0 (< pos). The online state of
 // head n % 8 (m, l) sits in every lane of column n; O[nb][i] is row 4 g + i (head (4 g + i) % 8,
@@ -301,8 +287,15 @@ struct PagedRegs {
     u32x4 v[4];  // V rows: piece j is token 4 j + lane / 16, dims 8 (lane % 16) .. +8
 };
 
+// the pool's layer slice as the page loop sees it
+struct PagedSrc {
+    const uint8_t *pool;
+    KvGeom g;
+    uint32_t layer;
+};
+
 template <int MUT>
-__device__ __forceinline__ void paged_load(const AttnArgs &a, const int32_t *tab, uint32_t blk, uint32_t h,
+__device__ __forceinline__ void paged_load(const PagedSrc &a, const int32_t *tab, uint32_t blk, uint32_t h,
                                            uint32_t page, uint32_t ctx, uint32_t lane, PagedRegs &R) {
     const uint32_t g = lane >> 4, n = lane & 15;
     const uint8_t *pg = a.pool + (uint64_t)blk * a.g.block_stride + (uint64_t)a.layer * a.g.layer_stride;
@@ -350,32 +343,15 @@ __device__ __forceinline__ void paged_stage_v(const PagedRegs &R, uint32_t tok0,
     for (int ks = 0; ks < 4; ++ks) T.k[ks] = R.k[ks];
 }
 
-template <int MUT>
-__global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
-    __shared__ __align__(16) uint16_t qhl[2][8][128];  // the 8 q heads: bf16 hi, lo halves
-    __shared__ __align__(16) uint8_t vt[16 * kVtRow];  // one staged V tile
-    const uint32_t lane = threadIdx.x, h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+// The 8 q heads of kv head h (f32 rows q[8][128]) as the bf16 hi/lo B operand of S^T = K q^T.
+__device__ __forceinline__ void paged_q(const float *q, uint32_t lane, uint16_t (*qhl)[8][128], bf16x8 (&qop)[4]) {
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t ctx = (uint32_t)a.context_lens[b];
-    const uint32_t pages = (ctx + 15) / 16;
-    uint32_t active, pps;
-    attn_split_plan(pages, a.splits, 0, active, pps);
-    if (c >= active) return;
-    const uint32_t p_begin = c * pps, p_end = min(pages, p_begin + pps);
-    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
-    // the split's page ids, 64 at a time (lane i: page base + i)
-    uint32_t tbase = p_begin;
-    int32_t tl = tab[min(tbase + lane, pages - 1)];
-    const float *q = a.q + ((size_t)b * a.qh + h * 8) * 128;
     float q0[8], q1[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         q0[r] = *as_global_f32(q + r * 128 + lane);
         q1[r] = *as_global_f32(q + r * 128 + 64 + lane);
     }
-    PagedRegs R;
-    paged_load<MUT>(a, tab, (uint32_t)__builtin_amdgcn_readfirstlane(tl), h, p_begin, ctx, lane, R);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         qhl[0][r][lane] = bf16_split_hi(q0[r]);
@@ -384,18 +360,30 @@ __global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
         qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
     }
     __syncthreads();
-    bf16x8 qop[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
         qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[n >> 3][n & 7][32 * ks + 8 * g]));
+}
 
-    float m_l = -INFINITY, l_l = 0.f;
-    f32x4 O[8];
+// Pages [p_begin, p_end) of a sequence of `ctx` tokens (table tab): the online softmax of the 8 q
+// heads of kv head h. The split's page ids are read 64 at a time into one VGPR and taken by
+// readlane, so no page load waits on a table load; the next page's loads go out before this
+// page's math.
+template <int MUT>
+__device__ __forceinline__ void paged_pages(const PagedSrc &src, const int32_t *tab, uint32_t h, uint32_t p_begin,
+                                            uint32_t p_end, uint32_t pages, uint32_t ctx, const bf16x8 (&qop)[4],
+                                            uint8_t *vt, uint32_t lane, float &m_l, float &l_l, f32x4 (&O)[8]) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    uint32_t tbase = p_begin;
+    int32_t tl = tab[min(tbase + lane, pages - 1)];
+    PagedRegs R;
+    paged_load<MUT>(src, tab, (uint32_t)__builtin_amdgcn_readfirstlane(tl), h, p_begin, ctx, lane, R);
+    m_l = -INFINITY;
+    l_l = 0.f;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     DattnPage T;
     for (uint32_t p = p_begin; p < p_end; ++p) {
-        // the next page's loads go out before this page's math
         PagedRegs nx;
         const bool more = p + 1 < p_end;
         if (more) {
@@ -404,27 +392,85 @@ __global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
                 tl = tab[min(tbase + lane, pages - 1)];
             }
             const uint32_t nblk = (uint32_t)__builtin_amdgcn_readlane(tl, p + 1 - tbase);
-            paged_load<MUT>(a, tab, nblk, h, p + 1, ctx, lane, nx);
+            paged_load<MUT>(src, tab, nblk, h, p + 1, ctx, lane, nx);
         }
         paged_stage_v(R, p * 16, ctx, lane, vt, T);
         if (p == p_begin) dattn_page<true>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
         else dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
         if (more) R = nx;
     }
+}
+
+// The split's partial (m, l, o[128]) of the 8 heads: head r at part + r * stride floats.
+__device__ __forceinline__ void paged_store(float *part, size_t stride, uint32_t lane, float m_l, float l_l,
+                                            const f32x4 (&O)[8]) {
+    const uint32_t g = lane >> 4, n = lane & 15;
     // rows 4 g + i: hi half of head 4 g + i (g < 2) or lo half (g >= 2); see k_dattn
     const uint32_t hg = g & 1, nb_off = (g >> 1) * 4;
-    float *part = a.part + (((size_t)b * a.qh + h * 8) * a.splits + c) * kPartStride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float *pp = part + (size_t)(4 * hg + i) * a.splits * kPartStride;
+        float *pp = part + (size_t)(4 * hg + i) * stride;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) pp[4 + 16 * (nb + nb_off) + n] = pair_sum<32>(O[nb][i], O[nb + 4][i]);
     }
     if (lane < 8) {  // lane r holds head r's running max and sum
-        float *pp = part + (size_t)lane * a.splits * kPartStride;
+        float *pp = part + (size_t)lane * stride;
         pp[0] = m_l;
         pp[1] = l_l;
     }
+}
+
+template <int MUT>
+__global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
+    __shared__ __align__(16) uint16_t qhl[2][8][128];  // the 8 q heads: bf16 hi, lo halves
+    __shared__ __align__(16) uint8_t vt[16 * kVtRow];  // one staged V tile
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint32_t ctx = (uint32_t)a.context_lens[b];
+    const uint32_t pages = (ctx + 15) / 16;
+    uint32_t active, pps;
+    attn_split_plan(pages, a.splits, 0, active, pps);
+    if (c >= active) return;
+    const uint32_t p_begin = c * pps, p_end = min(pages, p_begin + pps);
+    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
+    bf16x8 qop[4];
+    paged_q(a.q + ((size_t)b * a.qh + h * 8) * 128, lane, qhl, qop);
+    const PagedSrc src{a.pool, a.g, a.layer};
+    float m_l, l_l;
+    f32x4 O[8];
+    paged_pages<MUT>(src, tab, h, p_begin, p_end, pages, ctx, qop, vt, lane, m_l, l_l, O);
+    paged_store(a.part + (((size_t)b * a.qh + h * 8) * a.splits + c) * kPartStride, (size_t)a.splits * kPartStride,
+                lane, m_l, l_l, O);
+}
+
+// Ragged work items (the batched decode step): item i of the launch is split i - item_off[s] of
+// sequence s (item_off[s] <= i < item_off[s + 1]), pages [split * pps_s, +pps_s) of its
+// pos_s + 1 tokens; partials at part[(i * 32 + q head) * kPartStride]. The grid loops over the
+// items (a fixed grid serves every step of a captured graph).
+__global__ __launch_bounds__(64) void k_paged_items(const PagedItemsArgs a) {
+    __shared__ __align__(16) uint16_t qhl[2][8][128];
+    __shared__ __align__(16) uint8_t vt[16 * kVtRow];
+    const uint32_t lane = threadIdx.x, h = blockIdx.x;
+    const uint32_t total = a.item_off[a.seqs];
+    const PagedSrc src{a.pool, a.g, a.layer};
+    for (uint32_t it = blockIdx.y; it < total; it += gridDim.y) {
+        uint32_t s = 0;
+        while (s + 1 < a.seqs && a.item_off[s + 1] <= it) ++s;
+        const uint32_t ctx = a.pos[s] + 1, pages = (ctx + 15) / 16, pps = a.pps[s];
+        const uint32_t p_begin = (it - a.item_off[s]) * pps, p_end = min(pages, p_begin + pps);
+        __syncthreads();  // the previous item's LDS reads are done
+        bf16x8 qop[4];
+        paged_q(a.q + ((size_t)s * 32 + h * 8) * 128, lane, qhl, qop);
+        float m_l, l_l;
+        f32x4 O[8];
+        paged_pages<0>(src, a.tables + (size_t)s * a.max_blocks, h, p_begin, p_end, pages, ctx, qop, vt, lane, m_l,
+                       l_l, O);
+        paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
+    }
+}
+
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t grid_items, hipStream_t st) {
+    OMEGA_LAUNCH(k_paged_items, dim3(4, grid_items), dim3(64), 0, st, a);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------------ paged (VALU)
@@ -619,6 +665,69 @@ __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
     if (a.splits > 64) OMEGA_LAUNCH(k_attn_combine<4>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
     else OMEGA_LAUNCH(k_attn_combine<1>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+// The ragged splits of every (seq, q head) combined, then split into the o projection's e4m3
+// terms (the head's 128 dims are one 128-column block of o's input). Workgroup = (seq, head),
+// wavefront q = dims 32 q .. 32 q + 31 of up to 256 splits (the k_attn_combine<4> pattern); the
+// head's row meets in LDS and 16 lanes split it.
+__global__ __launch_bounds__(256) void k_attn_combine_items(const CombineItemsArgs a) {
+    constexpr int CH = 4;
+    __shared__ float wsh[4][64 * CH];
+    __shared__ float orow[128];
+    const uint32_t s = blockIdx.x >> 5, head = blockIdx.x & 31;
+    const uint32_t lane = lane_id(), quarter = threadIdx.x >> 6;
+    const uint32_t d = 32 * quarter + (lane & 31), half = lane >> 5;
+    const uint32_t off = a.item_off[s], splits = a.item_off[s + 1] - off;  // 1 ..= 256
+    auto slot = [&](uint32_t j) { return a.part + ((size_t)(off + min(j, splits - 1)) * 32 + head) * kPartStride; };
+    float m_raw[CH], l_raw[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        m_raw[c] = *as_global_f32(slot(64 * c + lane));
+        l_raw[c] = *as_global_f32(slot(64 * c + lane) + 1);
+    }
+    constexpr uint32_t kPer = 32 * CH;
+    float f[kPer];
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) f[k] = *as_global_f32(slot(2 * k + half) + 4 + d);
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) M = fmaxf(M, 64 * c + lane < splits ? m_raw[c] : -INFINITY);
+    M = row16_max(M);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    float L = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const bool mine = 64 * c + lane < splits;
+        const float w = mine ? expf(m_raw[c] - M) : 0.f;
+        L += wave_sum(w * (mine ? l_raw[c] : 0.f));
+        wsh[quarter][64 * c + lane] = w;
+    }
+    __syncthreads();
+    float O = 0.f;
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; ++k) {
+        const uint32_t j = 2 * k + half;
+        O = j < splits ? fmaf(f[k], wsh[quarter][j], O) : O;
+    }
+    O = xor_sum<32>(O);
+    if (lane < 32) orow[d] = O / L;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const uint32_t j = threadIdx.x;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = orow[8 * j + i];
+        u32x2 q[kTerms];
+        float sc[kTerms];
+        split8(v, q, sc, false);
+        store_split(a.oq, a.os, s, 32, head, j, q, sc);
+    }
+}
+
+hipError_t launch_attn_combine_items(const CombineItemsArgs &a, uint32_t seqs, hipStream_t st) {
+    OMEGA_LAUNCH(k_attn_combine_items, dim3(seqs * 32), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -20,15 +20,6 @@
 
 namespace omega {
 
-// order-preserving key: larger value wins, then the lower index; NaN never beats a number
-__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-    uint32_t ord = 0;
-    if (v == v) {
-        const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0
-        ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    }
-    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
-}
 
 uint32_t argmax_from_slots(const unsigned long long *slots) {
     unsigned long long best = 0;
@@ -250,6 +241,46 @@ static int bf16_run(const OmegaGpuBf16Tensor *t, const float *x, float *y, Omega
 
 }  // namespace omega
 
+namespace omega {
+// row-major bf16 -> the tiled twin (runtime.hpp): one thread per 16 output bytes (8 elements)
+__global__ __launch_bounds__(256) void k_bf16_tile(const uint16_t *w, uint16_t *wt, uint32_t n, uint32_t k,
+                                                   size_t pieces) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    const size_t b = i >> 6;  // 64 pieces of 16 B per 1 KiB block
+    const uint32_t l = (uint32_t)i & 63u, r = l & 15u, gq = l >> 4;
+    const uint32_t kbs = k / 32;
+    const size_t rt = b / kbs;
+    const uint32_t kb = (uint32_t)(b % kbs);
+    const size_t row = rt * 16 + r;
+    const u32x4 v = *as_global(w + row * k + (size_t)kb * 32 + 8 * gq);
+    *reinterpret_cast<u32x4 *>(wt + i * 8) = v;
+}
+
+int bf16_ensure_tiled(Family f, OmegaGpuBf16Tensor *t) {
+    if (t->wt) return OMEGA_GPU_OK;
+    if (t->n % 16 != 0 || t->k % 32 != 0) {
+        set_error(f, "bf16 tiled twin: %u x %u is not whole 16 x 32 blocks", t->n, t->k);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    Ctx *c = ctx(f);
+    if (!c) return OMEGA_GPU_CHIP_FAIL;
+    const size_t elems = (size_t)t->n * t->k, pieces = elems / 8;
+    OMEGA_HIP(f, hipMalloc(&t->wt, elems * 2));
+    hipLaunchKernelGGL(k_bf16_tile, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, c->stream, t->w, t->wt,
+                       t->n, t->k, pieces);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(t->wt);
+        t->wt = nullptr;
+        set_error(f, "bf16 tiled twin: %s", hipGetErrorString(e));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    return OMEGA_GPU_OK;
+}
+}  // namespace omega
+
 using namespace omega;
 
 extern "C" {
@@ -326,6 +357,7 @@ void omega_gpu_bf16_tensor_free(OmegaGpuBf16Tensor *t) {
     Ctx *c = ctx(F_BF16);
     if (c) (void)hipStreamSynchronize(c->stream);
     if (t->w) (void)hipFree(t->w);
+    if (t->wt) (void)hipFree(t->wt);
     delete t;
 }
 

@@ -48,6 +48,7 @@ __device__ __forceinline__ const gf32x4 *as_global_f32x4(const void *p) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // ------------------------------------------------------------------ reductions
 template <int CTRL>
@@ -238,6 +239,33 @@ __device__ __forceinline__ uint64_t kv_row_offset(const KvGeom &g, uint32_t bloc
     return (uint64_t)block * g.block_stride + (uint64_t)layer * g.layer_stride +
            (uint64_t)plane * g.plane_stride + (uint64_t)token * g.token_stride +
            (uint64_t)head * g.head_stride;
+}
+
+// argmax key: larger value wins, then the lower index (sample_argmax's strict scan,
+// crates/aien-inference-abi/src/tensor.rs:299-318); NaN never beats a number. An integer max of
+// keys is order-independent, so fire-and-forget atomicMax slots give a deterministic argmax.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+    uint32_t ord = 0;
+    if (v == v) {
+        const uint32_t u = __float_as_uint(v + 0.0f);  // -0 -> +0
+        ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    }
+    return ((unsigned long long)ord << 32) | (unsigned long long)(0xffffffffu - idx);
+}
+
+// RMSNorm (given the head's scale) then RoPE of one head held as (dims lane, lane + 64)
+__device__ __forceinline__ void head_scale_rope(float &v0, float &v1, float scale, float w0, float w1, float rc,
+                                                float rs, bool rope) {
+    float n0 = v0 * scale * w0;
+    float n1 = v1 * scale * w1;
+    if (rope) {
+        const float r0 = __fsub_rn(__fmul_rn(n0, rc), __fmul_rn(n1, rs));
+        const float r1 = __fadd_rn(__fmul_rn(n0, rs), __fmul_rn(n1, rc));
+        n0 = r0;
+        n1 = r1;
+    }
+    v0 = n0;
+    v1 = n1;
 }
 
 // RMSNorm scale with the f64 sum of squares (tensor.rs:94-110)

@@ -200,12 +200,15 @@ struct MoeArgs {
     const uint8_t *dn_wt = nullptr;    // [128][2048][768] e4m3, tiled twin
     const float *dn_s = nullptr;       // [128][16][6]
     const float *resid = nullptr;      // optional: out = resid + moe
+    const float *opart = nullptr;      // optional: h += sum of oslices k-slices [oslices][T][2048]
+    uint32_t oslices = 0;              //   (the o projection's partials), stored to hout
+    float *hout = nullptr;
     uint32_t *ids = nullptr;           // [T][8]
     float *weights = nullptr;          // [T][8]
     float *out = nullptr;              // [T][2048]
     // workspace (moe_work_carve)
     float *xn = nullptr;               // [T][2048] x'
-    uint8_t *xq = nullptr;             // [T][16][3][128] e4m3 terms of x'
+    uint8_t *xq = nullptr;             // [T][16][4][128] e4m3 terms of x'
     float *xs = nullptr;               // [T][16][4] their scales
     float *logits = nullptr;           // [T][128]
     uint32_t *plan = nullptr;          // [0]: segments
@@ -213,7 +216,7 @@ struct MoeArgs {
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
     uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row
     float *gp = nullptr;               // [8 k-slices][T * 8][1536] gate|up partial sums
-    uint8_t *aq = nullptr;             // [T * 8][6][3][128] split terms of the SwiGLU rows
+    uint8_t *aq = nullptr;             // [T * 8][6][4][128] split terms of the SwiGLU rows
     float *as = nullptr;               // [T * 8][6][4]
     float *dp = nullptr;               // [3 k-slices][T * 8][2048] down partial sums
     uint32_t nt[2] = {16, 8};          // tiles per wavefront (gate|up, down)
@@ -223,6 +226,33 @@ struct MoeArgs {
 hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st);
 size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens);
 size_t moe_work_bytes(uint32_t tokens);
+
+// ---------------------------------------------------------------- batched decode attention
+// Ragged paged attention (GQA 32 q / 4 kv heads over 16-token pages, the matrix-core page loop):
+// item i is split i - item_off[s] of sequence s, pages [split * pps[s], +pps[s]) of its pos[s] + 1
+// tokens; partials at part[(i * 32 + q head) * kPartStride].
+struct PagedItemsArgs {
+    const float *q = nullptr;            // [seqs][32][128] post-norm, post-RoPE
+    const uint8_t *pool = nullptr;
+    KvGeom g{};
+    uint32_t layer = 0;
+    const int32_t *tables = nullptr;     // [seqs][max_blocks]
+    uint32_t max_blocks = 0, seqs = 0;
+    const uint32_t *pos = nullptr;       // [seqs]
+    const uint32_t *item_off = nullptr;  // [seqs + 1]
+    const uint32_t *pps = nullptr;       // [seqs] pages per item
+    float *part = nullptr;
+};
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t grid_items, hipStream_t st);
+// the items' partials of every (seq, q head) combined (at most 256 items per sequence) and split
+// into the o projection's input terms: oq [seqs][32][4][128] e4m3, os [seqs][32][4]
+struct CombineItemsArgs {
+    const float *part = nullptr;
+    const uint32_t *item_off = nullptr;
+    uint8_t *oq = nullptr;
+    float *os = nullptr;
+};
+hipError_t launch_attn_combine_items(const CombineItemsArgs &a, uint32_t seqs, hipStream_t st);
 
 // RoPE table of one position range (host twin of the oracle's rope_cos_sin)
 void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out);

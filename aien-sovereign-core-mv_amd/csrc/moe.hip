@@ -11,9 +11,9 @@
 //
 // The GEMMs run on the FP8 matrix cores (v_mfma_scale_f32_16x16x128_f8f6f4, unit scales). The
 // weights are the e4m3 bytes as stored; the f32 activations are split per 128-column block into
-// three e4m3 terms with power-of-two scales, x = s1 q1 + s2 q2 + s3 q3 + r, each term taken from
-// the exact residual of the previous one (so about 12 significant bits survive against fp8's 4),
-// and the three products are summed in f32 with the weight block scale. A wavefront owns 16
+// four e4m3 terms with power-of-two scales, x = s1 q1 + s2 q2 + s3 q3 + s4 q4 + r, each term taken
+// from the exact residual of the previous one (so about 16 significant bits survive against fp8's
+// 4), and the four products are summed in f32 with the weight block scale. A wavefront owns 16
 // output features of one expert segment (gate and up features together for SwiGLU) and all of
 // the segment's rows (16 per MFMA column tile); nothing is exchanged between workgroups inside a
 // launch: the grouping is one workgroup's launch, the combine a launch of its own.
@@ -22,68 +22,13 @@
 
 #include "device.hpp"
 #include "kernels.hpp"
+#include "mfma.hpp"
 #include "route.hpp"
 #include "runtime.hpp"
 
 namespace omega {
 
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-constexpr uint32_t kMH = 2048, kMI = 768, kME = 128, kTerms = 3;
-
-// ------------------------------------------------------------------ activation split
-// 2^(floor(log2 amax) - 7): amax / s lies in [128, 256), inside e4m3's range; a zero block gets 1
-__device__ __forceinline__ float pow2_scale(float amax, float &inv) {
-    int e = (int)((__float_as_uint(amax) >> 23) & 0xff);
-    if (e == 0) {
-        inv = 1.0f;
-        return 1.0f;
-    }
-    e = e - 7 < 1 ? 1 : e - 7;
-    inv = __uint_as_float((uint32_t)(254 - e) << 23);
-    return __uint_as_float((uint32_t)e << 23);
-}
-
-// 8 consecutive values of a 128-value block held by one lane of a 16-lane row -> kTerms e4m3
-// terms (8 bytes each) and their scales. Each term is the e4m3 rounding of the exact residual
-// of the terms before it, scaled by a power of two from the residual's block maximum.
-// one_term (test mutant 7): only the first term is kept, the precision of a plain fp8 cast.
-__device__ __forceinline__ void split8(float (&v)[8], u32x2 (&q)[kTerms], float (&s)[kTerms], bool one_term) {
-#pragma unroll
-    for (uint32_t t = 0; t < kTerms; ++t) {
-        float am = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-        am = row16_max(am);
-        float inv;
-        const float sc = pow2_scale(am, inv);
-        uint32_t w[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h] * inv, v[4 * h + 1] * inv, 0, false);
-            p = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * h + 2] * inv, v[4 * h + 3] * inv, p, true);
-            w[h] = (uint32_t)p;
-            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(p, false);
-            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(p, true);
-            v[4 * h] -= lo.x * sc;
-            v[4 * h + 1] -= lo.y * sc;
-            v[4 * h + 2] -= hi.x * sc;
-            v[4 * h + 3] -= hi.y * sc;
-        }
-        q[t] = u32x2{w[0], w[1]};
-        s[t] = (one_term && t > 0) ? 0.f : sc;
-    }
-}
-
-// stores one lane's share of a block: q[row][block][term][128], s[row][block][4]
-__device__ __forceinline__ void store_split(uint8_t *q, float *s, uint32_t row, uint32_t blocks, uint32_t blk,
-                                            uint32_t j, const u32x2 (&tq)[kTerms], const float (&ts)[kTerms]) {
-    uint8_t *qb = q + ((size_t)row * blocks + blk) * kTerms * 128;
-#pragma unroll
-    for (uint32_t t = 0; t < kTerms; ++t) *reinterpret_cast<u32x2 *>(qb + t * 128 + 8 * j) = tq[t];
-    if (j == 0)
-        *reinterpret_cast<f32x4 *>(s + ((size_t)row * blocks + blk) * 4) = f32x4{ts[0], ts[1], ts[2], 0.f};
-}
+constexpr uint32_t kMH = 2048, kMI = 768, kME = 128;
 
 // ------------------------------------------------------------------ 1. RMSNorm + split (one workgroup per token)
 __global__ __launch_bounds__(256) void k_moe_prep(const MoeArgs a) {
@@ -94,6 +39,20 @@ __global__ __launch_bounds__(256) void k_moe_prep(const MoeArgs a) {
     const f32x4 w0 = *as_global_f32x4(a.norm_w + 8 * tid), w1 = *as_global_f32x4(a.norm_w + 8 * tid + 4);
     float v[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
     const float nw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    if (a.opart) {  // the residual row after attention: h + (o projection's k-slices in order)
+        float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (uint32_t k = 0; k < a.oslices; ++k) {
+            const float *p = a.opart + ((size_t)k * a.tokens + t) * kMH + 8 * tid;
+            const f32x4 p0 = *as_global_f32x4(p), p1 = *as_global_f32x4(p + 4);
+            o[0] += p0.x; o[1] += p0.y; o[2] += p0.z; o[3] += p0.w;
+            o[4] += p1.x; o[5] += p1.y; o[6] += p1.z; o[7] += p1.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] += o[i];
+        float *ho = a.hout + (size_t)t * kMH + 8 * tid;
+        *reinterpret_cast<f32x4 *>(ho) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4 *>(ho + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    }
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += (double)v[i] * (double)v[i];
@@ -216,23 +175,7 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
 }
 
 // ------------------------------------------------------------------ 4/6. grouped FP8 GEMM on the matrix cores
-__device__ __forceinline__ i32x8 ld32_cached(const uint8_t *p) {
-    const u32x4 a = *as_global(p);
-    const u32x4 b = *as_global(p + 64);
-    return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
-}
-__device__ __forceinline__ f32x4 mfma_fp8(const i32x8 &a, const i32x8 &b) {
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
-}
-// acc + A (e4m3) x (2^(sb - 127) B) (e4m3): the B scale is the E8M0 exponent of a power-of-two
-// activation term scale, the same in every lane of a column, so the k-to-lane mapping of the
-// scale blocks does not matter
-__device__ __forceinline__ f32x4 mfma_fp8_sb(const i32x8 &a, const i32x8 &b, const f32x4 &acc, int sb) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, sb);
-}
-// the E8M0 exponent of a power-of-two f32 scale (0: a dropped term, 2^-127)
-__device__ __forceinline__ int e8m0_of(float s) { return (int)((__float_as_uint(s) >> 23) & 0xff); }
+
 
 // Grouped GEMM on the matrix cores, one independent wavefront per (expert segment, run of NT
 // tiles, k-slice). A tile is 16 gate features j0..j0+15 and their 16 up features (gate|up) or 32
@@ -254,26 +197,6 @@ struct MoeGemm {
     static_assert(KB % KBW == 0, "whole k-blocks per slice");
 };
 
-// one k-block of a 16-row tile from the tiled twin: the lane's two 16-byte pieces, each load
-// instruction 1 KiB contiguous
-__device__ __forceinline__ i32x8 ld_tile(const uint8_t *blk, uint32_t lane) {
-    const u32x4 a = __builtin_nontemporal_load(as_global(blk + 16 * lane));
-    const u32x4 b = __builtin_nontemporal_load(as_global(blk + 1024 + 16 * lane));
-    return i32x8{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
-}
-
-template <int KBW>
-struct MoeTileA {
-    i32x8 A[2][KBW];
-    // t0, t1: the twin's blocks of the two 16-row halves at the slice's first k-block
-    __device__ __forceinline__ void load(const uint8_t *t0, const uint8_t *t1, uint32_t lane) {
-#pragma unroll
-        for (int j = 0; j < KBW; ++j) {
-            A[0][j] = ld_tile(t0 + 2048 * j, lane);
-            A[1][j] = ld_tile(t1 + 2048 * j, lane);
-        }
-    }
-};
 
 template <int EPI>
 __global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
@@ -318,6 +241,7 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
             sbe[j][0] = e8m0_of(v.x);
             sbe[j][1] = e8m0_of(v.y);
             sbe[j][2] = e8m0_of(v.z);
+            sbe[j][3] = e8m0_of(v.w);
         }
         float *prow = part + (size_t)row * G::NOUT + 4 * g;
 #pragma unroll 1

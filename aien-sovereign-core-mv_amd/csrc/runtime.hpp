@@ -126,9 +126,19 @@ namespace omega {
 // builds t's tiled twin when it has none (synchronises the library stream; not during capture)
 int fp8_ensure_tiled(Family f, OmegaGpuFp8Tensor *t);
 }  // namespace omega
+struct OmegaGpuBf16Tensor;
+namespace omega {
+// the same for a bf16 tensor (n a multiple of 16, k of 32)
+int bf16_ensure_tiled(Family f, OmegaGpuBf16Tensor *t);
+}  // namespace omega
 
 // Device layout of a bf16 tensor: row-major [n][k] (n_pad == n).
+// The batched lm_head reads a tiled twin (built on first batched use): block (16-row tile rt,
+// 32-column block kb) is 1 KiB at (rt * k/32 + kb) * 512 elements, and inside it element
+// (row r, column c) sits at ((c / 8) * 16 + r) * 8 + c % 8 — the bf16 MFMA operand order, each
+// operand load instruction of a wavefront 1 KiB contiguous.
 struct OmegaGpuBf16Tensor {
     uint32_t n = 0, k = 0, n_pad = 0;
     uint16_t *w = nullptr;
+    uint16_t *wt = nullptr;  // tiled twin, or null until first needed
 };

@@ -105,6 +105,15 @@ class KvLayout(C.Structure):
                 ("block_size", C.c_uint32)]
 
 
+class BatchDecodeConfig(C.Structure):
+    """OmegaGpuBatchDecodeConfig (include/omega_gpu.h), 136 bytes."""
+    _fields_ = [("layers", C.c_uint32), ("vocab", C.c_uint32), ("max_seqs", C.c_uint32),
+                ("max_blocks_per_seq", C.c_uint32), ("max_pos", C.c_uint32), ("eps", C.c_float),
+                ("norm_topk", C.c_int32), ("rope_theta", C.c_double), ("router", C.c_void_p),
+                ("lm_head", C.c_void_p), ("embed", C.c_void_p), ("pool", C.c_void_p),
+                ("layout", KvLayout)]
+
+
 P = C.c_void_p
 U8P, U16P, U32P, U64P, F32P = (C.POINTER(C.c_uint8), C.POINTER(C.c_uint16),
                                 C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
@@ -199,6 +208,15 @@ SIGNATURES = {
     "omega_gpu_moe_batch_f32": (i32, [P, u32, P, P, u32, P, f32, i32, P, P, P]),
     "omega_gpu_moe_batch_dev": (i32, [P, u32, P, P, u32, P, f32, i32, P, P, P, P]),
     "omega_gpu_moe_test_set_mutant": (None, [i32]),
+    "omega_gpu_batch_decode_create": (i32, [C.POINTER(BatchDecodeConfig), C.POINTER(P)]),
+    "omega_gpu_batch_decode_free": (None, [P]),
+    "omega_gpu_batch_decode_set_layer": (i32, [P, u32, P, P, P, P, P, P, P]),
+    "omega_gpu_batch_decode_set_final_norm": (i32, [P, P]),
+    "omega_gpu_batch_decode_set_tables": (i32, [P, u32, P]),
+    "omega_gpu_batch_decode_set_keep_logits": (None, [P, i32]),
+    "omega_gpu_batch_decode_set_eager": (None, [P, i32]),
+    "omega_gpu_batch_decode_step": (i32, [P, u32, P, P, P]),
+    "omega_gpu_batch_decode_read": (i32, [P, u32, P, P, P, P]),
     "omega_gpu_fp8_gemv_dev": (i32, [P, u32, P, P]),
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
@@ -789,6 +807,85 @@ class StreamTimer:
         v = C.c_float()
         assert hip().hipEventElapsedTime(C.byref(v), self.a, self.b) == 0
         return v.value
+
+
+def kv_layout(num_blocks, block_size, layers, kv_heads, head_dim):
+    """The aien-kv-cache bf16 page layout (crates/aien-kv-cache/src/lib.rs:247-292): element
+    (block, layer, plane, token, head, dim) at block*BS + layer*LS + plane*PS + token*TS + head*HS
+    + dim*2."""
+    hs = head_dim * 2
+    ts = kv_heads * hs
+    ps = block_size * ts
+    ls = 2 * ps
+    bs = layers * ls
+    return KvLayout(bs, ls, ps, ts, hs, num_blocks * bs, num_blocks, layers, block_size)
+
+
+class BatchDecode:
+    """The batched serving decode (omega_gpu_batch_decode_*) over a device KV pool."""
+
+    def __init__(self, layers, vocab, max_seqs, max_blocks, max_pos, eps, rope_theta, router, lm_head,
+                 embed, pool_ptr, layout, norm_topk=True):
+        cfg = BatchDecodeConfig(layers, vocab, max_seqs, max_blocks, max_pos, eps, int(norm_topk),
+                                rope_theta, router.as_raw(), lm_head.as_raw(), embed.as_raw(),
+                                pool_ptr, layout)
+        self.cfg = cfg
+        self._keep = (router, lm_head, embed)
+        h = P()
+        self._rc(lib().omega_gpu_batch_decode_create(C.byref(cfg), C.byref(h)))
+        self.h = h
+
+    @staticmethod
+    def _rc(rc):
+        if rc:
+            raise OmegaGpuError(rc, _s(lib().omega_gpu_session_last_error()))
+
+    def set_layer(self, layer, qkv, o, gate_up, down, input_norm, q_norm, k_norm):
+        args = [np.ascontiguousarray(a, dtype=np.float32) for a in (input_norm, q_norm, k_norm)]
+        self._rc(lib().omega_gpu_batch_decode_set_layer(self.h, layer, qkv.as_raw(), o.as_raw(),
+                                                        gate_up.as_raw(), down.as_raw(),
+                                                        *[ptr(a) for a in args]))
+
+    def set_final_norm(self, w):
+        self._rc(lib().omega_gpu_batch_decode_set_final_norm(
+            self.h, ptr(np.ascontiguousarray(w, dtype=np.float32))))
+
+    def set_tables(self, tables):
+        t = np.ascontiguousarray(tables, dtype=np.int32)
+        self._rc(lib().omega_gpu_batch_decode_set_tables(self.h, t.shape[0], ptr(t)))
+
+    def set_keep_logits(self, on):
+        lib().omega_gpu_batch_decode_set_keep_logits(self.h, int(on))
+
+    def set_eager(self, on):
+        lib().omega_gpu_batch_decode_set_eager(self.h, int(on))
+
+    def step(self, tokens, positions):
+        tk = np.ascontiguousarray(tokens, dtype=np.uint32)
+        ps = np.ascontiguousarray(positions, dtype=np.uint32)
+        out = np.empty(tk.size, np.uint32)
+        self._rc(lib().omega_gpu_batch_decode_step(self.h, tk.size, ptr(tk), ptr(ps), ptr(out)))
+        return out
+
+    def read(self, seqs, x=False, hidden=False, logits=False, routes=False):
+        c = self.cfg
+        xa = np.empty((seqs, 2048), np.float32) if x else None
+        ha = np.empty((seqs, 2048), np.float32) if hidden else None
+        la = np.empty((seqs, c.vocab), np.float32) if logits else None
+        ra = np.empty((c.layers, seqs, 8), np.uint32) if routes else None
+        self._rc(lib().omega_gpu_batch_decode_read(self.h, seqs, ptr(xa), ptr(ha), ptr(la), ptr(ra)))
+        return xa, ha, la, ra
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().omega_gpu_batch_decode_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 def moe_batch(router, layer, gate_up, down, h, eps, norm_topk=True):

@@ -196,15 +196,9 @@ def bench_paged(om, args):
     import ctypes as C
 
     max_pages = max(b * l // 16 for b, l in PAGED_POINTS)
-    layers = L
-    import pyoracle as orc
-
-    lay = orc.kv_layout(max_pages, 16, layers, KVH, HD)
-    L_ = om.KvLayout(lay.block_stride_bytes, lay.layer_stride_bytes, lay.kv_plane_stride_bytes,
-                     lay.token_stride_bytes, lay.head_stride_bytes, lay.pool_bytes, lay.num_blocks,
-                     lay.num_layers, lay.block_size)
-    pool = om.DeviceBuffer(lay.pool_bytes)
-    om.synth_bf16_dev(pool, lay.pool_bytes // 2, SEED, 77, 1.0)
+    L_ = om.kv_layout(max_pages, 16, L, KVH, HD)
+    pool = om.DeviceBuffer(L_.pool_bytes)
+    om.synth_bf16_dev(pool, L_.pool_bytes // 2, SEED, 77, 1.0)
     flush = om.DeviceBuffer(1 << 30)
     om.sync()
     lib = om.lib()
@@ -346,6 +340,148 @@ def bench_moe(om, args):
         "points": lines, "cpu_baseline": cpu}), flush=True)
 
 
+# ---------------------------------------------------------------- configuration 5: batched serving decode
+SERVE_SEQS = 32
+KV_BYTES_PER_TOKEN = L * 2 * KVH * HD * 2                         # 98,304: K and V of 48 layers
+DENSE_BYTES_PER_LAYER = 5120 * 2048 + 2048 * 4096 + E * H * 2     # q|k|v + o (e4m3) + router (bf16)
+EXPERT_BYTES = 1536 * 2048 + 2048 * 768                           # gate|up + down of one expert (e4m3)
+
+
+def serve_contexts():
+    """32 context lengths drawn log-uniform in [1024, 131072] (seeded)."""
+    rng = np.random.default_rng(SEED + 5)
+    return np.exp(rng.uniform(np.log(1024), np.log(131072), SERVE_SEQS)).astype(np.int64)
+
+
+def serve_cpu_baseline(threads, mean_ctx):
+    """The oracle engine per token at a short context (4 of 48 layers, scaled) plus the oracle's
+    paged attention of one layer at the mean context (times 48) plus one lm_head, times 32
+    sequences: the CPU restatement serving the same step one sequence at a time."""
+    import ctypes as C
+
+    import pyoracle as orc
+
+    cfg = dict(layers=4, hidden=H, q_heads=QH, kv_heads=KVH, head_dim=HD, experts=E, top_k=TOPK,
+               inter=I, vocab=V, eps=1e-6, rope_theta=1e6)
+    m = orc.Model(cfg, SEED, sigma=0.02, norm_sigma=0.0, threads=threads)
+    eng = orc.Engine(m, 256, refined_router=True, threads=threads)
+    hid = eng.step(1)
+    t0 = time.perf_counter()
+    for t in range(16):
+        hid = eng.step(2 + t)
+    t_layer = (time.perf_counter() - t0) / 16 / 4
+    t1 = time.perf_counter()
+    eng.logits(hid)
+    t_lm = time.perf_counter() - t1
+    rng = np.random.default_rng(1)
+    pages = (mean_ctx + 15) // 16
+    lay = orc.kv_layout(pages, 16, 1, KVH, HD)
+    pool = orc.f32_to_bf16(rng.standard_normal(lay.pool_bytes // 2).astype(np.float32)).view(np.uint8)
+    tab = np.arange(pages, dtype=np.int32)
+    q = rng.standard_normal(QH * HD).astype(np.float32)
+    out = np.zeros(QH * HD, np.float32)
+    t2 = time.perf_counter()
+    orc.lib().oref_paged_attention(orc.ptr(q), orc.ptr(pool), C.byref(lay), orc.ptr(tab), int(mean_ctx), 0,
+                                   QH, KVH, HD, orc.ptr(out))
+    t_attn = time.perf_counter() - t2
+    per_token = t_layer * L + t_attn * L + t_lm
+    return {"value": round(SERVE_SEQS / (per_token * SERVE_SEQS), 4), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle engine (oracle/oracle.c, {threads} threads): 4 of 48 layers x 16 tokens "
+                      f"({t_layer * 1e3:.1f} ms/layer) + oref_paged_attention of one layer at the mean "
+                      f"context {int(mean_ctx)} ({t_attn * 1e3:.0f} ms, one thread) + one 151936-row "
+                      f"lm_head ({t_lm * 1e3:.0f} ms), scaled to 48 layers: {per_token:.2f} s per token, "
+                      f"the 32 sequences served one after another"}
+
+
+def bench_serve(om, args):
+    """Configuration 5: 32 concurrent sequences of the random-init 48-layer model, contexts
+    log-uniform in [1k, 128k] already resident as bf16 KV (N(0,1)) in 16-token pages of the pool
+    (pages of every sequence a random permutation of the pool), `serve_steps` greedy steps of all
+    32 sequences timed after `serve_warmup`, each step one hipGraph replay."""
+    ctx = serve_contexts()
+    steps, warmup = args.serve_steps, args.serve_warmup
+    need = ctx + warmup + steps + 1
+    pages = (need + 15) // 16
+    max_blocks = int(pages.max())
+    total = int(pages.sum())
+    lay = om.kv_layout(total, 16, L, KVH, HD)
+    t_build = time.time()
+    pool = om.DeviceBuffer(lay.pool_bytes)
+    om.synth_bf16_dev(pool, lay.pool_bytes // 2, SEED, 78, 1.0)
+    rng = np.random.default_rng(SEED)
+    perm = rng.permutation(total).astype(np.int32)
+    tables = np.full((SERVE_SEQS, max_blocks), -1, np.int32)
+    off = 0
+    for s in range(SERVE_SEQS):
+        tables[s, :pages[s]] = perm[off:off + pages[s]]
+        off += pages[s]
+    router = om.Router(L)
+    ones = np.ones(H, np.float32)
+    layers = []
+    for l in range(L):
+        qkv = om.Fp8Tensor.synth(1, 5120, 2048, SEED, tid(l, 0))
+        o = om.Fp8Tensor.synth(1, 2048, 4096, SEED, tid(l, 1))
+        gu = om.Fp8Tensor.synth(E, 1536, 2048, SEED, tid(l, 2))
+        dn = om.Fp8Tensor.synth(E, 2048, 768, SEED, tid(l, 3))
+        layers.append((qkv, o, gu, dn))
+        router.set_layer(l, om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02), ones)
+        router.set_directory(l, np.zeros(2 * E, np.uint64), np.zeros(2 * E, np.uint64))
+    lm = om.Bf16Tensor.synth(V, H, SEED, 2, 0.02)
+    embed = om.Bf16Tensor.synth(V, H, SEED, 1, 0.02)
+    bd = om.BatchDecode(L, V, SERVE_SEQS, max_blocks, max_blocks * 16, 1e-6, 1e6, router, lm, embed,
+                        pool.ptr, lay)
+    hd1 = np.ones(HD, np.float32)
+    for l, (qkv, o, gu, dn) in enumerate(layers):
+        bd.set_layer(l, qkv, o, gu, dn, ones, hd1, hd1)
+    bd.set_final_norm(ones)
+    bd.set_tables(tables)
+    if args.eager:
+        bd.set_eager(True)
+    om.sync()
+    t_build = time.time() - t_build
+    tok = rng.integers(0, V, SERVE_SEQS).astype(np.uint32)
+    pos = ctx.astype(np.uint32).copy()
+    for _ in range(warmup):
+        tok = bd.step(tok, pos)
+        pos += 1
+    om.sync()
+    ctx_mid = pos.astype(np.int64) + steps // 2 + 1
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = bd.step(tok, pos)
+        pos += 1
+    om.sync()
+    elapsed = time.perf_counter() - t0
+    _, _, _, routes = bd.read(SERVE_SEQS, routes=True)
+    distinct = [len(np.unique(routes[l])) for l in range(L)]
+    step_bytes = int(ctx_mid.sum() * KV_BYTES_PER_TOKEN + sum(distinct) * EXPERT_BYTES +
+                     L * DENSE_BYTES_PER_LAYER + V * H * 2)
+    ms = elapsed * 1e3 / steps
+    tok_s = SERVE_SEQS * steps / elapsed
+    gbs = step_bytes / (ms * 1e6)
+    cpu = None if args.no_cpu else serve_cpu_baseline(args.cpu_threads, int(ctx_mid.mean()))
+    print(json.dumps({
+        "metric": "Qwen3-30B-A3B FP8 batched serving decode (configuration 5): 32 sequences, tok/s",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8", "data": "synthetic random-init weights, N(0,1) bf16 KV of the drawn contexts",
+        "config": {"workload": "Qwen3-30B-A3B FP8 batched decode, 32 sequences, contexts log-uniform "
+                               "in [1k, 128k], bf16 KV in 16-token pages, "
+                               + ("direct launches" if args.eager else "one hipGraph per step"),
+                   "global_batch": SERVE_SEQS, "context_mean": int(ctx_mid.mean()),
+                   "context_min": int(ctx_mid.min()), "context_max": int(ctx_mid.max()),
+                   "kv_pool_GB": round(lay.pool_bytes / 1e9, 1), "parallelism": "single GPU"},
+        "step_roofline": {"bound": "hbm", "algorithmic_bytes_per_step": step_bytes,
+                          "achieved_GBs": round(gbs, 1), "peak": PEAK_GBS, "frac": round(gbs / PEAK_GBS, 4),
+                          "distinct_experts_mean": round(float(np.mean(distinct)), 1),
+                          "kv_bytes_per_step": int(ctx_mid.sum() * KV_BYTES_PER_TOKEN)},
+        "cpu_baseline": cpu,
+        "extra": {"build_s": round(t_build, 1), "last_tokens_head": tok[:4].tolist()}}), flush=True)
+    bd.free()
+    pool.free()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -357,10 +493,13 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "paged", "moe"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "paged", "moe", "serve"], default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
                          "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
-                         "at token batch 1 and 32 (configuration 2)")
+                         "at token batch 1 and 32 (configuration 2); serve: 32 sequences of batched "
+                         "decode over long contexts (configuration 5)")
+    ap.add_argument("--serve-steps", type=int, default=128)
+    ap.add_argument("--serve-warmup", type=int, default=4)
     ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -384,6 +523,9 @@ def main():
         return
     if args.workload == "moe":
         bench_moe(om, args)
+        return
+    if args.workload == "serve":
+        bench_serve(om, args)
         return
     total = args.prompt + args.warmup + args.steps + 8
     max_pos = om.round_max_pos(total)

@@ -529,6 +529,49 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
 /* test mutants of the batched MoE block: 1 rank mask on id^1, 2 weights not normalised, 5 gate and
  * up swapped, 6 slot 7 dropped from the combine, 7 one activation term (a plain fp8 cast) */
 void omega_gpu_moe_test_set_mutant(int mutant);
+/* Batched serving decode (not in the reference ABI; the multi-sequence decode that
+ * crates/aien-serve-http's Engine::concurrency / generate_group would drive for the 30B,
+ * engine.rs:131-179): one greedy step of up to 32 sequences of the Qwen3-30B-A3B FP8 model
+ * (the per-token semantics of Qwen3MoeOmegaEngine::step, qwen3_moe_omega.rs:4096-4345) over
+ * the caller's device KV pool in the aien-kv-cache page layout (crates/aien-kv-cache/src/
+ * lib.rs:129-365), read and written in place. Each step appends every sequence's K/V at its
+ * position through its page table and attends over positions 0..=pos. One hipGraph per batch
+ * size; errors are reported by omega_gpu_session_last_error. The router, tensors, pool and
+ * page tables are borrowed and must outlive the handle. */
+typedef struct OmegaGpuBatchDecode OmegaGpuBatchDecode;
+typedef struct OmegaGpuBatchDecodeConfig {
+    uint32_t layers, vocab, max_seqs, max_blocks_per_seq, max_pos;
+    float eps;
+    int32_t norm_topk;
+    double rope_theta;
+    void *router;    /* OmegaGpuRouter (128 experts; the post-attention norm per layer) */
+    void *lm_head;   /* OmegaGpuBf16Tensor [vocab][2048], vocab a multiple of 16 */
+    void *embed;     /* OmegaGpuBf16Tensor [vocab][2048] */
+    void *pool;      /* device KV pool */
+    OmegaGpuKvLayout layout;
+} OmegaGpuBatchDecodeConfig;
+int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpuBatchDecode **out);
+void omega_gpu_batch_decode_free(OmegaGpuBatchDecode *b);
+/* q|k|v 1x5120x2048, o 1x2048x4096, gate|up 128x1536x2048, down 128x2048x768 FP8 tensors, the
+ * input norm [2048] and the q / k head norms [128] of a layer */
+int omega_gpu_batch_decode_set_layer(OmegaGpuBatchDecode *b, uint32_t layer, const void *qkv, const void *o,
+                                     const void *gate_up, const void *down, const float *input_norm,
+                                     const float *q_norm, const float *k_norm);
+int omega_gpu_batch_decode_set_final_norm(OmegaGpuBatchDecode *b, const float *final_norm);
+/* page tables [seqs][max_blocks_per_seq] (-1: none), copied to the device */
+int omega_gpu_batch_decode_set_tables(OmegaGpuBatchDecode *b, uint32_t seqs, const int32_t *tables);
+/* keep every step's logits [seqs][vocab] for omega_gpu_batch_decode_read (off by default) */
+void omega_gpu_batch_decode_set_keep_logits(OmegaGpuBatchDecode *b, int on);
+/* launch the step's kernels directly instead of replaying the hipGraph (profilers that cannot
+ * follow graph capture); the same kernels and arguments */
+void omega_gpu_batch_decode_set_eager(OmegaGpuBatchDecode *b, int on);
+/* one step: sequence s feeds tokens[s] at positions[s]; next_tokens[s] = its greedy token */
+int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uint32_t *tokens,
+                                const uint32_t *positions, uint32_t *next_tokens);
+/* the last step's residual rows x, final-normed rows, logits (kept) [seqs][...] and routed expert
+ * ids [layers][seqs][8]; any pointer may be NULL */
+int omega_gpu_batch_decode_read(OmegaGpuBatchDecode *b, uint32_t seqs, float *x, float *hidden, float *logits,
+                                uint32_t *route_ids);
 /* the library's HIP stream (hipStream_t) and a full synchronisation of it */
 void *omega_gpu_stream(void);
 int omega_gpu_sync(void);
@@ -573,6 +616,8 @@ static_assert(offsetof(OmegaGpuAttnInfo, kv_blocks_logical) == 136, "AttnInfo.kv
 static_assert(offsetof(OmegaGpuAttnInfo, q_bytes) == 144, "AttnInfo.q_bytes");
 static_assert(offsetof(OmegaGpuAttnInfo, kv_source) == 168, "AttnInfo.kv_source");
 static_assert(sizeof(OmegaGpuKvLayout) == 64, "KvLayout");
+static_assert(sizeof(OmegaGpuBatchDecodeConfig) == 136, "BatchDecodeConfig");
+static_assert(offsetof(OmegaGpuBatchDecodeConfig, layout) == 72, "BatchDecodeConfig.layout");
 static_assert(offsetof(OmegaGpuKvLayout, block_size) == 56, "KvLayout.block_size");
 #endif
 

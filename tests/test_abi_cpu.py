@@ -93,3 +93,11 @@ def test_host_checks_refuse_before_touching_the_device():
     assert "layers" in om._s(lib.omega_gpu_session_last_error())
     # NULL handles
     assert lib.omega_gpu_fp8_tensor_entry(None, 0, None, None) == -1
+
+
+def test_kv_layout_helper_matches_the_oracle(oracle):
+    import omega_amd
+
+    for args in ((100, 16, 48, 4, 128), (7, 16, 2, 4, 128), (3, 8, 1, 2, 64)):
+        a, b = omega_amd.kv_layout(*args), oracle.kv_layout(*args)
+        assert [getattr(a, f) for f, _ in a._fields_] == [getattr(b, f) for f, _ in b._fields_]

@@ -1,0 +1,177 @@
+"""GPU parity of the batched serving decode (configuration 5's step) against the oracle engine.
+
+The model has the real Qwen3-30B-A3B layer shape (hidden 2048, 32/4 heads of 128, 128 experts
+top-8, intermediate 768) with 2 layers and a vocabulary of 8192 so the CPU oracle runs in
+seconds; seeded random-init weights, norm weights 1 + N(0, 0.1). The sequences live in one
+device KV pool of the aien-kv-cache page layout, each with its own random page table.
+
+Bars: per sequence and step, the greedy token equals the oracle engine's (one engine per
+sequence, the reference's per-token step); logits within 2e-3 relative while the routing of
+every layer agrees; a first routing difference only at a near tie (the oracle's logit margin
+< 1e-3 between the two ranks that differ: rank 8 / 9, or two ranks swapped inside the top 8). Batch invariance: a sequence's tokens and logits are bit-identical whatever the rest
+of the batch holds and whatever the batch size.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+SEED = 2027
+
+
+def rel_err(a, e):
+    return float(np.abs(a - e).max() / max(np.abs(e).max(), 1e-30))
+
+
+def model_config(layers, vocab):
+    return dict(layers=layers, hidden=2048, q_heads=32, kv_heads=4, head_dim=128, experts=128,
+                top_k=8, inter=768, vocab=vocab, eps=1e-6, rope_theta=1e6)
+
+
+class BatchModel:
+    """An oracle model uploaded through the C ABI with a device KV pool of `blocks` pages."""
+
+    def __init__(self, omega, oracle, m, max_seqs, blocks, max_blocks):
+        c = m.cfg
+        self.omega, self.m = omega, m
+        self.router = omega.Router(c.layers)
+        self.tensors = []
+        for l in range(c.layers):
+            ts = []
+            for kind in range(4):
+                w, s = m.tensor(l, kind)
+                ts.append(omega.Fp8Tensor.upload(w.shape[0], w.shape[1], w.shape[2], w, s))
+            self.tensors.append(ts)
+            self.router.set_layer(l, m.tensor(l, 4), m.tensor(l, 6))
+            self.router.set_directory(l, np.zeros(2 * c.experts, np.uint64), np.zeros(2 * c.experts, np.uint64))
+        self.lm = omega.Bf16Tensor.upload(c.vocab, c.hidden, m.lm_head())
+        self.embed = omega.Bf16Tensor.upload(c.vocab, c.hidden, m.embed())
+        self.lay = oracle.kv_layout(blocks, 16, c.layers, c.kv_heads, c.head_dim)
+        L = omega.KvLayout(self.lay.block_stride_bytes, self.lay.layer_stride_bytes,
+                           self.lay.kv_plane_stride_bytes, self.lay.token_stride_bytes,
+                           self.lay.head_stride_bytes, self.lay.pool_bytes, self.lay.num_blocks,
+                           self.lay.num_layers, self.lay.block_size)
+        self.pool = omega.DeviceBuffer(self.lay.pool_bytes)
+        self.bd = omega.BatchDecode(c.layers, c.vocab, max_seqs, max_blocks, max_blocks * 16, c.eps,
+                                    c.rope_theta, self.router, self.lm, self.embed, self.pool.ptr, L)
+        for l in range(c.layers):
+            q, o, g, d = self.tensors[l]
+            self.bd.set_layer(l, q, o, g, d, m.tensor(l, 5), m.tensor(l, 7), m.tensor(l, 8))
+        self.bd.set_final_norm(m.final_norm())
+
+    def free(self):
+        self.bd.free()
+        for ts in self.tensors:
+            for t in ts:
+                t.free()
+        self.router.free()
+        self.lm.free()
+        self.embed.free()
+        self.pool.free()
+
+
+@pytest.fixture(scope="module")
+def small(omega, oracle):
+    m = oracle.Model(model_config(2, 8192), seed=SEED, sigma=0.02, norm_sigma=0.1, threads=16)
+    bm = BatchModel(omega, oracle, m, max_seqs=32, blocks=1024, max_blocks=16)
+    yield m, bm
+    bm.free()
+
+
+def tie_margin(gpu_ids, ids, w, margin89):
+    """The oracle's logit margin at the first rank where the two routings differ: between the
+    swapped ranks (ln of their weight ratio) when the expert sets agree, else rank 8 / rank 9."""
+    if set(gpu_ids.tolist()) == set(ids.tolist()):
+        k = int(np.argmax(gpu_ids != ids))
+        return float(np.log(w[k] / w[k + 1]))
+    return float(margin89)
+
+
+def tables_for(rng, seqs, max_blocks, blocks):
+    free = rng.permutation(blocks)
+    return free[: seqs * max_blocks].reshape(seqs, max_blocks).astype(np.int32)
+
+
+def test_mixed_prompts_match_the_oracle(omega, oracle, small):
+    m, bm = small
+    rng = np.random.default_rng(1)
+    prompts = [[5, 1000, 77], list(rng.integers(0, 8192, 10)), list(rng.integers(0, 8192, 21)),
+               list(rng.integers(0, 8192, 37))]
+    S, new = len(prompts), 12
+    bm.bd.set_tables(tables_for(rng, S, 16, 1024))
+    bm.bd.set_keep_logits(True)
+    engines = [oracle.Engine(m, 256, refined_router=True, threads=16) for _ in range(S)]
+    seqs = [list(p) for p in prompts]
+    pos = [0] * S
+    worst, flips, diverged = 0.0, [], [False] * S
+    steps = max(len(p) for p in prompts) + new
+    for step in range(steps):
+        toks = [seqs[s][pos[s]] for s in range(S)]
+        got = bm.bd.step(toks, pos)
+        _, _, gl, groutes = bm.bd.read(S, logits=True, routes=True)
+        for s in range(S):
+            logits = engines[s].logits(engines[s].step(toks[s]))
+            want = oracle.argmax(logits)
+            o_ids, o_w, o_margin = engines[s].last_routes()
+            if not diverged[s] and not np.array_equal(groutes[:, s, :], o_ids):
+                bad = [l for l in range(m.cfg.layers) if not np.array_equal(groutes[l, s], o_ids[l])]
+                flips.append((s, pos[s], bad, [tie_margin(groutes[l, s], o_ids[l], o_w[l], o_margin[l])
+                                               for l in bad]))
+                diverged[s] = True
+            if not diverged[s]:
+                worst = max(worst, rel_err(gl[s], logits))
+            assert got[s] == want, (s, pos[s], int(got[s]), want)
+            pos[s] += 1
+            if pos[s] >= len(seqs[s]):
+                seqs[s].append(int(got[s]))
+    bm.bd.set_keep_logits(False)
+    for s, p, layers, mg in flips:
+        assert mg[0] < 1e-3, (s, p, layers, mg)
+    assert worst <= TOL, worst
+    print(f"worst logit rel err {worst:.2e}, flips {flips}")
+
+
+def test_batch_invariance(omega, oracle, small):
+    # one prompt in every slot of a 32-sequence batch (each with its own pages), then alone: the
+    # per-sequence arithmetic does not depend on the rest of the batch
+    m, bm = small
+    rng = np.random.default_rng(2)
+    prompt = list(rng.integers(0, 8192, 9))
+    runs = {}
+    for S in (32, 1, 5):
+        bm.bd.set_tables(tables_for(rng, S, 16, 1024))
+        bm.bd.set_keep_logits(True)
+        tok, toks, logits = [prompt[0]] * S, [], []
+        for p in range(len(prompt) + 4):
+            out = bm.bd.step(tok, [p] * S)
+            _, _, gl, _ = bm.bd.read(S, logits=True)
+            toks.append(out.copy())
+            logits.append(gl.copy())
+            nxt = prompt[p + 1] if p + 1 < len(prompt) else int(out[0])
+            tok = [nxt] * S
+        runs[S] = (np.array(toks), np.array(logits))
+    bm.bd.set_keep_logits(False)
+    t32, l32 = runs[32]
+    assert (t32 == t32[:, :1]).all()
+    for s in range(1, 32):
+        np.testing.assert_array_equal(l32[:, s], l32[:, 0])
+    for S in (1, 5):
+        np.testing.assert_array_equal(runs[S][0][:, 0], t32[:, 0])
+        np.testing.assert_array_equal(runs[S][1][:, 0], l32[:, 0])
+
+
+def test_refusals(omega, small):
+    m, bm = small
+    with pytest.raises(omega.OmegaGpuError):
+        bm.bd.step([1] * 33, [0] * 33)            # more than max_seqs
+    with pytest.raises(omega.OmegaGpuError):
+        bm.bd.step([1], [16 * 16])                # position past the table
+    bad = np.full((2, 16), 5000, np.int32)        # entry outside the pool
+    with pytest.raises(omega.OmegaGpuError):
+        bm.bd.set_tables(bad)
+    short = np.full((2, 16), -1, np.int32)        # the table names pages 0..1 only
+    short[:, :2] = [[1, 2], [3, 4]]
+    bm.bd.set_tables(short)
+    bm.bd.step([1, 2], [31, 0])
+    with pytest.raises(omega.OmegaGpuError):
+        bm.bd.step([1, 2], [32, 0])               # page 2 is not in the table

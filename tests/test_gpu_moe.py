@@ -5,7 +5,7 @@ SwiGLU, down grouped GEMV, slot-order combine).
 
 Bars: expert ids bit-exact, weights within 1e-6 relative, moe_out within 2e-3 relative
 (max abs error over max abs value, per token). The GEMMs run on the FP8 matrix cores with the
-activations split into three e4m3 terms; the one-term mutant (a plain fp8 cast of the
+activations split into four e4m3 terms; the one-term mutant (a plain fp8 cast of the
 activations) must fail the 2e-3 bar, which shows the bar resolves the split's precision.
 """
 import numpy as np
