@@ -23,6 +23,7 @@
 // appends this token's K/V and folds it in as one more online-softmax step. A second small
 // launch combines the splits (k_attn_combine); nothing is exchanged between workgroups inside a
 // launch.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <vector>
@@ -366,38 +367,41 @@ __device__ __forceinline__ void paged_q(const float *q, uint32_t lane, uint16_t 
 }
 
 // Pages [p_begin, p_end) of a sequence of `ctx` tokens (table tab): the online softmax of the 8 q
-// heads of kv head h. The split's page ids are read 64 at a time into one VGPR and taken by
-// readlane, so no page load waits on a table load; the next page's loads go out before this
-// page's math.
+// heads of kv head h. Two register sets take turns (the loop is unrolled by two, so no set is
+// ever copied into the other): while one page is staged and multiplied, the other set's page is
+// in flight, and a set is reloaded as soon as its page is consumed. The loop body is one
+// straight path: every load is issued unconditionally (the page index clamped to the last page)
+// and the second page of an iteration past p_end is processed as a null page (no valid token:
+// its scores are -inf and its staged V rows zero, so m, l and O come out unchanged, exactly), so
+// the vector-memory waits never merge over branches and waiting for one set never waits for the
+// other. Page ids come from scalar loads one iteration ahead of their use. The first page goes
+// through the same update as the others: from m = -inf, l = 0, O = 0 the rescale factor is
+// exp(-inf) = 0 and the result is the first page's own.
 template <int MUT>
 __device__ __forceinline__ void paged_pages(const PagedSrc &src, const int32_t *tab, uint32_t h, uint32_t p_begin,
-                                            uint32_t p_end, uint32_t pages, uint32_t ctx, const bf16x8 (&qop)[4],
-                                            uint8_t *vt, uint32_t lane, float &m_l, float &l_l, f32x4 (&O)[8]) {
-    const uint32_t g = lane >> 4, n = lane & 15;
-    uint32_t tbase = p_begin;
-    int32_t tl = tab[min(tbase + lane, pages - 1)];
-    PagedRegs R;
-    paged_load<MUT>(src, tab, (uint32_t)__builtin_amdgcn_readfirstlane(tl), h, p_begin, ctx, lane, R);
+                                            uint32_t p_end, uint32_t ctx, const bf16x8 (&qop)[4], uint8_t *vt,
+                                            uint32_t lane, float &m_l, float &l_l, f32x4 (&O)[8]) {
+    const uint32_t g = lane >> 4, n = lane & 15, last = p_end - 1;
+    const cu32 *ctab = as_const_u32(tab);
+    PagedRegs A, B;
+    const uint32_t p1 = min(p_begin + 1, last);
+    paged_load<MUT>(src, tab, ctab[p_begin], h, p_begin, ctx, lane, A);
+    paged_load<MUT>(src, tab, ctab[p1], h, p1, ctx, lane, B);
     m_l = -INFINITY;
     l_l = 0.f;
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
     DattnPage T;
-    for (uint32_t p = p_begin; p < p_end; ++p) {
-        PagedRegs nx;
-        const bool more = p + 1 < p_end;
-        if (more) {
-            if (p + 1 - tbase >= 64) {
-                tbase += 64;
-                tl = tab[min(tbase + lane, pages - 1)];
-            }
-            const uint32_t nblk = (uint32_t)__builtin_amdgcn_readlane(tl, p + 1 - tbase);
-            paged_load<MUT>(src, tab, nblk, h, p + 1, ctx, lane, nx);
-        }
-        paged_stage_v(R, p * 16, ctx, lane, vt, T);
-        if (p == p_begin) dattn_page<true>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
-        else dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
-        if (more) R = nx;
+    for (uint32_t p = p_begin; p < p_end; p += 2) {
+        const uint32_t pa = min(p + 2, last), pb = min(p + 3, last);
+        const uint32_t blk_a = ctab[pa], blk_b = ctab[pb];
+        const uint32_t ctx_b = p + 1 < p_end ? ctx : 0u;  // 0: the null page
+        paged_stage_v(A, p * 16, ctx, lane, vt, T);
+        dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        paged_load<MUT>(src, tab, blk_a, h, pa, ctx, lane, A);
+        paged_stage_v(B, (p + 1) * 16, ctx_b, lane, vt, T);
+        dattn_page<false>(T, qop, (p + 1) * 16, ctx_b, g, n, m_l, l_l, O);
+        paged_load<MUT>(src, tab, blk_b, h, pb, ctx, lane, B);
     }
 }
 
@@ -437,39 +441,65 @@ __global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
     const PagedSrc src{a.pool, a.g, a.layer};
     float m_l, l_l;
     f32x4 O[8];
-    paged_pages<MUT>(src, tab, h, p_begin, p_end, pages, ctx, qop, vt, lane, m_l, l_l, O);
+    paged_pages<MUT>(src, tab, h, p_begin, p_end, ctx, qop, vt, lane, m_l, l_l, O);
     paged_store(a.part + (((size_t)b * a.qh + h * 8) * a.splits + c) * kPartStride, (size_t)a.splits * kPartStride,
                 lane, m_l, l_l, O);
 }
 
-// Ragged work items (the batched decode step): item i of the launch is split i - item_off[s] of
-// sequence s (item_off[s] <= i < item_off[s + 1]), pages [split * pps_s, +pps_s) of its
-// pos_s + 1 tokens; partials at part[(i * 32 + q head) * kPartStride]. The grid loops over the
-// items (a fixed grid serves every step of a captured graph).
+// Wavefront w takes the run [w r, (w + 1) r) of the pages laid end to end, r = ceil(total /
+// kItemWaves), cut into items at sequence boundaries. The items come out in page order, so each
+// sequence's items are consecutive (item_off) and at most kItemWaves + seqs - 1 of them exist; a
+// sequence gets at most one item per wavefront.
+void plan_items(const uint32_t *first, uint32_t seqs, ItemPlan &p) {
+    const uint32_t total = first[seqs], run = (total + kItemWaves - 1) / kItemWaves;
+    uint32_t n = 0, s = 0;
+    for (uint32_t w = 0; w < kItemWaves; ++w) {
+        p.wave_off[w] = n;
+        uint32_t b = std::min(total, w * run);
+        const uint32_t e = std::min(total, b + run);
+        while (b < e) {
+            while (first[s + 1] <= b) ++s;
+            const uint32_t pe = std::min(e, first[s + 1]);
+            if (b == first[s]) p.item_off[s] = n;
+            p.items[n][0] = (s << 24) | (b - first[s]);
+            p.items[n][1] = pe - first[s];
+            ++n;
+            b = pe;
+        }
+    }
+    p.wave_off[kItemWaves] = n;
+    p.item_off[seqs] = n;
+}
+
+// Balanced work items (the batched decode step): the pages of all sequences, laid end to end,
+// are cut into one contiguous run per wavefront (the same number of pages each, so every
+// wavefront of a kv head finishes together), and each run into items at sequence boundaries.
+// Wavefront w of kv head h serves items [wave_off[w], wave_off[w + 1]); item i is pages
+// [first, end) of sequence seq (items[i] = {seq << 24 | first, end}), its partials at
+// part[(i * 32 + q head) * kPartStride].
 __global__ __launch_bounds__(64) void k_paged_items(const PagedItemsArgs a) {
     __shared__ __align__(16) uint16_t qhl[2][8][128];
     __shared__ __align__(16) uint8_t vt[16 * kVtRow];
-    const uint32_t lane = threadIdx.x, h = blockIdx.x;
-    const uint32_t total = a.item_off[a.seqs];
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, w = blockIdx.y;
+    const uint32_t i0 = a.wave_off[w], i1 = a.wave_off[w + 1];
     const PagedSrc src{a.pool, a.g, a.layer};
-    for (uint32_t it = blockIdx.y; it < total; it += gridDim.y) {
-        uint32_t s = 0;
-        while (s + 1 < a.seqs && a.item_off[s + 1] <= it) ++s;
-        const uint32_t ctx = a.pos[s] + 1, pages = (ctx + 15) / 16, pps = a.pps[s];
-        const uint32_t p_begin = (it - a.item_off[s]) * pps, p_end = min(pages, p_begin + pps);
+    for (uint32_t it = i0; it < i1; ++it) {
+        const uint32_t e0 = a.items[2 * it], e1 = a.items[2 * it + 1];
+        const uint32_t s = e0 >> 24, p_begin = e0 & 0xffffffu, p_end = e1;
+        const uint32_t ctx = a.pos[s] + 1;
         __syncthreads();  // the previous item's LDS reads are done
         bf16x8 qop[4];
         paged_q(a.q + ((size_t)s * 32 + h * 8) * 128, lane, qhl, qop);
         float m_l, l_l;
         f32x4 O[8];
-        paged_pages<0>(src, a.tables + (size_t)s * a.max_blocks, h, p_begin, p_end, pages, ctx, qop, vt, lane, m_l,
-                       l_l, O);
+        paged_pages<0>(src, a.tables + (size_t)s * a.max_blocks, h, p_begin, p_end, ctx, qop, vt, lane, m_l, l_l,
+                       O);
         paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
     }
 }
 
-hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t grid_items, hipStream_t st) {
-    OMEGA_LAUNCH(k_paged_items, dim3(4, grid_items), dim3(64), 0, st, a);
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t waves, hipStream_t st) {
+    OMEGA_LAUNCH(k_paged_items, dim3(4, waves), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -668,61 +698,89 @@ hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// The ragged splits of every (seq, q head) combined, then split into the o projection's e4m3
-// terms (the head's 128 dims are one 128-column block of o's input). Workgroup = (seq, head),
-// wavefront q = dims 32 q .. 32 q + 31 of up to 256 splits (the k_attn_combine<4> pattern); the
-// head's row meets in LDS and 16 lanes split it.
+// The items of every (seq, q head) combined, then split into the o projection's e4m3 terms (the
+// head's 128 dims are one 128-column block of o's input). Workgroup = (seq, head) of 256 threads:
+// the items' (m, l) are read by thread j % 256 of item j, their weights exp(m - M) staged in LDS;
+// thread t then sums dims 4 (t % 32) .. +3 over the items j = t / 32 (mod 8) and the 8 groups
+// meet in LDS in a fixed order; 16 lanes split the head's row.
 __global__ __launch_bounds__(256) void k_attn_combine_items(const CombineItemsArgs a) {
-    constexpr int CH = 4;
-    __shared__ float wsh[4][64 * CH];
+    constexpr uint32_t kRounds = (kCombineMaxItems + 255) / 256;
+    __shared__ float wsh[kRounds * 256];
+    __shared__ float red[2][4];
+    __shared__ f32x4 osum[8][32];
     __shared__ float orow[128];
-    const uint32_t s = blockIdx.x >> 5, head = blockIdx.x & 31;
-    const uint32_t lane = lane_id(), quarter = threadIdx.x >> 6;
-    const uint32_t d = 32 * quarter + (lane & 31), half = lane >> 5;
-    const uint32_t off = a.item_off[s], splits = a.item_off[s + 1] - off;  // 1 ..= 256
-    auto slot = [&](uint32_t j) { return a.part + ((size_t)(off + min(j, splits - 1)) * 32 + head) * kPartStride; };
-    float m_raw[CH], l_raw[CH];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        m_raw[c] = *as_global_f32(slot(64 * c + lane));
-        l_raw[c] = *as_global_f32(slot(64 * c + lane) + 1);
-    }
-    constexpr uint32_t kPer = 32 * CH;
-    float f[kPer];
-#pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) f[k] = *as_global_f32(slot(2 * k + half) + 4 + d);
+    const uint32_t s = blockIdx.x >> 5, head = blockIdx.x & 31, t = threadIdx.x;
+    const uint32_t lane = lane_id(), wid = t >> 6;
+    const uint32_t off = a.item_off[s], n = a.item_off[s + 1] - off;  // 1 ..= kCombineMaxItems
+    constexpr size_t kItem = 32 * (size_t)kPartStride;                // floats from one item to the next
+    const float *base = a.part + ((size_t)off * 32 + head) * kPartStride;
+    float mv[kRounds], lv[kRounds];
     float M = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) M = fmaxf(M, 64 * c + lane < splits ? m_raw[c] : -INFINITY);
+    for (uint32_t r = 0; r < kRounds; ++r) {
+        const uint32_t j = min(t + 256 * r, n - 1);
+        const u32x2 ml = *as_global_u32x2(base + j * kItem);
+        mv[r] = __uint_as_float(ml.x);
+        lv[r] = __uint_as_float(ml.y);
+        M = t + 256 * r < n ? fmaxf(M, mv[r]) : M;
+    }
     M = row16_max(M);
     M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
-    float L = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const bool mine = 64 * c + lane < splits;
-        const float w = mine ? expf(m_raw[c] - M) : 0.f;
-        L += wave_sum(w * (mine ? l_raw[c] : 0.f));
-        wsh[quarter][64 * c + lane] = w;
-    }
+    if (lane == 0) red[0][wid] = M;
     __syncthreads();
-    float O = 0.f;
+    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float Lp = 0.f;
 #pragma unroll
-    for (uint32_t k = 0; k < kPer; ++k) {
-        const uint32_t j = 2 * k + half;
-        O = j < splits ? fmaf(f[k], wsh[quarter][j], O) : O;
+    for (uint32_t r = 0; r < kRounds; ++r) {
+        const uint32_t j = t + 256 * r;
+        const float w = j < n ? expf(mv[r] - M) : 0.f;
+        wsh[j] = w;
+        Lp += j < n ? w * lv[r] : 0.f;
     }
-    O = xor_sum<32>(O);
-    if (lane < 32) orow[d] = O / L;
+    Lp = wave_sum(Lp);
+    if (lane == 0) red[1][wid] = Lp;
     __syncthreads();
-    if (threadIdx.x < 16) {
-        const uint32_t j = threadIdx.x;
+    const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    const uint32_t grp = t >> 5, d4 = t & 31;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (uint32_t j = grp; j < n; j += 8) {
+        const f32x4 v = *as_global_f32x4(base + j * kItem + 4 + 4 * d4);
+        const float w = wsh[j];
+        o.x = fmaf(w, v.x, o.x);
+        o.y = fmaf(w, v.y, o.y);
+        o.z = fmaf(w, v.z, o.z);
+        o.w = fmaf(w, v.w, o.w);
+    }
+    osum[grp][d4] = o;
+    __syncthreads();
+    if (t < 32) {
+        f32x4 sum = osum[0][t];
+#pragma unroll
+        for (int g = 1; g < 8; ++g) {
+            const f32x4 v = osum[g][t];
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        const f32x4 r = {sum.x / L, sum.y / L, sum.z / L, sum.w / L};
+        if (a.out) *reinterpret_cast<f32x4 *>(a.out + ((size_t)s * 32 + head) * 128 + 4 * t) = r;
+        orow[4 * t + 0] = r.x;
+        orow[4 * t + 1] = r.y;
+        orow[4 * t + 2] = r.z;
+        orow[4 * t + 3] = r.w;
+    }
+    if (a.out) return;  // uniform: the f32 rows are the result
+    __syncthreads();
+    if (t < 16) {
         float v[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = orow[8 * j + i];
+        for (int i = 0; i < 8; ++i) v[i] = orow[8 * t + i];
         u32x2 q[kTerms];
         float sc[kTerms];
         split8(v, q, sc, false);
-        store_split(a.oq, a.os, s, 32, head, j, q, sc);
+        store_split(a.oq, a.os, s, 32, head, t, q, sc);
     }
 }
 
@@ -1332,6 +1390,69 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     cb.mutant = a.mutant;
     OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
     OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
+    return OMEGA_GPU_ATTN_OK;
+}
+
+int omega_gpu_paged_attention_items_dev(const float *q_dev, const void *pool_dev, const OmegaGpuKvLayout *layout,
+                                        const int32_t *block_tables_dev, uint32_t max_blocks_per_seq,
+                                        const uint32_t *positions, uint32_t num_seqs, uint32_t layer_idx,
+                                        float *out_dev) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_ATTN);
+    if (!q_dev || !pool_dev || !layout || !block_tables_dev || !positions || !out_dev || num_seqs == 0 ||
+        num_seqs > kItemMaxSeqs) {
+        set_error(F_ATTN, "paged attention items: NULL pointer or %u sequences (1..=%u)", num_seqs, kItemMaxSeqs);
+        return OMEGA_GPU_ATTN_BAD_ARGS;
+    }
+    int rc = check_layout(layout, layer_idx, 4);
+    if (rc) return rc;
+    if (layout->block_size != 16) {
+        set_error(F_ATTN, "paged attention items: 16-token pages required (block_size %u)", layout->block_size);
+        return OMEGA_GPU_ATTN_BAD_ARGS;
+    }
+    ItemPlan plan{};
+    uint32_t first[kItemMaxSeqs + 1];
+    uint32_t total = 0;
+    for (uint32_t s = 0; s < num_seqs; ++s) {
+        if ((uint64_t)positions[s] >= (uint64_t)max_blocks_per_seq * 16) {
+            set_error(F_ATTN, "paged attention items: sequence %u position %u past its %u-page table", s,
+                      positions[s], max_blocks_per_seq);
+            return OMEGA_GPU_ATTN_BAD_ARGS;
+        }
+        first[s] = total;
+        total += (positions[s] + 1 + 15) / 16;
+    }
+    first[num_seqs] = total;
+    plan_items(first, num_seqs, plan);
+    Ctx *cx = ctx(F_ATTN);
+    if (!cx) return OMEGA_GPU_ATTN_CHIP_FAIL;
+    const size_t plan_bytes = (sizeof(ItemPlan) + 255) / 256 * 256, pos_bytes = 256;
+    if (!ensure_scratch(F_ATTN, cx, plan_bytes + pos_bytes + (size_t)kItemMax * 32 * kPartStride * 4))
+        return OMEGA_GPU_ATTN_CHIP_FAIL;
+    uint8_t *base = static_cast<uint8_t *>(cx->scratch);
+    ItemPlan *dplan = reinterpret_cast<ItemPlan *>(base);
+    uint32_t *dpos = reinterpret_cast<uint32_t *>(base + plan_bytes);
+    OMEGA_HIP(F_ATTN, hipMemcpyAsync(dplan, &plan, sizeof(ItemPlan), hipMemcpyHostToDevice, cx->stream));
+    OMEGA_HIP(F_ATTN, hipMemcpyAsync(dpos, positions, num_seqs * 4, hipMemcpyHostToDevice, cx->stream));
+    PagedItemsArgs pa;
+    pa.q = q_dev;
+    pa.pool = static_cast<const uint8_t *>(pool_dev);
+    pa.g = geom_of(*layout);
+    pa.layer = layer_idx;
+    pa.tables = block_tables_dev;
+    pa.max_blocks = max_blocks_per_seq;
+    pa.pos = dpos;
+    pa.wave_off = dplan->wave_off;
+    pa.items = &dplan->items[0][0];
+    pa.part = reinterpret_cast<float *>(base + plan_bytes + pos_bytes);
+    OMEGA_HIP(F_ATTN, launch_paged_items(pa, kItemWaves, cx->stream));
+    CombineItemsArgs ca;
+    ca.part = pa.part;
+    ca.item_off = dplan->item_off;
+    ca.out = out_dev;
+    OMEGA_HIP(F_ATTN, launch_attn_combine_items(ca, num_seqs, cx->stream));
+    // the host plan and positions are read by the copies above: wait before they go out of scope
+    OMEGA_HIP(F_ATTN, hipStreamSynchronize(cx->stream));
     return OMEGA_GPU_ATTN_OK;
 }
 

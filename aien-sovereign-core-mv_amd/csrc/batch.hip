@@ -38,17 +38,13 @@ void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out
 
 constexpr uint32_t kBdH = 2048, kBdQkv = 5120, kBdAttn = 4096;
 constexpr uint32_t kBdMaxSeqs = 32;
-constexpr uint32_t kBdMinPps = 32;     // pages per attention work item (512 tokens) at least
-constexpr uint32_t kBdMaxItems = 256;  // attention work items per sequence at most
-constexpr uint32_t kBdGridItems = 1024;
+static_assert(kBdMaxSeqs <= kItemMaxSeqs, "the attention plan covers every sequence");
 
 // the device words the host writes before every step (and the argmax slots it reads back)
 struct BdIo {
     uint32_t tok[kBdMaxSeqs];
     uint32_t pos[kBdMaxSeqs];           // the token's position: its KV slot; context = pos + 1
-    uint32_t item_off[kBdMaxSeqs + 1];  // attention items of sequence s: [item_off[s], item_off[s + 1])
-    uint32_t pps[kBdMaxSeqs];           // pages per item of sequence s
-    uint32_t pad[3];
+    ItemPlan plan;                      // the step's attention work items
     unsigned long long argmax[kBdMaxSeqs][kArgmaxSlots];
 };
 static_assert(offsetof(BdIo, argmax) % 8 == 0, "argmax slots 8-byte aligned");
@@ -475,15 +471,14 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         pa.layer = l;
         pa.tables = b->tables;
         pa.max_blocks = c.max_blocks_per_seq;
-        pa.seqs = T;
         pa.pos = b->io->pos;
-        pa.item_off = b->io->item_off;
-        pa.pps = b->io->pps;
+        pa.wave_off = b->io->plan.wave_off;
+        pa.items = &b->io->plan.items[0][0];
         pa.part = b->apart;
-        OMEGA_HIP(F_SESSION, launch_paged_items(pa, kBdGridItems, st));
+        OMEGA_HIP(F_SESSION, launch_paged_items(pa, kItemWaves, st));
         CombineItemsArgs ca;
         ca.part = b->apart;
-        ca.item_off = b->io->item_off;
+        ca.item_off = b->io->plan.item_off;
         ca.oq = b->oq;
         ca.os = b->os;
         OMEGA_HIP(F_SESSION, launch_attn_combine_items(ca, T, st));
@@ -600,7 +595,7 @@ int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpu
     M((void **)&b->xs, (size_t)T * (kBdH / 128) * 16);
     M((void **)&b->qkv_part, (size_t)(kBdH / 256) * T * kBdQkv * 4);
     M((void **)&b->q, (size_t)T * 32 * 128 * 4);
-    M((void **)&b->apart, (size_t)T * kBdMaxItems * 32 * kPartStride * 4);
+    M((void **)&b->apart, (size_t)kItemMax * 32 * kPartStride * 4);
     M((void **)&b->oq, (size_t)T * 32 * kTerms * 128);
     M((void **)&b->os, (size_t)T * 32 * 16);
     M((void **)&b->o_part, (size_t)(kBdAttn / 256) * T * kBdH * 4);
@@ -768,7 +763,8 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
         }
     BdIo *p = b->pin;
     memset(p, 0, sizeof(BdIo));
-    uint32_t off = 0;
+    uint32_t total = 0;
+    uint32_t first[kBdMaxSeqs + 1];  // the sequences' pages laid end to end
     for (uint32_t s = 0; s < seqs; ++s) {
         if (positions[s] >= b->cfg.max_pos) {
             set_error(F_SESSION, "batch decode step: sequence %u position %u >= max_pos %u", s, positions[s],
@@ -783,13 +779,11 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
         }
         p->tok[s] = tokens[s];
         p->pos[s] = positions[s];
-        const uint32_t pages = (positions[s] + 1 + 15) / 16;
-        const uint32_t pps = std::max(kBdMinPps, (pages + kBdMaxItems - 1) / kBdMaxItems);
-        p->pps[s] = pps;
-        p->item_off[s] = off;
-        off += (pages + pps - 1) / pps;
+        first[s] = total;
+        total += (positions[s] + 1 + 15) / 16;
     }
-    p->item_off[seqs] = off;
+    first[seqs] = total;
+    plan_items(first, seqs, p->plan);
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     if (b->eager) {

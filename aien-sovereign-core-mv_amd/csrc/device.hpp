@@ -47,6 +47,13 @@ __device__ __forceinline__ const gf32x4 *as_global_f32x4(const void *p) {
     return (const gf32x4 *)(uintptr_t)p;
 }
 
+// Read-only words at a wave-uniform address, through the constant address space: the load is a
+// scalar load (its result in an SGPR, counted by lgkmcnt rather than the vector-memory counter).
+typedef const __attribute__((address_space(4))) uint32_t cu32;
+__device__ __forceinline__ const cu32 *as_const_u32(const void *p) {
+    return (const cu32 *)(uintptr_t)p;
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -231,26 +231,46 @@ size_t moe_work_bytes(uint32_t tokens);
 // Ragged paged attention (GQA 32 q / 4 kv heads over 16-token pages, the matrix-core page loop):
 // item i is split i - item_off[s] of sequence s, pages [split * pps[s], +pps[s]) of its pos[s] + 1
 // tokens; partials at part[(i * 32 + q head) * kPartStride].
+// The attention work of a batched decode step over ragged sequences: the sequences' pages laid
+// end to end are cut into kItemWaves equal runs, one per wavefront of each kv head (4 x 512 =
+// 2048 = 256 CUs x 8, the paged kernel's occupancy of 2 per SIMD: every wavefront is resident at
+// once and they all finish together), and each run into items at sequence boundaries.
+constexpr uint32_t kItemWaves = 512;
+constexpr uint32_t kItemMaxSeqs = 32;
+constexpr uint32_t kItemMax = kItemWaves + kItemMaxSeqs;  // items of a step at most
+struct ItemPlan {
+    uint32_t item_off[kItemMaxSeqs + 1];  // items of sequence s: [item_off[s], item_off[s + 1])
+    uint32_t pad[3];
+    uint32_t wave_off[kItemWaves + 4];    // items of wavefront w: [wave_off[w], wave_off[w + 1])
+    uint32_t items[kItemMax][2];          // {seq << 24 | first page, end page}
+};
+// first[s] .. first[s + 1]: sequence s's pages laid end to end (every sequence has >= 1 page)
+void plan_items(const uint32_t *first, uint32_t seqs, ItemPlan &p);
+
 struct PagedItemsArgs {
     const float *q = nullptr;            // [seqs][32][128] post-norm, post-RoPE
     const uint8_t *pool = nullptr;
     KvGeom g{};
     uint32_t layer = 0;
     const int32_t *tables = nullptr;     // [seqs][max_blocks]
-    uint32_t max_blocks = 0, seqs = 0;
+    uint32_t max_blocks = 0;
     const uint32_t *pos = nullptr;       // [seqs]
-    const uint32_t *item_off = nullptr;  // [seqs + 1]
-    const uint32_t *pps = nullptr;       // [seqs] pages per item
-    float *part = nullptr;
+    const uint32_t *wave_off = nullptr;  // [waves + 1]: items of wavefront w
+    const uint32_t *items = nullptr;     // [items][2]: {seq << 24 | first page, end page}
+    float *part = nullptr;               // [items][32][kPartStride]
 };
-hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t grid_items, hipStream_t st);
-// the items' partials of every (seq, q head) combined (at most 256 items per sequence) and split
-// into the o projection's input terms: oq [seqs][32][4][128] e4m3, os [seqs][32][4]
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t waves, hipStream_t st);
+// the items' partials of every (seq, q head) combined (at most kCombineMaxItems items per
+// sequence) and split into the o projection's input terms: oq [seqs][32][4][128] e4m3,
+// os [seqs][32][4]
+constexpr uint32_t kCombineMaxItems = 768;
+static_assert(kItemWaves <= kCombineMaxItems, "a sequence may get an item from every wavefront");
 struct CombineItemsArgs {
     const float *part = nullptr;
-    const uint32_t *item_off = nullptr;
+    const uint32_t *item_off = nullptr;  // [seqs + 1]: items of sequence s
     uint8_t *oq = nullptr;
     float *os = nullptr;
+    float *out = nullptr;                // when set: the f32 rows [seqs][32][128] instead of the split
 };
 hipError_t launch_attn_combine_items(const CombineItemsArgs &a, uint32_t seqs, hipStream_t st);
 

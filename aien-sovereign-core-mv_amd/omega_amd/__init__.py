@@ -220,6 +220,7 @@ SIGNATURES = {
     "omega_gpu_fp8_gemv_dev": (i32, [P, u32, P, P]),
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
+    "omega_gpu_paged_attention_items_dev": (i32, [P, P, C.POINTER(KvLayout), P, u32, P, u32, u32, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),

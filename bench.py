@@ -152,6 +152,85 @@ def copy_probe(nbytes):
     print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
 
 
+# ---------------------------------------------------------------- configuration 1: the q|k|v FP8 GEMV
+GEMV_COPIES = 48
+
+
+def gemv_bytes():
+    """Algorithmic HBM bytes of one configuration-1 GEMV: 5120 x 2048 e4m3 weights, 40 x 16 f32
+    block scales, the f32 activation row in and the f32 output row out."""
+    return 5120 * 2048 + 40 * 16 * 4 + H * 4 + 5120 * 4
+
+
+def gemv_cpu_baseline():
+    """The oracle's FP8 GEMV (oref_fp8_grouped: one group, in-order f32 accumulation) on one host
+    thread, for about 10 s."""
+    import pyoracle as orc
+
+    w, s_ = orc.synth_fp8(SEED, 3000, 1, 5120, 2048)
+    x = orc.bf16_to_f32(orc.synth_bf16(SEED, 7, (H,), 1.0))
+    reps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        orc.fp8_grouped(w, s_, np.zeros(1, np.uint32), x, threads=1)
+        reps += 1
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return {"value": round(us, 1), "unit": "us/GEMV", "cores": 1, "kind": "port",
+            "sample": f"oracle oref_fp8_grouped (oracle/oracle.c), one 5120 x 2048 GEMV, {reps} calls "
+                      f"in about 10 s on one host thread"}
+
+
+def bench_gemv(om, args):
+    """Configuration 1: the fused q|k|v FP8 GEMV (5120 x 2048 e4m3 N(0, 0.02) block-quantised,
+    x a bf16 N(0, 1) row) as device-pointer GEMVs rotating over 48 distinct weight copies (504 MB,
+    about twice the 256 MB Infinity Cache), captured once as a hipGraph of 48 launches and replayed;
+    the time per GEMV includes the graph's launch gap between dependent kernels."""
+    import ctypes as C
+
+    h = om.hip()
+    lib = om.lib()
+    ts = [om.Fp8Tensor.synth(1, 5120, 2048, SEED, 3000 + c) for c in range(GEMV_COPIES)]
+    x = om.DeviceBuffer.from_array(om.synth_bf16_host(SEED, 7, (H,), 1.0).astype(np.uint32) << 16)
+    y = om.DeviceBuffer(5120 * 4)
+    om.sync()
+    stream = lib.omega_gpu_stream()
+    graph, exe = C.c_void_p(), C.c_void_p()
+    assert h.hipStreamBeginCapture(C.c_void_p(stream), 1) == 0   # hipStreamCaptureModeThreadLocal
+    for t in ts:
+        assert lib.omega_gpu_fp8_gemv_dev(t.as_raw(), 0, x.ptr, y.ptr) == 0
+    assert h.hipStreamEndCapture(C.c_void_p(stream), C.byref(graph)) == 0
+    assert h.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)) == 0
+    timer = om.StreamTimer()
+    reps = args.gemv_reps
+    for _ in range(2):
+        assert h.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
+    timer.start()
+    for _ in range(reps):
+        assert h.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
+    timer.stop()
+    ms = timer.ms()
+    us = ms * 1e3 / (reps * GEMV_COPIES)
+    b = gemv_bytes()
+    gbs = b / (us * 1e3)
+    h.hipGraphExecDestroy(exe)
+    h.hipGraphDestroy(graph)
+    cpu = None if args.no_cpu else gemv_cpu_baseline()
+    print(json.dumps({
+        "metric": "FP8 block-scaled GEMV 5120 x 2048 (configuration 1), achieved HBM GB/s vs peak",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "us_per_gemv": round(us, 3), "gemvs": reps * GEMV_COPIES,
+        "dtype": "fp8 (e4m3 weights, f32 activations, fp32 accumulate)",
+        "data": "synthetic N(0, 0.02) weights block-quantised to e4m3, bf16 N(0,1) row",
+        "config": {"workload": "q|k|v GEMV 5120 x 2048, 48 weight copies, hipGraph of 48 launches"},
+        "roofline": {"bound": "hbm", "kernel": "k_fp8_rows", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu}), flush=True)
+    for t in ts:
+        t.free()
+    x.free()
+    y.free()
+
+
 # ---------------------------------------------------------------- configuration 3: paged attention
 PAGED_POINTS = [(b, l) for b in (1, 8, 32) for l in (2048, 8192, 32768)]
 
@@ -331,7 +410,7 @@ def bench_moe(om, args):
     print(json.dumps({
         "metric": "Qwen3-30B-A3B MoE block (configuration 2) at token batch 32, achieved HBM GB/s vs peak",
         "value": big["GBs"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
-        "dtype": "fp8 (e4m3 weights, 3-term e4m3 activations, fp32 accumulate)",
+        "dtype": "fp8 (e4m3 weights, 4-term e4m3 activations, fp32 accumulate)",
         "data": "synthetic random-init weights and bf16 N(0,1) rows",
         "config": {"workload": "MoE block, 128 experts top-8, hidden 2048, intermediate 768",
                    "tokens": [1, 32]},
@@ -493,8 +572,9 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "paged", "moe", "serve"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve"], default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
+                         "gemv: the q|k|v FP8 GEMV (configuration 1); "
                          "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
                          "at token batch 1 and 32 (configuration 2); serve: 32 sequences of batched "
                          "decode over long contexts (configuration 5)")
@@ -502,6 +582,7 @@ def main():
     ap.add_argument("--serve-warmup", type=int, default=4)
     ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--moe-reps", type=int, default=20)
+    ap.add_argument("--gemv-reps", type=int, default=200)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES (byte-counter calibration)")
     args = ap.parse_args()
@@ -517,6 +598,9 @@ def main():
         sys.exit(3)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.workload == "gemv":
+        bench_gemv(om, args)
         return
     if args.workload == "paged":
         bench_paged(om, args)

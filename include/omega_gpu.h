@@ -500,6 +500,17 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
                                         uint32_t max_context, uint32_t layer_idx,
                                         uint32_t num_q_heads, uint32_t num_kv_heads,
                                         uint32_t head_dim, float *out_dev);
+/* The batched serving step's attention on its own (not in the reference ABI; the ragged batch of
+ * paged_attention_batch_bf16, crates/aien-omega-gpu/src/lib.rs:910-1041, with GQA 32 q / 4 kv
+ * heads of 128 over 16-token pages): sequence s attends over positions 0..=positions[s] (host
+ * array) through its table row; the pages of all sequences are split into equal runs per
+ * wavefront (the work plan of omega_gpu_batch_decode_step). q_dev [num_seqs][32][128] f32
+ * (post-norm, post-RoPE), out_dev [num_seqs][32][128] f32; num_seqs <= 32. Synchronises the
+ * library stream before returning. */
+int omega_gpu_paged_attention_items_dev(const float *q_dev, const void *pool_dev, const OmegaGpuKvLayout *layout,
+                                        const int32_t *block_tables_dev, uint32_t max_blocks_per_seq,
+                                        const uint32_t *positions, uint32_t num_seqs, uint32_t layer_idx,
+                                        float *out_dev);
 /* the decode graph with the embedding row gathered on the device: set a [vocab][2048] bf16
  * tensor once, then each token passes only its id */
 int omega_gpu_decode_graph_set_embedding(OmegaGpuDecodeGraph *g, const void *embed_bf16);

@@ -8,8 +8,14 @@ device KV pool of the aien-kv-cache page layout, each with its own random page t
 Bars: per sequence and step, the greedy token equals the oracle engine's (one engine per
 sequence, the reference's per-token step); logits within 2e-3 relative while the routing of
 every layer agrees; a first routing difference only at a near tie (the oracle's logit margin
-< 1e-3 between the two ranks that differ: rank 8 / 9, or two ranks swapped inside the top 8). Batch invariance: a sequence's tokens and logits are bit-identical whatever the rest
-of the batch holds and whatever the batch size.
+< 1e-3 between the two ranks that differ: rank 8 / 9, or two ranks swapped inside the top 8).
+
+Batch invariance: every kernel but attention computes a sequence's row the same way whatever the
+batch holds. Attention cuts the step's pages into equal runs per wavefront, so while the step
+holds at most 512 pages (here: 32 sequences of at most 16 pages) every page is its own work item
+and a sequence's tokens and logits are bit-identical whatever the rest of the batch holds and
+whatever the batch size; past that, a sequence's split points depend on the other sequences'
+lengths and its results agree to rounding.
 """
 import numpy as np
 import pytest

@@ -159,3 +159,78 @@ def test_paged_mutants_are_caught(omega, oracle, mutant):
     assert max(errs) > TOL, errs
     clean = run_dev(omega, pool, q, tabs, lens, 0).reshape(2, QH * HD)
     assert max(rel_err(clean[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) for b in range(2)) <= TOL
+
+
+# ---------------------------------------------------------------- the serving step's balanced items
+def run_items(omega, pool, q, tabs, lens, layer):
+    """omega_gpu_paged_attention_items_dev: sequence b attends over positions 0..lens[b]-1."""
+    lib = omega.lib()
+    seqs, maxb = tabs.shape
+    qd = omega.DeviceBuffer.from_array(q)
+    td = omega.DeviceBuffer.from_array(tabs.astype(np.int32))
+    od = omega.DeviceBuffer(q.nbytes)
+    pos = np.ascontiguousarray(lens - 1, dtype=np.uint32)
+    rc = lib.omega_gpu_paged_attention_items_dev(qd.ptr, pool.dev.ptr, C.byref(pool.L), td.ptr, maxb,
+                                                 pos.ctypes.data, seqs, layer, od.ptr)
+    if rc != 0:
+        raise omega.OmegaGpuError(rc, omega._s(lib.omega_gpu_attention_last_error()))
+    out = od.download(np.float32, q.size)
+    for b in (qd, td, od):
+        b.free()
+    return out
+
+
+@pytest.mark.parametrize("case", ["mixed", "one_long", "many_short", "config5_like"])
+def test_balanced_items_match_the_oracle(omega, oracle, case):
+    # The pages of all sequences are cut into 512 equal runs per kv head: a run may cover several
+    # short sequences, a long sequence spans many runs, and a run may start or end inside a page
+    # range of any sequence. Contexts ending inside a page have NaN / inf in the unwritten slots.
+    rng = np.random.default_rng({"mixed": 41, "one_long": 42, "many_short": 43, "config5_like": 44}[case])
+    if case == "mixed":
+        lens = np.array([1, 5, 17, 333, 1000, 2047, 4099, 9001, 16000], np.int32)
+    elif case == "one_long":
+        lens = np.array([32768 - 5], np.int32)
+    elif case == "many_short":
+        lens = rng.integers(1, 40, 32).astype(np.int32)
+    else:
+        lens = np.exp(rng.uniform(np.log(1024), np.log(12288), 32)).astype(np.int32)
+    pages = (lens + 15) // 16
+    nb = max(4096, int(pages.sum()) + 1)
+    pool = Pool(omega, oracle, rng, nb, 2)
+    maxb = int(pages.max()) + 2
+    tabs = np.full((lens.size, maxb), -1, np.int32)
+    free = rng.permutation(nb)  # disjoint pages: a poisoned tail belongs to its sequence only
+    used = 0
+    for b, n_b in enumerate(pages):
+        tabs[b, :n_b] = free[used:used + n_b]
+        used += n_b
+    for b, cl in enumerate(lens):
+        if cl % 16:
+            pool.poison_tail(oracle, tabs[b], int(cl), 1)
+    q = rng.standard_normal((lens.size, QH * HD)).astype(np.float32)
+    out = run_items(omega, pool, q, tabs, lens, 1).reshape(lens.size, QH * HD)
+    assert np.isfinite(out).all()
+    check = range(lens.size) if lens.size <= 9 else (0, 7, 19, 31)
+    for b in check:
+        e = rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], int(lens[b]), 1))
+        assert e <= TOL, (case, b, int(lens[b]), e)
+    # deterministic: the same call gives the same bits
+    np.testing.assert_array_equal(run_items(omega, pool, q, tabs, lens, 1).reshape(lens.size, QH * HD), out)
+    pool.dev.free()
+
+
+def test_balanced_items_refusals(omega, oracle):
+    rng = np.random.default_rng(45)
+    pool = Pool(omega, oracle, rng, 64, 1)
+    q = rng.standard_normal((2, QH * HD)).astype(np.float32)
+    tabs = rng.permutation(64)[:8].reshape(2, 4).astype(np.int32)
+    with pytest.raises(omega.OmegaGpuError):
+        run_items(omega, pool, q, tabs, np.array([65, 3], np.int32), 0)   # position 64 past 4 pages
+    with pytest.raises(omega.OmegaGpuError):
+        run_items(omega, pool, q, tabs, np.array([3, 3], np.int32), 1)    # layer outside the pool
+    q33 = rng.standard_normal((33, QH * HD)).astype(np.float32)
+    with pytest.raises(omega.OmegaGpuError):
+        run_items(omega, pool, q33, np.zeros((33, 4), np.int32), np.full(33, 3, np.int32), 0)
+    out = run_items(omega, pool, q, tabs, np.array([64, 1], np.int32), 0)  # the whole table
+    assert np.isfinite(out).all()
+    pool.dev.free()
