@@ -279,8 +279,7 @@ hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
 // so each page's V tile is read coalesced (16 lanes per 256-byte row), staged in LDS and read
 // back transposed. Tokens at or past the context in the last page may hold anything (unwritten
 // slots): their scores are selected to -inf and their V rows to zero before staging, so neither
-// reaches the result. The page table of the split is read 64 entries at a time into one VGPR
-// and the page ids taken by readlane, so no page load waits on a table load.
+// reaches the result.
 constexpr uint32_t kVtRow = 272;  // bytes per staged V row: 256 + 16 (rows 4 g apart on distinct banks)
 
 struct PagedRegs {
@@ -446,15 +445,15 @@ __global__ __launch_bounds__(64) void k_paged(const AttnArgs a) {
                 lane, m_l, l_l, O);
 }
 
-// Wavefront w takes the run [w r, (w + 1) r) of the pages laid end to end, r = ceil(total /
-// kItemWaves), cut into items at sequence boundaries. The items come out in page order, so each
-// sequence's items are consecutive (item_off) and at most kItemWaves + seqs - 1 of them exist; a
-// sequence gets at most one item per wavefront.
+// Workgroup w takes the run [w r, (w + 1) r) of the pages laid end to end, r = ceil(total /
+// kItemRuns), cut into items at sequence boundaries. The items come out in page order, so each
+// sequence's items are consecutive (item_off) and at most kItemRuns + seqs - 1 of them exist; a
+// sequence gets at most one item per run.
 void plan_items(const uint32_t *first, uint32_t seqs, ItemPlan &p) {
-    const uint32_t total = first[seqs], run = (total + kItemWaves - 1) / kItemWaves;
+    const uint32_t total = first[seqs], run = (total + kItemRuns - 1) / kItemRuns;
     uint32_t n = 0, s = 0;
-    for (uint32_t w = 0; w < kItemWaves; ++w) {
-        p.wave_off[w] = n;
+    for (uint32_t w = 0; w < kItemRuns; ++w) {
+        p.run_off[w] = n;
         uint32_t b = std::min(total, w * run);
         const uint32_t e = std::min(total, b + run);
         while (b < e) {
@@ -467,21 +466,137 @@ void plan_items(const uint32_t *first, uint32_t seqs, ItemPlan &p) {
             b = pe;
         }
     }
-    p.wave_off[kItemWaves] = n;
+    p.run_off[kItemRuns] = n;
     p.item_off[seqs] = n;
 }
 
-// Balanced work items (the batched decode step): the pages of all sequences, laid end to end,
-// are cut into one contiguous run per wavefront (the same number of pages each, so every
-// wavefront of a kv head finishes together), and each run into items at sequence boundaries.
-// Wavefront w of kv head h serves items [wave_off[w], wave_off[w + 1]); item i is pages
+// ---------------------------------------------------------------- paged, four kv heads per workgroup
+// GQA group 8 with four kv heads (the Qwen3-30B-A3B shape): one workgroup of four wavefronts per
+// run of pages, wavefront w = kv head w. A page's K and V planes are loaded whole token rows at
+// a time (wavefront w loads tokens 4 w .. 4 w + 3, one contiguous 1 KiB row of all four heads
+// per load instruction, where a per-head load would read 64-byte pieces of 16 rows), staged in
+// LDS, and each wavefront reads its head's rows back in the matrix-core layouts; V rows past
+// the context are zeroed when staged. Two barriers per page: the previous page's reads are done,
+// the page is staged.
+constexpr uint32_t kRow4 = 1040;  // bytes per staged token row: 4 heads x 256 + 16
+
+struct Paged4Regs {
+    u32x4 k[4];  // token rows 4 w + j: lane l holds head l / 16, bytes 16 (l % 16) .. +16
+    u32x4 v[4];
+};
+
+template <int MUT>
+__device__ __forceinline__ void paged4_load(const PagedSrc &a, const cu32 *ctab, uint32_t blk, uint32_t page,
+                                            uint32_t ctx, uint32_t w, uint32_t lane, Paged4Regs &R) {
+    const uint64_t lane_off = (uint64_t)(lane >> 4) * a.g.head_stride + 16 * (lane & 15);
+    const uint64_t layer_off = (uint64_t)a.layer * a.g.layer_stride;
+    const uint8_t *pg = a.pool + (uint64_t)blk * a.g.block_stride + layer_off + lane_off;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t t = 4 * w + j;
+        R.k[j] = __builtin_nontemporal_load(as_global(pg + (uint64_t)t * a.g.token_stride));
+        const uint8_t *vpg = pg;
+        uint32_t tv = t;
+        if (MUT == 2) {  // test mutant: V one position late (clamped to the last token)
+            const uint32_t pos = min(page * 16 + t + 1, ctx - 1);
+            tv = pos & 15;
+            vpg = a.pool + (uint64_t)ctab[pos >> 4] * a.g.block_stride + layer_off + lane_off;
+        }
+        R.v[j] = __builtin_nontemporal_load(as_global(vpg + a.g.plane_stride + (uint64_t)tv * a.g.token_stride));
+    }
+}
+
+// stage the page (all waves) and read back kv head w's operands
+__device__ __forceinline__ void paged4_stage(const Paged4Regs &R, uint32_t tok0, uint32_t ctx, uint32_t w,
+                                             uint32_t lane, uint8_t *kt, uint8_t *vt, DattnPage &T) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    __syncthreads();  // every wave's reads of the previous page are done
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t t = 4 * w + j;
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4 *>(kt + t * kRow4 + 16 * lane) = R.k[j];
+        *reinterpret_cast<u32x4 *>(vt + t * kRow4 + 16 * lane) = tok0 + t < ctx ? R.v[j] : z;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        T.k[ks] = *reinterpret_cast<const u32x4 *>(kt + n * kRow4 + 256 * w + 64 * ks + 16 * g);
+    const uint16_t *v16 = reinterpret_cast<const uint16_t *>(vt) + 128 * w;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        const uint32_t col = 16 * nb + n;
+        const uint32_t e0 = v16[(4 * g + 0) * (kRow4 / 2) + col];
+        const uint32_t e1 = v16[(4 * g + 1) * (kRow4 / 2) + col];
+        const uint32_t e2 = v16[(4 * g + 2) * (kRow4 / 2) + col];
+        const uint32_t e3 = v16[(4 * g + 3) * (kRow4 / 2) + col];
+        T.v[nb] = u32x2{e0 | (e1 << 16), e2 | (e3 << 16)};
+    }
+}
+
+// pages [p_begin, p_end) of all four kv heads: the two-set straight-path loop of paged_pages
+template <int MUT>
+__device__ __forceinline__ void paged4_pages(const PagedSrc &src, const int32_t *tab, uint32_t w, uint32_t p_begin,
+                                             uint32_t p_end, uint32_t ctx, const bf16x8 (&qop)[4], uint8_t *kt,
+                                             uint8_t *vt, uint32_t lane, float &m_l, float &l_l, f32x4 (&O)[8]) {
+    const uint32_t g = lane >> 4, n = lane & 15, last = p_end - 1;
+    const cu32 *ctab = as_const_u32(tab);
+    Paged4Regs A, B;
+    const uint32_t p1 = min(p_begin + 1, last);
+    paged4_load<MUT>(src, ctab, ctab[p_begin], p_begin, ctx, w, lane, A);
+    paged4_load<MUT>(src, ctab, ctab[p1], p1, ctx, w, lane, B);
+    m_l = -INFINITY;
+    l_l = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    DattnPage T;
+    for (uint32_t p = p_begin; p < p_end; p += 2) {
+        const uint32_t pa = min(p + 2, last), pb = min(p + 3, last);
+        const uint32_t blk_a = ctab[pa], blk_b = ctab[pb];
+        const uint32_t ctx_b = p + 1 < p_end ? ctx : 0u;  // 0: the null page
+        paged4_stage(A, p * 16, ctx, w, lane, kt, vt, T);
+        dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        paged4_load<MUT>(src, ctab, blk_a, pa, ctx, w, lane, A);
+        paged4_stage(B, (p + 1) * 16, ctx_b, w, lane, kt, vt, T);
+        dattn_page<false>(T, qop, (p + 1) * 16, ctx_b, g, n, m_l, l_l, O);
+        paged4_load<MUT>(src, ctab, blk_b, pb, ctx, w, lane, B);
+    }
+}
+
+// Configuration-3 form: workgroup (split c, sequence b) with the split plan of k_paged.
+template <int MUT>
+__global__ __launch_bounds__(256) void k_paged4(const AttnArgs a) {
+    __shared__ __align__(16) uint16_t qhl[4][2][8][128];
+    __shared__ __align__(16) uint8_t kt[16 * kRow4];
+    __shared__ __align__(16) uint8_t vt[16 * kRow4];
+    const uint32_t lane = lane_id(), w = threadIdx.x >> 6, c = blockIdx.x, b = blockIdx.y;
+    const uint32_t ctx = (uint32_t)a.context_lens[b];
+    const uint32_t pages = (ctx + 15) / 16;
+    uint32_t active, pps;
+    attn_split_plan(pages, a.splits, 0, active, pps);
+    if (c >= active) return;  // uniform over the workgroup
+    const uint32_t p_begin = c * pps, p_end = min(pages, p_begin + pps);
+    bf16x8 qop[4];
+    paged_q(a.q + ((size_t)b * a.qh + w * 8) * 128, lane, qhl[w], qop);
+    const PagedSrc src{a.pool, a.g, a.layer};
+    float m_l, l_l;
+    f32x4 O[8];
+    paged4_pages<MUT>(src, a.block_tables + (size_t)b * a.max_blocks, w, p_begin, p_end, ctx, qop, kt, vt, lane, m_l,
+                      l_l, O);
+    paged_store(a.part + (((size_t)b * a.qh + w * 8) * a.splits + c) * kPartStride, (size_t)a.splits * kPartStride,
+                lane, m_l, l_l, O);
+}
+
+// Balanced work items (the batched decode step): workgroup r serves items [run_off[r],
+// run_off[r + 1]) of the plan (one run of pages, cut at sequence boundaries); item i is pages
 // [first, end) of sequence seq (items[i] = {seq << 24 | first, end}), its partials at
 // part[(i * 32 + q head) * kPartStride].
-__global__ __launch_bounds__(64) void k_paged_items(const PagedItemsArgs a) {
-    __shared__ __align__(16) uint16_t qhl[2][8][128];
-    __shared__ __align__(16) uint8_t vt[16 * kVtRow];
-    const uint32_t lane = threadIdx.x, h = blockIdx.x, w = blockIdx.y;
-    const uint32_t i0 = a.wave_off[w], i1 = a.wave_off[w + 1];
+__global__ __launch_bounds__(256) void k_paged_items(const PagedItemsArgs a) {
+    __shared__ __align__(16) uint16_t qhl[4][2][8][128];
+    __shared__ __align__(16) uint8_t kt[16 * kRow4];
+    __shared__ __align__(16) uint8_t vt[16 * kRow4];
+    const uint32_t lane = lane_id(), w = threadIdx.x >> 6, r = blockIdx.x;
+    const uint32_t i0 = a.run_off[r], i1 = a.run_off[r + 1];
     const PagedSrc src{a.pool, a.g, a.layer};
     for (uint32_t it = i0; it < i1; ++it) {
         const uint32_t e0 = a.items[2 * it], e1 = a.items[2 * it + 1];
@@ -489,17 +604,17 @@ __global__ __launch_bounds__(64) void k_paged_items(const PagedItemsArgs a) {
         const uint32_t ctx = a.pos[s] + 1;
         __syncthreads();  // the previous item's LDS reads are done
         bf16x8 qop[4];
-        paged_q(a.q + ((size_t)s * 32 + h * 8) * 128, lane, qhl, qop);
+        paged_q(a.q + ((size_t)s * 32 + w * 8) * 128, lane, qhl[w], qop);
         float m_l, l_l;
         f32x4 O[8];
-        paged_pages<0>(src, a.tables + (size_t)s * a.max_blocks, h, p_begin, p_end, ctx, qop, vt, lane, m_l, l_l,
-                       O);
-        paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
+        paged4_pages<0>(src, a.tables + (size_t)s * a.max_blocks, w, p_begin, p_end, ctx, qop, kt, vt, lane, m_l,
+                        l_l, O);
+        paged_store(a.part + ((size_t)it * 32 + w * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
     }
 }
 
-hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t waves, hipStream_t st) {
-    OMEGA_LAUNCH(k_paged_items, dim3(4, waves), dim3(64), 0, st, a);
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t runs, hipStream_t st) {
+    OMEGA_LAUNCH(k_paged_items, dim3(runs), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -615,6 +730,12 @@ __global__ __launch_bounds__(64) void k_attn(const AttnArgs a) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const dim3 grid(a.splits, a.kvh, a.seqs);
+    if (paged_mfma(a.qh, a.kvh, a.g.block_size) && a.kvh == 4) {
+        const dim3 wgrid(a.splits, a.seqs);
+        if (a.mutant == 2) hipLaunchKernelGGL(k_paged4<2>, wgrid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(k_paged4<0>, wgrid, dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     if (paged_mfma(a.qh, a.kvh, a.g.block_size)) {
         // kv head fastest: the heads of one split are dispatched together and read the same
         // pages' 1 KiB token rows at about the same time
@@ -1442,10 +1563,10 @@ int omega_gpu_paged_attention_items_dev(const float *q_dev, const void *pool_dev
     pa.tables = block_tables_dev;
     pa.max_blocks = max_blocks_per_seq;
     pa.pos = dpos;
-    pa.wave_off = dplan->wave_off;
+    pa.run_off = dplan->run_off;
     pa.items = &dplan->items[0][0];
     pa.part = reinterpret_cast<float *>(base + plan_bytes + pos_bytes);
-    OMEGA_HIP(F_ATTN, launch_paged_items(pa, kItemWaves, cx->stream));
+    OMEGA_HIP(F_ATTN, launch_paged_items(pa, kItemRuns, cx->stream));
     CombineItemsArgs ca;
     ca.part = pa.part;
     ca.item_off = dplan->item_off;

@@ -472,10 +472,10 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         pa.tables = b->tables;
         pa.max_blocks = c.max_blocks_per_seq;
         pa.pos = b->io->pos;
-        pa.wave_off = b->io->plan.wave_off;
+        pa.run_off = b->io->plan.run_off;
         pa.items = &b->io->plan.items[0][0];
         pa.part = b->apart;
-        OMEGA_HIP(F_SESSION, launch_paged_items(pa, kItemWaves, st));
+        OMEGA_HIP(F_SESSION, launch_paged_items(pa, kItemRuns, st));
         CombineItemsArgs ca;
         ca.part = b->apart;
         ca.item_off = b->io->plan.item_off;

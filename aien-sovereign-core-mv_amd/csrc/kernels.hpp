@@ -232,16 +232,17 @@ size_t moe_work_bytes(uint32_t tokens);
 // item i is split i - item_off[s] of sequence s, pages [split * pps[s], +pps[s]) of its pos[s] + 1
 // tokens; partials at part[(i * 32 + q head) * kPartStride].
 // The attention work of a batched decode step over ragged sequences: the sequences' pages laid
-// end to end are cut into kItemWaves equal runs, one per wavefront of each kv head (4 x 512 =
-// 2048 = 256 CUs x 8, the paged kernel's occupancy of 2 per SIMD: every wavefront is resident at
-// once and they all finish together), and each run into items at sequence boundaries.
-constexpr uint32_t kItemWaves = 512;
+// end to end are cut into kItemRuns equal runs, one per workgroup of four wavefronts (one per
+// kv head; 512 x 4 = 2048 = 256 CUs x 8, the paged kernel's occupancy of 2 per SIMD: every
+// wavefront is resident at once and they all finish together), and each run into items at
+// sequence boundaries.
+constexpr uint32_t kItemRuns = 512;
 constexpr uint32_t kItemMaxSeqs = 32;
-constexpr uint32_t kItemMax = kItemWaves + kItemMaxSeqs;  // items of a step at most
+constexpr uint32_t kItemMax = kItemRuns + kItemMaxSeqs;  // items of a step at most
 struct ItemPlan {
     uint32_t item_off[kItemMaxSeqs + 1];  // items of sequence s: [item_off[s], item_off[s + 1])
     uint32_t pad[3];
-    uint32_t wave_off[kItemWaves + 4];    // items of wavefront w: [wave_off[w], wave_off[w + 1])
+    uint32_t run_off[kItemRuns + 4];      // items of run (workgroup) r: [run_off[r], run_off[r + 1])
     uint32_t items[kItemMax][2];          // {seq << 24 | first page, end page}
 };
 // first[s] .. first[s + 1]: sequence s's pages laid end to end (every sequence has >= 1 page)
@@ -255,16 +256,16 @@ struct PagedItemsArgs {
     const int32_t *tables = nullptr;     // [seqs][max_blocks]
     uint32_t max_blocks = 0;
     const uint32_t *pos = nullptr;       // [seqs]
-    const uint32_t *wave_off = nullptr;  // [waves + 1]: items of wavefront w
+    const uint32_t *run_off = nullptr;  // [runs + 1]: items of workgroup r
     const uint32_t *items = nullptr;     // [items][2]: {seq << 24 | first page, end page}
     float *part = nullptr;               // [items][32][kPartStride]
 };
-hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t waves, hipStream_t st);
+hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t runs, hipStream_t st);
 // the items' partials of every (seq, q head) combined (at most kCombineMaxItems items per
 // sequence) and split into the o projection's input terms: oq [seqs][32][4][128] e4m3,
 // os [seqs][32][4]
 constexpr uint32_t kCombineMaxItems = 768;
-static_assert(kItemWaves <= kCombineMaxItems, "a sequence may get an item from every wavefront");
+static_assert(kItemRuns <= kCombineMaxItems, "a sequence may get an item from every wavefront");
 struct CombineItemsArgs {
     const float *part = nullptr;
     const uint32_t *item_off = nullptr;  // [seqs + 1]: items of sequence s

@@ -234,3 +234,34 @@ def test_balanced_items_refusals(omega, oracle):
     out = run_items(omega, pool, q, tabs, np.array([64, 1], np.int32), 0)  # the whole table
     assert np.isfinite(out).all()
     pool.dev.free()
+
+
+@pytest.mark.parametrize("qh,kvh", [(64, 8), (16, 2), (32, 8)])
+def test_other_gqa_geometries(omega, oracle, qh, kvh):
+    # GQA group 8 with a kv head count other than four takes the one-head-per-wavefront
+    # matrix-core kernel; other groups the VALU kernel
+    rng = np.random.default_rng(50 + qh + kvh)
+    nb = 256
+    lay = oracle.kv_layout(nb, 16, 2, kvh, HD)
+    host = oracle.f32_to_bf16(rng.standard_normal(lay.pool_bytes // 2).astype(np.float32)).view(np.uint8)
+    L = _omega_layout(omega, lay)
+    dev = omega.DeviceBuffer.from_array(host)
+    lens = np.array([1, 300, 1777], np.int32)
+    maxb = (int(lens.max()) + 15) // 16
+    tabs = np.stack([rng.permutation(nb)[:maxb] for _ in lens]).astype(np.int32)
+    q = rng.standard_normal((lens.size, qh * HD)).astype(np.float32)
+    lib = omega.lib()
+    qd, td, ld = (omega.DeviceBuffer.from_array(x) for x in (q, tabs, lens))
+    od = omega.DeviceBuffer(q.nbytes)
+    rc = lib.omega_gpu_paged_attention_batch_dev(qd.ptr, dev.ptr, C.byref(L), td.ptr, ld.ptr, maxb, lens.size,
+                                                 int(lens.max()), 1, qh, kvh, HD, od.ptr)
+    assert rc == 0, omega._s(lib.omega_gpu_attention_last_error())
+    out = od.download(np.float32, q.size).reshape(lens.size, qh * HD)
+    for b, cl in enumerate(lens):
+        want = np.zeros(qh * HD, np.float32)
+        oracle.lib().oref_paged_attention(oracle.ptr(np.ascontiguousarray(q[b])), oracle.ptr(host), C.byref(lay),
+                                          oracle.ptr(tabs[b]), int(cl), 1, qh, kvh, HD, oracle.ptr(want))
+        e = rel_err(out[b], want)
+        assert e <= TOL, (qh, kvh, b, int(cl), e)
+    for x in (qd, td, ld, od, dev):
+        x.free()
