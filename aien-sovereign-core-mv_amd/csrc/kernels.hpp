@@ -219,6 +219,7 @@ struct MoeArgs {
     uint8_t *aq = nullptr;             // [T * 8][6][4][128] split terms of the SwiGLU rows
     float *as = nullptr;               // [T * 8][6][4]
     float *dp = nullptr;               // [3 k-slices][T * 8][2048] down partial sums
+    float *sink = nullptr;             // [2048]: where the GEMMs' lanes past a segment's rows store
     uint32_t nt[2] = {16, 8};          // tiles per wavefront (gate|up, down)
     int mutant = 0;  // 1: rank mask id^1; 2: weights not normalised; 5: gate/up swapped;
                      // 6: slot 7 dropped; 7: one activation term

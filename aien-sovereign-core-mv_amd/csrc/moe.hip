@@ -207,8 +207,10 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
     const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const uint32_t split = item % G::SPLITS, rest = item / G::SPLITS;
     const uint32_t grp = rest % groups, seg = rest / groups;
-    if (seg >= a.plan[0]) return;
-    const uint32_t e = a.seg_expert[seg], r0 = a.seg_start[seg], cnt = a.seg_count[seg];
+    if (seg >= *as_const_u32(a.plan)) return;
+    // wave-uniform words through scalar loads: the weight addresses stay in SGPRs
+    const uint32_t e = as_const_u32(a.seg_expert)[seg], r0 = as_const_u32(a.seg_start)[seg];
+    const uint32_t cnt = as_const_u32(a.seg_count)[seg];
     const uint32_t kb0 = split * KBW, t0 = grp * nt;
     // the expert's tiled twin: (N / 16) row tiles of KB 2 KiB blocks
     const uint8_t *wb = EPI == 0 ? a.gu_wt + (size_t)e * 2 * kMI * kMH : a.dn_wt + (size_t)e * kMH * kMI;
@@ -243,24 +245,23 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
             sbe[j][2] = e8m0_of(v.z);
             sbe[j][3] = e8m0_of(v.w);
         }
-        float *prow = part + (size_t)row * G::NOUT + 4 * g;
-#pragma unroll 1
-        for (uint32_t i = 0; i < nt; ++i) {
-            const uint32_t tile = t0 + i, tn = i + 1 < nt ? tile + 1 : tile;  // the last reloads itself
-            MoeTileA<KBW> nxt;
-            nxt.load(blk(f0(tn)), blk(f1(tn)), lane);
-            const float *ws0 = sb + (size_t)(f0(tile) >> 7) * G::KB;
-            const float *ws1 = sb + (size_t)(f1(tile) >> 7) * G::KB;
+        // lanes past the segment's rows store to the sink: every store is unconditional, so no
+        // branch joins the loop's vector-memory waits
+        float *prow = (valid ? part + (size_t)row * G::NOUT : a.sink) + 4 * g;
+        // tile i's products with the slice's terms; its weight scales come from scalar loads
+        auto tile_out = [&](const MoeTileA<KBW> &T, uint32_t tile) {
+            const cu32 *ws0 = as_const_u32(sb + (size_t)(f0(tile) >> 7) * G::KB + kb0);
+            const cu32 *ws1 = as_const_u32(sb + (size_t)(f1(tile) >> 7) * G::KB + kb0);
             f32x4 tot[2];
             tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < KBW; ++j) {
-                const float w0 = ws0[kb0 + j], w1 = ws1[kb0 + j];
+                const float w0 = __uint_as_float(ws0[j]), w1 = __uint_as_float(ws1[j]);
                 f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (uint32_t t = 0; t < kTerms; ++t) {
-                    c0 = mfma_fp8_sb(cur.A[0][j], B[j][t], c0, sbe[j][t]);
-                    c1 = mfma_fp8_sb(cur.A[1][j], B[j][t], c1, sbe[j][t]);
+                    c0 = mfma_fp8_sb(T.A[0][j], B[j][t], c0, sbe[j][t]);
+                    c1 = mfma_fp8_sb(T.A[1][j], B[j][t], c1, sbe[j][t]);
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -268,12 +269,24 @@ __global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
                     tot[1][q] = fmaf(c1[q], w1, tot[1][q]);
                 }
             }
-            if (valid) {
-                *reinterpret_cast<f32x4 *>(prow + f0(tile)) = tot[0];
-                *reinterpret_cast<f32x4 *>(prow + f1(tile)) = tot[1];
-            }
-            cur = nxt;
+            *reinterpret_cast<f32x4 *>(prow + f0(tile)) = tot[0];
+            *reinterpret_cast<f32x4 *>(prow + f1(tile)) = tot[1];
+        };
+        // Two tile sets take turns (nt is even): while one tile's products run, the other set's
+        // tile is in flight, and a set is reloaded as soon as its tile is consumed. The loop body
+        // is one straight path with every load unconditional, so waiting for one set never waits
+        // for the other; the last two tiles are peeled off so no load reaches past the run.
+        MoeTileA<KBW> nx;
+        nx.load(blk(f0(t0 + 1)), blk(f1(t0 + 1)), lane);
+#pragma unroll 1
+        for (uint32_t i = 0; i + 2 < nt; i += 2) {
+            tile_out(cur, t0 + i);
+            cur.load(blk(f0(t0 + i + 2)), blk(f1(t0 + i + 2)), lane);
+            tile_out(nx, t0 + i + 1);
+            nx.load(blk(f0(t0 + i + 3)), blk(f1(t0 + i + 3)), lane);
         }
+        tile_out(cur, t0 + nt - 2);
+        tile_out(nx, t0 + nt - 1);
     }
 }
 
@@ -383,6 +396,7 @@ size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens) {
     a.aq = take(P * (kMI / 128) * kTerms * 128);
     a.as = reinterpret_cast<float *>(take(P * (kMI / 128) * 16));
     a.dp = reinterpret_cast<float *>(take(MoeGemm<1>::SPLITS * P * MoeGemm<1>::NOUT * 4));
+    a.sink = reinterpret_cast<float *>(take(kMH * 4));
     // tiles per wavefront: long runs once there are segments enough to fill the chip
     a.nt[0] = tokens >= 8 ? 16 : 2;
     a.nt[1] = tokens >= 8 ? 8 : 2;
