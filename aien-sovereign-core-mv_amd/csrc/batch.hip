@@ -111,9 +111,12 @@ __global__ __launch_bounds__(256) void k_bd_rows(const BdArgs a) {
 }
 
 // ------------------------------------------------------------------ dense FP8 GEMM (the batch's rows)
-// A wavefront = (run of nt 32-row tiles, k-slice of 2 blocks), all T <= 16 MT rows: the slice's
-// activation terms of every row held in registers, the tiles' weights streamed from the tiled
-// twin (the next tile's in flight), partial sums stored per k-slice.
+// A wavefront = (32-row tile, k-slice of 2 blocks), all T <= 16 MT rows: the tile's weights
+// (8 KiB from the tiled twin, 1 KiB contiguous per load instruction) and the slice's activation
+// terms of every row go out together, one round trip, then the products and the partial sums
+// of the k-slice. One tile per wavefront puts the whole weight stream in flight at once (q|k|v:
+// 160 tiles x 8 slices = 1280 wavefronts). Scales come through scalar loads and every store is
+// unconditional (rows past T write the sink), so no wait merges over a branch.
 struct DenseArgs {
     const uint8_t *wt = nullptr;  // tiled twin of a [1][n][k] FP8 tensor
     const float *s = nullptr;     // [n/128][k/128]
@@ -122,18 +125,20 @@ struct DenseArgs {
     const float *xs = nullptr;    // [T][k/128][4]
     uint32_t T = 0;
     float *part = nullptr;        // [k/256][T][n]
-    uint32_t nt = 2;
+    float *sink = nullptr;        // [64]: where the lanes of rows past T store
 };
 
 template <int MT>
 __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
     constexpr int KBW = 2;
     const uint32_t lane = lane_id(), g = lane >> 4, n = lane & 15;
-    const uint32_t KB = a.k / 128, splits = KB / KBW, tiles = a.n / 32, groups = (tiles + a.nt - 1) / a.nt;
+    const uint32_t KB = a.k / 128, splits = KB / KBW, tiles = a.n / 32;
     const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    const uint32_t split = item % splits, grp = item / splits;
-    if (grp >= groups) return;
-    const uint32_t kb0 = split * KBW, t0 = grp * a.nt, t1 = min(tiles, t0 + a.nt);
+    const uint32_t split = item % splits, tile = item / splits;
+    if (tile >= tiles) return;
+    const uint32_t kb0 = split * KBW;
+    MoeTileA<KBW> A;
+    A.load(a.wt + ((size_t)(2 * tile) * KB + kb0) * 2048, a.wt + ((size_t)(2 * tile + 1) * KB + kb0) * 2048, lane);
     i32x8 B[MT][KBW][kTerms];
     int sbe[MT][KBW][kTerms];
 #pragma unroll
@@ -152,49 +157,36 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
             sbe[m][j][3] = e8m0_of(v.w);
         }
     }
-    auto blk = [&](uint32_t f) { return a.wt + ((size_t)(f >> 4) * KB + kb0) * 2048; };
-    MoeTileA<KBW> cur;
-    cur.load(blk(32 * t0), blk(32 * t0 + 16), lane);
+    const cu32 *ws = as_const_u32(a.s + (size_t)((32 * tile) >> 7) * KB + kb0);
     float *part = a.part + (size_t)split * a.T * a.n;
-#pragma unroll 1
-    for (uint32_t tile = t0; tile < t1; ++tile) {
-        const uint32_t tn = tile + 1 < t1 ? tile + 1 : tile;  // the last tile reloads itself
-        MoeTileA<KBW> nxt;
-        nxt.load(blk(32 * tn), blk(32 * tn + 16), lane);
-        const float *ws = a.s + (size_t)((32 * tile) >> 7) * KB + kb0;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            f32x4 tot[2];
-            tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MT; ++m) {
+        f32x4 tot[2];
+        tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < KBW; ++j) {
-                const float w = ws[j];
-                f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < KBW; ++j) {
+            const float w = __uint_as_float(ws[j]);
+            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (uint32_t t = 0; t < kTerms; ++t) {
-                    c0 = mfma_fp8_sb(cur.A[0][j], B[m][j][t], c0, sbe[m][j][t]);
-                    c1 = mfma_fp8_sb(cur.A[1][j], B[m][j][t], c1, sbe[m][j][t]);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    tot[0][q] = fmaf(c0[q], w, tot[0][q]);
-                    tot[1][q] = fmaf(c1[q], w, tot[1][q]);
-                }
+            for (uint32_t t = 0; t < kTerms; ++t) {
+                c0 = mfma_fp8_sb(A.A[0][j], B[m][j][t], c0, sbe[m][j][t]);
+                c1 = mfma_fp8_sb(A.A[1][j], B[m][j][t], c1, sbe[m][j][t]);
             }
-            const uint32_t tok = 16 * m + n;
-            if (tok < a.T) {
-                float *y = part + (size_t)tok * a.n + 32 * tile + 4 * g;
-                *reinterpret_cast<f32x4 *>(y) = tot[0];
-                *reinterpret_cast<f32x4 *>(y + 16) = tot[1];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                tot[0][q] = fmaf(c0[q], w, tot[0][q]);
+                tot[1][q] = fmaf(c1[q], w, tot[1][q]);
             }
         }
-        cur = nxt;
+        const uint32_t tok = 16 * m + n;
+        float *y = (tok < a.T ? part + (size_t)tok * a.n + 32 * tile : a.sink) + 4 * g;
+        *reinterpret_cast<f32x4 *>(y) = tot[0];
+        *reinterpret_cast<f32x4 *>(y + 16) = tot[1];
     }
 }
 
 hipError_t launch_dense_gemm(const DenseArgs &a, hipStream_t st) {
-    const uint32_t splits = a.k / 256, tiles = a.n / 32, groups = (tiles + a.nt - 1) / a.nt;
-    const uint32_t waves = groups * splits;
+    const uint32_t waves = (a.k / 256) * (a.n / 32);
     if (a.T <= 16) OMEGA_LAUNCH(k_dense_gemm<1>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
     else OMEGA_LAUNCH(k_dense_gemm<2>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
@@ -406,6 +398,7 @@ struct OmegaGpuBatchDecode {
     float *rope_cos = nullptr, *rope_sin = nullptr;
     // workspace
     float *x = nullptr, *qkv_part = nullptr, *q = nullptr, *apart = nullptr, *o_part = nullptr;
+    float *sink = nullptr;  // the dense GEMMs' stores of rows past the batch
     float *hidden = nullptr, *logits = nullptr;
     uint8_t *xq = nullptr, *oq = nullptr;
     float *xs = nullptr, *os = nullptr;
@@ -462,6 +455,7 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         dq.xs = b->xs;
         dq.T = T;
         dq.part = b->qkv_part;
+        dq.sink = b->sink;
         OMEGA_HIP(F_SESSION, launch_dense_gemm(dq, st));
         OMEGA_LAUNCH(k_bd_qkv, dim3(T, 4), dim3(64), 0, st, a);
         PagedItemsArgs pa;
@@ -491,6 +485,7 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         dO.xs = b->os;
         dO.T = T;
         dO.part = b->o_part;
+        dO.sink = b->sink;
         OMEGA_HIP(F_SESSION, launch_dense_gemm(dO, st));
         MoeArgs m;
         moe_work_carve(m, b->moe, T);
@@ -599,6 +594,7 @@ int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpu
     M((void **)&b->oq, (size_t)T * 32 * kTerms * 128);
     M((void **)&b->os, (size_t)T * 32 * 16);
     M((void **)&b->o_part, (size_t)(kBdAttn / 256) * T * kBdH * 4);
+    M((void **)&b->sink, 256);
     M((void **)&b->hidden, (size_t)T * kBdH * 4);
     M((void **)&b->hid_hi, (size_t)T * kBdH * 2);
     M((void **)&b->hid_lo, (size_t)T * kBdH * 2);
@@ -640,7 +636,7 @@ void omega_gpu_batch_decode_free(OmegaGpuBatchDecode *b) {
     if (c) (void)hipStreamSynchronize(c->stream);
     for (auto &kv : b->exec) (void)hipGraphExecDestroy(kv.second);
     for (hipGraph_t gr : b->graphs) (void)hipGraphDestroy(gr);
-    void *ps[] = {b->x, b->xq, b->xs, b->qkv_part, b->q, b->apart, b->oq, b->os, b->o_part, b->hidden,
+    void *ps[] = {b->x, b->xq, b->xs, b->qkv_part, b->q, b->apart, b->oq, b->os, b->o_part, b->sink, b->hidden,
                   b->hid_hi, b->hid_lo, b->logits, b->tables, b->moe, b->route_ids, b->route_w, b->io,
                   b->final_norm, b->rope_cos, b->rope_sin};
     for (void *p : ps)
