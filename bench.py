@@ -18,6 +18,10 @@ The JSON line also carries:
   cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
             host cores: a bounded sample of 4 of the 48 layers x 128 tokens plus 4 full-vocab
             lm_heads (about 10 s of CPU work), scaled to the 48-layer step.
+  bs32:     the metric's batch-32 figure, measured after the bs=1 model is freed: configuration
+            5's batched step (32 sequences, contexts log-uniform in [1k, 128k], one hipGraph per
+            step) for --bs32-steps steps; --no-bs32 skips it. --workload serve prints the full
+            line for that configuration.
 """
 import argparse
 import json
@@ -473,7 +477,7 @@ def serve_cpu_baseline(threads, mean_ctx):
                       f"the 32 sequences served one after another"}
 
 
-def bench_serve(om, args):
+def bench_serve(om, args, emit=True):
     """Configuration 5: 32 concurrent sequences of the random-init 48-layer model, contexts
     log-uniform in [1k, 128k] already resident as bf16 KV (N(0,1)) in 16-token pages of the pool
     (pages of every sequence a random permutation of the pool), `serve_steps` greedy steps of all
@@ -540,7 +544,7 @@ def bench_serve(om, args):
     tok_s = SERVE_SEQS * steps / elapsed
     gbs = step_bytes / (ms * 1e6)
     cpu = None if args.no_cpu else serve_cpu_baseline(args.cpu_threads, int(ctx_mid.mean()))
-    print(json.dumps({
+    line = {
         "metric": "Qwen3-30B-A3B FP8 batched serving decode (configuration 5): 32 sequences, tok/s",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -556,9 +560,18 @@ def bench_serve(om, args):
                           "distinct_experts_mean": round(float(np.mean(distinct)), 1),
                           "kv_bytes_per_step": int(ctx_mid.sum() * KV_BYTES_PER_TOKEN)},
         "cpu_baseline": cpu,
-        "extra": {"build_s": round(t_build, 1), "last_tokens_head": tok[:4].tolist()}}), flush=True)
+        "extra": {"build_s": round(t_build, 1), "last_tokens_head": tok[:4].tolist()}}
+    if emit:
+        print(json.dumps(line), flush=True)
     bd.free()
     pool.free()
+    for ts in layers:
+        for t in ts:
+            t.free()
+    router.free()
+    lm.free()
+    embed.free()
+    return line
 
 
 def main():
@@ -583,6 +596,9 @@ def main():
     ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--gemv-reps", type=int, default=200)
+    ap.add_argument("--no-bs32", action="store_true",
+                    help="decode workload: skip the 32-sequence batched figure (configuration 5)")
+    ap.add_argument("--bs32-steps", type=int, default=64)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES (byte-counter calibration)")
     args = ap.parse_args()
@@ -718,6 +734,24 @@ def main():
                   "prompt_s": round(t_prompt, 2),
                   "generated_head": generated[:8]},
     }
+    if not args.no_bs32:
+        # the metric's bs32 figure: configuration 5's batched step over the same architecture
+        # (its own model build; the bs=1 model is freed first)
+        g.free()
+        for ts in model["layers"]:
+            for t in ts:
+                t.free()
+        for k in ("router", "cache", "lm", "embed"):
+            model[k].free()
+        sargs = argparse.Namespace(serve_steps=args.bs32_steps, serve_warmup=4, no_cpu=True, eager=False,
+                                   cpu_threads=args.cpu_threads)
+        sl = bench_serve(om, sargs, emit=False)
+        line["bs32"] = {"metric": sl["metric"], "value": sl["value"], "unit": "tok/s",
+                        "ms_per_step": sl["ms_per_step"], "steps": sl["steps"],
+                        "context_mean": sl["config"]["context_mean"],
+                        "step_roofline_frac": sl["step_roofline"]["frac"],
+                        "achieved_GBs": sl["step_roofline"]["achieved_GBs"],
+                        "workload": sl["config"]["workload"]}
     print(json.dumps(line))
 
 
