@@ -613,6 +613,99 @@ __global__ __launch_bounds__(256) void k_paged_items(const PagedItemsArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- prefill over the fused cache
+// m consecutive tokens at positions pos0 .. pos0 + m - 1 (positions before pos0 already cached):
+// token t's attention is the decode step's at position pos0 + t (per-head q / k RMSNorm, RoPE,
+// its K / V appended, softmax over positions 0 ..= pos0 + t). Three launches: the preparation of
+// every token (q normed and rotated into a scratch row, K and V appended to the cache), the pages
+// of every (token, chunk of kPattnChunk pages, kv head) as one wavefront, and the items combine.
+constexpr uint32_t kPattnChunk = 32;
+
+struct PattnArgs {
+    const float *qkv = nullptr;  // [m][5120] raw projection rows
+    uint8_t *pool = nullptr;
+    KvGeom g{};
+    uint32_t layer = 0, pos0 = 0, m = 0;
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    float eps = 1e-6f;
+    float *qn = nullptr;               // [m][32][128] prepared q
+    const uint32_t *items = nullptr;   // [items][2]: token, chunk
+    float *part = nullptr;             // [items][32][kPartStride]
+};
+
+// grid (4 kv heads, m): the kv head's 8 q heads and its K / V row of token t
+__global__ __launch_bounds__(64) void k_pattn_prep(const PattnArgs a) {
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y, pos = a.pos0 + t;
+    const float *row = a.qkv + (size_t)t * 5120;
+    float q0[8], q1[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        q0[r] = *as_global_f32(row + (h * 8 + r) * 128 + lane);
+        q1[r] = *as_global_f32(row + (h * 8 + r) * 128 + 64 + lane);
+    }
+    const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
+    const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
+    const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
+    float k0 = *as_global_f32(row + 4096 + h * 128 + lane), k1 = *as_global_f32(row + 4096 + h * 128 + 64 + lane);
+    const float v0 = *as_global_f32(row + 4608 + h * 128 + lane);
+    const float v1 = *as_global_f32(row + 4608 + h * 128 + 64 + lane);
+    const float kw0 = *as_global_f32(a.k_norm + lane), kw1 = *as_global_f32(a.k_norm + 64 + lane);
+    double ss[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ss[r] = (double)q0[r] * (double)q0[r] + (double)q1[r] * (double)q1[r];
+    const float scale_l = rms_scale(head_sums8(ss, lane), 128, a.eps);
+    float *qo = a.qn + ((size_t)t * 32 + h * 8) * 128;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        head_scale_rope(q0[r], q1[r], readlane_f32(scale_l, 8 * r), qw0, qw1, rc, rs, true);
+        qo[r * 128 + lane] = q0[r];
+        qo[r * 128 + 64 + lane] = q1[r];
+    }
+    const float kscale = rms_scale(wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1), 128, a.eps);
+    head_scale_rope(k0, k1, kscale, kw0, kw1, rc, rs, true);
+    uint16_t *krow = reinterpret_cast<uint16_t *>(a.pool + kv_row_offset(a.g, pos >> 4, a.layer, 0, pos & 15, h));
+    krow[lane] = bf16_rne(k0);
+    krow[lane + 64] = bf16_rne(k1);
+    uint8_t *vplane = a.pool + (uint64_t)(pos >> 4) * a.g.block_stride + (uint64_t)a.layer * a.g.layer_stride +
+                      a.g.plane_stride + (uint64_t)h * kVtHead + (pos & 15) * 2;
+    *reinterpret_cast<uint16_t *>(vplane + lane * 32) = bf16_rne(v0);
+    *reinterpret_cast<uint16_t *>(vplane + (lane + 64) * 32) = bf16_rne(v1);
+}
+
+// one wavefront per (item, kv head): item = (token t, chunk c), pages [c C, min(pages, (c + 1) C))
+// of positions 0 ..= pos0 + t; the two-set straight-path page loop of paged_pages over the fused
+// cache's pages (K rows token-major, V transposed per page: no staging)
+__global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
+    __shared__ __align__(16) uint16_t qhl[2][8][128];
+    const uint32_t lane = threadIdx.x, h = blockIdx.x & 3, it = blockIdx.x >> 2;
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t t = a.items[2 * it], c = a.items[2 * it + 1];
+    const uint32_t ctx = a.pos0 + t + 1, pages = (ctx + 15) / 16;
+    const uint32_t p_begin = c * kPattnChunk, p_end = min(pages, p_begin + kPattnChunk), last = p_end - 1;
+    bf16x8 qop[4];
+    paged_q(a.qn + ((size_t)t * 32 + h * 8) * 128, lane, qhl, qop);
+    DattnArgs d;
+    d.pool = a.pool;
+    d.g = a.g;
+    d.layer = a.layer;
+    DattnPage A, B;
+    dattn_load(d, h, p_begin, lane, A);
+    dattn_load(d, h, min(p_begin + 1, last), lane, B);
+    float m_l = -INFINITY, l_l = 0.f;
+    f32x4 O[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t p = p_begin; p < p_end; p += 2) {
+        const uint32_t ctx_b = p + 1 < p_end ? ctx : 0u;  // 0: the null page (every score -inf)
+        dattn_page<false>(A, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        dattn_load(d, h, min(p + 2, last), lane, A);
+        dattn_page<false>(B, qop, (p + 1) * 16, ctx_b, g, n, m_l, l_l, O);
+        dattn_load(d, h, min(p + 3, last), lane, B);
+    }
+    paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
+}
+
 hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t runs, hipStream_t st) {
     OMEGA_LAUNCH(k_paged_items, dim3(runs), dim3(256), 0, st, a);
     return hipGetLastError();
@@ -885,7 +978,8 @@ __global__ __launch_bounds__(256) void k_attn_combine_items(const CombineItemsAr
             sum.z += v.z;
             sum.w += v.w;
         }
-        const f32x4 r = {sum.x / L, sum.y / L, sum.z / L, sum.w / L};
+        const f32x4 r = {sum.x / L * a.out_scale, sum.y / L * a.out_scale, sum.z / L * a.out_scale,
+                         sum.w / L * a.out_scale};
         if (a.out) *reinterpret_cast<f32x4 *>(a.out + ((size_t)s * 32 + head) * 128 + 4 * t) = r;
         orow[4 * t + 0] = r.x;
         orow[4 * t + 1] = r.y;
@@ -1191,6 +1285,164 @@ int omega_gpu_decode_attn_cache_read(OmegaGpuDecodeAttnCache *c, uint32_t layer,
 }
 
 const char *omega_gpu_decode_attn_last_error(void) { return last_error(F_DATTN); }
+// The prefill attention of m tokens on the fused cache (both entries): qkv_dev [m][5120] and
+// out_dev [m][4096] device rows. Sub-batches of at most 1024 tokens bound the scratch; each runs
+// the preparation (K / V of its tokens appended), the page items and their combine.
+static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m,
+                            const float *qkv_dev, float eps, float out_scale, float *out_dev,
+                            OmegaGpuPrefillAttnInfo *info, const uint64_t t_call) {
+    Ctx *cx = ctx(F_DATTN);
+    if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    constexpr uint32_t kSub = 1024;
+    const uint32_t max_chunks = (c->max_pos / 16 + kPattnChunk - 1) / kPattnChunk;
+    const size_t qn_bytes = (size_t)kSub * 32 * 128 * 4, max_items = (size_t)kSub * max_chunks;
+    const size_t item_bytes = (max_items * 8 + 255) / 256 * 256, off_bytes = ((kSub + 1) * 4 + 255) / 256 * 256;
+    if (!ensure_scratch(F_DATTN, cx, qn_bytes + item_bytes + off_bytes + max_items * 32 * kPartStride * 4))
+        return OMEGA_GPU_CHIP_FAIL;
+    uint8_t *base = static_cast<uint8_t *>(cx->scratch);
+    PattnArgs a;
+    a.pool = c->pool;
+    a.g = c->g;
+    a.layer = layer;
+    a.q_norm = c->q_norm + (size_t)layer * 128;
+    a.k_norm = c->k_norm + (size_t)layer * 128;
+    a.rope_cos = c->rope_cos;
+    a.rope_sin = c->rope_sin;
+    a.eps = eps;
+    a.qn = reinterpret_cast<float *>(base);
+    uint32_t *ditems = reinterpret_cast<uint32_t *>(base + qn_bytes);
+    uint32_t *doff = reinterpret_cast<uint32_t *>(base + qn_bytes + item_bytes);
+    a.items = ditems;
+    a.part = reinterpret_cast<float *>(base + qn_bytes + item_bytes + off_bytes);
+    std::vector<uint32_t> items, off;
+    uint32_t total_items = 0, widest = 0;
+    OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev0, cx->stream));
+    for (uint32_t t0 = 0; t0 < m; t0 += kSub) {
+        const uint32_t mm = std::min(kSub, m - t0);
+        items.clear();
+        off.assign(mm + 1, 0);
+        for (uint32_t t = 0; t < mm; ++t) {
+            const uint32_t pages = (pos0 + t0 + t + 1 + 15) / 16, chunks = (pages + kPattnChunk - 1) / kPattnChunk;
+            off[t] = (uint32_t)(items.size() / 2);
+            for (uint32_t ch = 0; ch < chunks; ++ch) {
+                items.push_back(t);
+                items.push_back(ch);
+            }
+            widest = std::max(widest, chunks);
+        }
+        const uint32_t n = (uint32_t)(items.size() / 2);
+        off[mm] = n;
+        total_items += n;
+        OMEGA_HIP(F_DATTN, hipMemcpyAsync(ditems, items.data(), items.size() * 4, hipMemcpyHostToDevice, cx->stream));
+        OMEGA_HIP(F_DATTN, hipMemcpyAsync(doff, off.data(), off.size() * 4, hipMemcpyHostToDevice, cx->stream));
+        a.qkv = qkv_dev + (size_t)t0 * 5120;
+        a.pos0 = pos0 + t0;
+        a.m = mm;
+        OMEGA_LAUNCH(k_pattn_prep, dim3(4, mm), dim3(64), 0, cx->stream, a);
+        OMEGA_HIP(F_DATTN, hipGetLastError());
+        OMEGA_LAUNCH(k_pattn, dim3(4 * n), dim3(64), 0, cx->stream, a);
+        OMEGA_HIP(F_DATTN, hipGetLastError());
+        CombineItemsArgs cb;
+        cb.part = a.part;
+        cb.item_off = doff;
+        cb.out = out_dev + (size_t)t0 * 4096;
+        cb.out_scale = out_scale;
+        OMEGA_HIP(F_DATTN, launch_attn_combine_items(cb, mm, cx->stream));
+        // the host plan is read by the copies above before the next sub-batch rewrites it
+        OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
+    }
+    OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev1, cx->stream));
+    OMEGA_HIP(F_DATTN, hipEventSynchronize(cx->ev1));
+    if (info) {
+        float ms = 0.f;
+        OMEGA_HIP(F_DATTN, hipEventElapsedTime(&ms, cx->ev0, cx->ev1));
+        memset(info, 0, sizeof(*info));
+        info->layer = layer;
+        info->pos0 = pos0;
+        info->m = m;
+        info->chunks = total_items;
+        info->grid_x = 4 * total_items;
+        info->grid_y = 1;
+        info->threads = 64;
+        info->splits = widest;
+        info->per_split = kPattnChunk * 16;
+        info->elapsed_ns = (uint64_t)((double)ms * 1e6);
+        info->call_ns = now_ns() - t_call;
+        info->kernel_cache_hit = 1;
+    }
+    return OMEGA_GPU_OK;
+}
+
+static int prefill_attn_check(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m) {
+    if (!c) {
+        set_error(F_DATTN, "prefill attn: NULL cache");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    if (m == 0 || layer >= c->layers || (uint64_t)pos0 + m > c->max_pos) {
+        set_error(F_DATTN, "prefill attn layer %u pos0 %u m %u refused: m >= 1, layer < %u, pos0 + m <= %u", layer,
+                  pos0, m, c->layers, c->max_pos);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    return OMEGA_GPU_OK;
+}
+
+int omega_gpu_prefill_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m, const float *qkv,
+                           float eps, float out_scale, float *out, OmegaGpuPrefillAttnInfo *info) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    const uint64_t t0 = now_ns();
+    clear_error(F_DATTN);
+    if (!qkv || !out) {
+        set_error(F_DATTN, "prefill attn: NULL q|k|v or out");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    int rc = prefill_attn_check(c, layer, pos0, m);
+    if (rc) return rc;
+    Ctx *cx = ctx(F_DATTN);
+    if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    const size_t qb = (size_t)m * 5120 * 4, ob = (size_t)m * 4096 * 4;
+    void *d = nullptr;
+    OMEGA_HIP(F_DATTN, hipMalloc(&d, qb + ob));
+    if (!ensure_pinned(F_DATTN, cx, std::max(qb, ob))) {
+        (void)hipFree(d);
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    memcpy(cx->pin, qkv, qb);
+    hipError_t e = hipMemcpyAsync(d, cx->pin, qb, hipMemcpyHostToDevice, cx->stream);
+    if (e == hipSuccess) {
+        float *od = reinterpret_cast<float *>(static_cast<uint8_t *>(d) + qb);
+        rc = prefill_attn_run(c, layer, pos0, m, static_cast<const float *>(d), eps, out_scale, od, info, t0);
+        if (!rc) {
+            e = hipMemcpyAsync(cx->pin, od, ob, hipMemcpyDeviceToHost, cx->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(cx->stream);
+            if (e == hipSuccess) memcpy(out, cx->pin, ob);
+        }
+    }
+    (void)hipStreamSynchronize(cx->stream);
+    (void)hipFree(d);
+    if (e != hipSuccess) {
+        set_error(F_DATTN, "prefill attn: %s", hipGetErrorString(e));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    if (info) info->call_ns = now_ns() - t0;
+    return rc;
+}
+
+int omega_gpu_prefill_attn_dev(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m,
+                               uint64_t qkv_va, float eps, float out_scale, uint64_t out_va,
+                               OmegaGpuPrefillAttnInfo *info) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    const uint64_t t0 = now_ns();
+    clear_error(F_DATTN);
+    if (!qkv_va || !out_va || qkv_va % 16 || out_va % 16) {
+        set_error(F_DATTN, "prefill attn dev: addresses must be non-zero and 16-byte aligned");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    int rc = prefill_attn_check(c, layer, pos0, m);
+    if (rc) return rc;
+    return prefill_attn_run(c, layer, pos0, m, reinterpret_cast<const float *>(qkv_va), eps, out_scale,
+                            reinterpret_cast<float *>(out_va), info, t0);
+}
+
 const char *omega_gpu_decode_attn_rc_name(int rc) { return rc_name(rc); }
 void omega_gpu_decode_attn_set_depth(uint32_t depth) { knobs().dattn_depth = depth; }
 void omega_gpu_decode_attn_set_per_split(uint32_t per_split) {

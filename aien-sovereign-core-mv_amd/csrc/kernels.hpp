@@ -273,6 +273,7 @@ struct CombineItemsArgs {
     uint8_t *oq = nullptr;
     float *os = nullptr;
     float *out = nullptr;                // when set: the f32 rows [seqs][32][128] instead of the split
+    float out_scale = 1.0f;              // the f32 rows' factor
 };
 hipError_t launch_attn_combine_items(const CombineItemsArgs &a, uint32_t seqs, hipStream_t st);
 

@@ -221,6 +221,24 @@ SIGNATURES = {
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
     "omega_gpu_paged_attention_items_dev": (i32, [P, P, C.POINTER(KvLayout), P, u32, P, u32, u32, P]),
+    # whole-prompt prefill (crates/aien-omega-pf/src/lib.rs:384-456, :542-571)
+    "omega_gpu_pf_rc_name": (cstr, [i32]),
+    "omega_gpu_pf_alloc_dev": (i32, [C.c_size_t, P]),
+    "omega_gpu_pf_alloc_host": (i32, [C.c_size_t, P]),
+    "omega_gpu_pf_free": (None, [P]),
+    "omega_gpu_pf_copy_va": (i32, [u64, u64, C.c_size_t]),
+    "omega_gpu_pf_stats": (None, [P, P]),
+    "omega_gpu_pf_stats_reset": (None, []),
+    "omega_gpu_pf_quant": (i32, [u32, u32, u32, u64, u64, u64, P]),
+    "omega_gpu_pf_qgemm_bm": (u32, []),
+    "omega_gpu_pf_qgemm_tiles_va": (u32, [u32, P, P, P, P, u32]),
+    "omega_gpu_pf_qgemm": (i32, [u32, u32, u32, u64, u32, u64, u64, u64, u64, P]),
+    "omega_gpu_pf_router_rows": (u32, []),
+    "omega_gpu_pf_router_pack": (None, [u32, u32, P, P]),
+    "omega_gpu_pf_router_logits": (i32, [u32, u32, u32, u64, u64, u64, P]),
+    "omega_gpu_pf_moe_combine": (i32, [u32, u32, u32, u64, u64, u64, u64, P]),
+    "omega_gpu_prefill_attn": (i32, [P, u32, u32, u32, P, f32, f32, P, P]),
+    "omega_gpu_prefill_attn_dev": (i32, [P, u32, u32, u32, u64, f32, f32, u64, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),

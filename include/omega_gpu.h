@@ -468,6 +468,77 @@ int omega_gpu_paged_attention_batch_bf16(const float *q, const void *pool,
 const char *omega_gpu_attention_rc_name(int rc);                              /* ffi.rs:463 */
 const char *omega_gpu_attention_last_error(void);                             /* ffi.rs:464 */
 
+/* ================================================================== whole-prompt prefill
+ * crates/aien-omega-pf/src/lib.rs:384-456 (the quantiser, the grouped W8A8 GEMM over a tile
+ * table, the session buffers, the router logits and the MoE combine of the whole-prompt driver
+ * qwen3_moe_omega_prefill.rs) and :542-571 (the prefill attention on the fused decode cache).
+ * Every call is synchronous and returns the chip nanoseconds of its launches in *ns (NULL
+ * allowed). Errors: omega_gpu_pf_rc_name + omega_gpu_session_last_error; the attention reports
+ * through the decode attention family (omega_gpu_decode_attn_rc_name / _last_error). */
+#define OMEGA_GPU_PF_PLAIN 0       /* y f32 rows of n */
+#define OMEGA_GPU_PF_SWIGLU_NAT 2  /* tensor [E][2I][k] gate rows then up rows; y bf16 act rows of n / 2 */
+#define OMEGA_QG_IN_F32 0
+#define OMEGA_QG_IN_BF16 1
+#define OMEGA_QG_TILE_BYTES 32
+/* lib.rs:337-347: a session buffer (kind 0 device, 1 host-visible; cpu is the host view) */
+typedef struct OmegaGpuMem {
+    uint32_t handle_index, handle_generation, kind;
+    void *cpu;
+    uint64_t va, size;
+} OmegaGpuMem;
+/* lib.rs:83-93: one tile of the grouped GEMM: up to qgemm_bm() rows of one expert */
+typedef struct OmegaGpuPfTile {
+    uint64_t w_va, s_va;
+    uint32_t row0, cnt;
+    uint64_t pad;
+} OmegaGpuPfTile;
+/* lib.rs:362-376 */
+typedef struct OmegaGpuPrefillAttnInfo {
+    uint32_t layer, pos0, m, chunks, grid_x, grid_y, threads, splits, per_split;
+    uint64_t elapsed_ns, call_ns;
+    int32_t kernel_cache_hit;
+} OmegaGpuPrefillAttnInfo;
+const char *omega_gpu_pf_rc_name(int rc);                                              /* :385 */
+int omega_gpu_pf_alloc_dev(size_t bytes, OmegaGpuMem *out);                            /* :387 */
+int omega_gpu_pf_alloc_host(size_t bytes, OmegaGpuMem *out);                           /* :388 */
+void omega_gpu_pf_free(OmegaGpuMem *m);                                                /* :389 */
+int omega_gpu_pf_copy_va(uint64_t dst_va, uint64_t src_va, size_t bytes);             /* :390 */
+void omega_gpu_pf_stats(uint64_t *chip_ns, uint64_t *launches);                        /* :391 */
+void omega_gpu_pf_stats_reset(void);                                                   /* :392 */
+/* :393-401: rows x k values (f32 or bf16) -> e4m3 codes [rows][k] and power-of-two block scales
+ * f32 [rows][k / 128], the fake_quant rule (qwen3_moe_omega_prefill/fake_quant.rs:31-104) */
+int omega_gpu_pf_quant(uint32_t k, uint32_t in_type, uint32_t rows, uint64_t x_va, uint64_t q_va, uint64_t s_va,
+                       uint64_t *ns);
+uint32_t omega_gpu_pf_qgemm_bm(void);                                                  /* :402 */
+/* :403-410: the tile table of rows grouped by expert (lib.rs:122-160); returns the tile count,
+ * 0 when it would exceed max */
+uint32_t omega_gpu_pf_qgemm_tiles_va(uint32_t experts, const uint64_t *w_va, const uint64_t *s_va,
+                                     const uint32_t *counts, void *tab, uint32_t max);
+/* :411-424: for every tile, output rows row0 .. row0 + cnt of W_expert x dequant(activation row
+ * rowidx[row] (or row when rowidx_va is 0)); the kernel reads activation rows (and row indices)
+ * up to row0 + bm - 1 of every tile */
+int omega_gpu_pf_qgemm(uint32_t n, uint32_t k, uint32_t layout, uint64_t tiles_va, uint32_t ntiles,
+                       uint64_t rowidx_va, uint64_t xq_va, uint64_t xs_va, uint64_t y_va, uint64_t *ns);
+uint32_t omega_gpu_pf_router_rows(void);                                               /* :430 */
+void omega_gpu_pf_router_pack(uint32_t e, uint32_t k, const float *w, float *wq);      /* :431 */
+/* :432-440: logits [rows][e] = the sequential f32 sum from -0.0 of w[ex][j] x[r][j] over the
+ * packed weights (router_logits_ref, lib.rs:505-517); reads and writes whole tiles of
+ * router_rows() rows */
+int omega_gpu_pf_router_logits(uint32_t k, uint32_t e, uint32_t rows, uint64_t x_va, uint64_t wq_va,
+                               uint64_t logits_va, uint64_t *ns);
+/* :441-450: out[r] = sum over slots from +0.0 of wt[r][slot] * down[inv[r][slot]]
+ * (moe_combine_ref, lib.rs:519-539) */
+int omega_gpu_pf_moe_combine(uint32_t h, uint32_t top_k, uint32_t rows, uint64_t down_va, uint64_t inv_va,
+                             uint64_t wt_va, uint64_t out_va, uint64_t *ns);
+/* :543-553: layer `layer` of the m tokens at pos0 .. pos0 + m - 1 (0 .. pos0 - 1 already cached):
+ * qkv f32 [m][5120] raw projection rows; appends their K / V; out f32 [m][4096] x out_scale */
+int omega_gpu_prefill_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m, const float *qkv,
+                           float eps, float out_scale, float *out, OmegaGpuPrefillAttnInfo *info);
+/* :559-571: the same on device rows (16-byte aligned) */
+int omega_gpu_prefill_attn_dev(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m,
+                               uint64_t qkv_va, float eps, float out_scale, uint64_t out_va,
+                               OmegaGpuPrefillAttnInfo *info);
+
 /* ================================================================== device-resident extensions
  * Not in the reference ABI: entry points for callers whose inputs already live in HBM (the
  * benchmark and the parity tests at full size). Same kernels as the entries above. */
@@ -592,6 +663,12 @@ int omega_gpu_sync(void);
 #endif
 
 #ifdef __cplusplus
+static_assert(sizeof(OmegaGpuMem) == 40, "OmegaGpuMem");
+static_assert(offsetof(OmegaGpuMem, va) == 24, "OmegaGpuMem.va");
+static_assert(sizeof(OmegaGpuPfTile) == 32, "OMEGA_QG_TILE_BYTES");
+static_assert(sizeof(OmegaGpuPrefillAttnInfo) == 64, "PrefillAttnInfo");
+static_assert(offsetof(OmegaGpuPrefillAttnInfo, elapsed_ns) == 40, "PrefillAttnInfo.elapsed_ns");
+static_assert(offsetof(OmegaGpuPrefillAttnInfo, kernel_cache_hit) == 56, "PrefillAttnInfo.hit");
 static_assert(sizeof(OmegaGpuFp8Info) == 160, "Fp8Info");
 static_assert(offsetof(OmegaGpuFp8Info, weight_bytes) == 48, "Fp8Info.weight_bytes");
 static_assert(offsetof(OmegaGpuFp8Info, kernel_cache_hit) == 84, "Fp8Info.kernel_cache_hit");

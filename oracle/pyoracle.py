@@ -349,6 +349,82 @@ class Dattn:
             self.h = None
 
 
+def quant_row(x):
+    """oref_quant_row (fake_quant.rs:85-104): e4m3 codes and power-of-two block scales of one row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.size, dtype=np.uint8)
+    s = np.empty(x.size // 128, dtype=np.float32)
+    lib().oref_quant_row(ptr(x), x.size, ptr(q), ptr(s))
+    return q, s
+
+
+def fake_quant(x):
+    """oref_fake_quant_row (fake_quant.rs:107-115): quantise then dequantise one row."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().oref_fake_quant_row(ptr(x), x.size)
+    return x
+
+
+def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, forced=None,
+                 forced_qkv=None, forced_att=None):
+    """The whole-prompt prefill's arithmetic (qwen3_moe_omega_prefill.rs:483-760, W8A8: every
+    GEMM input row fake-quantised per 128-block, the SwiGLU act rounded to bf16 first), layer by
+    layer over the prompt: input RMSNorm, q|k|v, the decode attention of each token at its
+    position (oref_dattn), o, residual, post RMSNorm, router logits (sequential f32), the routing
+    plan (oref_moe_plan), the W8A8 MoE block (oref_moe_block) and the residual. Returns the last
+    token's final-normed hidden row and per layer the residual rows after attention and after
+    the MoE, the router logits and the routed ids. `forced` (per layer the [T][hidden] rows to
+    use as that layer's input instead of the oracle's own, layer 0 included) checks one layer at
+    a time on another implementation's inputs; `forced_qkv` (per layer [T][5120]) gives the rows
+    the attention takes (its K / V rows are bf16-rounded, so an f32 difference of the projection
+    flips one now and then), and `forced_att` (per layer [T][4096]) replaces the
+    attention rows that enter the o projection (the W8A8 quantiser maps an f32 rounding difference
+    of its input to a whole e4m3 step now and then), while the oracle's own attention rows are
+    still returned for comparison."""
+    c = model.cfg
+    eps = c.eps
+    if cache is None:
+        cache = Dattn(c.layers, max_pos, c.rope_theta)
+        for l in range(c.layers):
+            cache.set_norms(l, model.tensor(l, 7), model.tensor(l, 8))
+    emb = model.embed()
+    x = np.stack([bf16_to_f32(emb[t]) for t in tokens]).astype(np.float32)
+    T = len(tokens)
+    out = dict(x_mid=[], x_out=[], logits=[], ids=[], qkv=[], att=[])
+    for l in range(c.layers):
+        if forced is not None:
+            x = np.array(forced[l], dtype=np.float32, copy=True)
+        qw, qs = model.tensor(l, 0)
+        ow, os_ = model.tensor(l, 1)
+        gw, gs = model.tensor(l, 2)
+        dw, ds = model.tensor(l, 3)
+        gate, in_norm, post_norm = model.tensor(l, 4), model.tensor(l, 5), model.tensor(l, 6)
+        qkvs, atts = [], []
+        for t in range(T):
+            xn = fake_quant(rmsnorm(x[t], in_norm, eps))
+            qkv = dequant_matvec(qw[0], qs[0], xn)
+            q_in = qkv if forced_qkv is None else np.asarray(forced_qkv[l][t], dtype=np.float32)
+            att = cache.attend(l, pos0 + t, q_in, eps)
+            qkvs.append(qkv)
+            atts.append(att)
+            a_in = att if forced_att is None else np.asarray(forced_att[l][t], dtype=np.float32)
+            x[t] = x[t] + dequant_matvec(ow[0], os_[0], fake_quant(a_in))
+        out["qkv"].append(np.stack(qkvs))
+        out["att"].append(np.stack(atts))
+        out["x_mid"].append(x.copy())
+        posts = np.stack([rmsnorm(x[t], post_norm, eps) for t in range(T)])
+        logits = np.stack([router_logits(gate, posts[t], refined=False) for t in range(T)])
+        plan = moe_plan(logits, T, c.experts, c.top_k)
+        ids = plan["topk_experts"].reshape(T, c.top_k)
+        wts = plan["topk_weights"].reshape(T, c.top_k)
+        for t in range(T):
+            x[t] = x[t] + moe_block(gw, gs, dw, ds, ids[t], wts[t], posts[t], w8a8=True)
+        out["x_out"].append(x.copy())
+        out["logits"].append(logits)
+        out["ids"].append(ids.copy())
+    return rmsnorm(x[-1], model.final_norm(), eps), out
+
+
 class Model:
     """Synthetic random-init model and the whole-step engine of the oracle."""
 

@@ -1,0 +1,80 @@
+"""Host-side pieces of the whole-prompt prefill boundary (no GPU): the C tile builder against the
+host mirror of build_tiles (aien-omega-pf/src/lib.rs:122-160), the C router packer against the
+packed layout (lib.rs:460-478), the routing plan of the driver against the oracle's
+MoeBatchPlan::from_logits, the host RMSNorm against the oracle's, and the struct layouts."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+
+@pytest.fixture(scope="module")
+def pf():
+    from omega_amd import prefill
+
+    return prefill
+
+
+def test_tile_builder_matches_the_host_mirror(pf):
+    rng = np.random.default_rng(1)
+    for counts in ([5], [64], [65], [0, 0, 3], [130, 0, 1, 64, 200], list(rng.integers(0, 40, 128))):
+        e = len(counts)
+        w = (np.arange(e, dtype=np.uint64) + 1) * 0x100000
+        s = (np.arange(e, dtype=np.uint64) + 1) * 0x1000 + 7
+        want = pf.build_tiles(pf.qgemm_bm(), w, s, counts)
+        got = pf.tiles_va_c(w, s, counts)
+        np.testing.assert_array_equal(got, want)
+        assert int(want["cnt"].sum()) == sum(counts)
+    # a table that would overflow its room is refused (0 tiles)
+    w = np.ones(1, np.uint64)
+    tab = np.zeros(2, pf.TILE_DTYPE)
+    n = pf.lib().omega_gpu_pf_qgemm_tiles_va(1, w.ctypes.data, w.ctypes.data,
+                                             np.array([200], np.uint32).ctypes.data, tab.ctypes.data, 2)
+    assert n == 0
+
+
+def test_router_pack_layout(pf):
+    rng = np.random.default_rng(2)
+    e, k = 6, 16
+    w = rng.standard_normal((e, k)).astype(np.float32)
+    wq = pf.pack_router(w)
+    assert wq.size == pf.router_packed_len(e, k)
+    for g in range(k // 4):
+        for ex in range(e):
+            np.testing.assert_array_equal(wq[(g * e + ex) * 4:(g * e + ex) * 4 + 4], w[ex, 4 * g:4 * g + 4])
+    assert (wq[(k // 4) * e * 4:] == 0).all()
+
+
+def test_routing_plan_matches_the_oracle(pf, oracle):
+    rng = np.random.default_rng(3)
+    T, E, K = 37, 128, 8
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[4, 10] = logits[4, 90] = logits[4].max() + 1.0     # a tie at the top: lower id first
+    logits[5, :] = 0.5                                          # all equal
+    logits[6, 3] = -0.0
+    logits[6, 4] = 0.0                                          # total order: +0.0 above -0.0
+    ids, wts, counts, gtok, a2g = pf.moe_plan(logits.reshape(-1), T, E, K)
+    ref = oracle.moe_plan(logits.reshape(-1), T, E, K)
+    np.testing.assert_array_equal(ids.reshape(-1), ref["topk_experts"])
+    np.testing.assert_allclose(wts.reshape(-1), ref["topk_weights"], rtol=1e-6, atol=0)
+    np.testing.assert_array_equal(counts, np.diff(ref["expert_offsets"]))
+    np.testing.assert_array_equal(gtok, ref["grouped_token_ids"])
+    np.testing.assert_array_equal(a2g, ref["assignment_to_grouped"])
+
+
+def test_host_rmsnorm_matches_the_oracle(pf, oracle):
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((5, 2048)) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2048)).astype(np.float32)
+    got = pf.rmsnorm_rows(x, w, 1e-6)
+    for r in range(5):
+        np.testing.assert_array_equal(got[r], oracle.rmsnorm(x[r], w, 1e-6))
+
+
+def test_struct_layouts(pf):
+    assert C.sizeof(pf.OmegaGpuMem) == 40
+    assert pf.OmegaGpuMem.va.offset == 24
+    assert C.sizeof(pf.PrefillAttnInfo) == 64
+    assert pf.PrefillAttnInfo.elapsed_ns.offset == 40
+    assert pf.PrefillAttnInfo.kernel_cache_hit.offset == 56
+    assert pf.TILE_DTYPE.itemsize == pf.TILE_BYTES
