@@ -235,6 +235,73 @@ def bench_gemv(om, args):
     y.free()
 
 
+# ---------------------------------------------------------------- whole-prompt prefill (time to first token)
+def bench_prefill(om, args):
+    """The whole-prompt prefill of the full 48-layer model (the reference's prefill boundary:
+    W8A8 quantiser + grouped GEMM + prefill attention, host RMSNorms / routing plan as in the
+    reference driver) for a seeded prompt of each length in --prefill-lengths, then the lm_head
+    and argmax of the last token: time to first token (wall, host included) and the chip time of
+    the prefill launches. The decode-graph alternative (every prompt token one decode step) is
+    printed beside it from the bs=1 step time when --prefill-decode-ms is given."""
+    from omega_amd import prefill as pf
+
+    lengths = [int(v) for v in args.prefill_lengths.split(",")]
+    max_pos = om.round_max_pos(max(lengths) + 8)
+    t0 = time.time()
+    layers, tensors = [], []
+    ones = np.ones(H, np.float32)
+    for l in range(L):
+        qkv = om.Fp8Tensor.synth(1, 5120, 2048, SEED, tid(l, 0))
+        o = om.Fp8Tensor.synth(1, 2048, 4096, SEED, tid(l, 1))
+        gu = om.Fp8Tensor.synth(E, 1536, 2048, SEED, tid(l, 2))
+        dn = om.Fp8Tensor.synth(E, 2048, 768, SEED, tid(l, 3))
+        tensors += [qkv, o, gu, dn]
+        gate = om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02)
+        layers.append(dict(qkv=qkv, o=o, gate_up=gu, down=dn, input_norm=ones, post_norm=ones,
+                           router=(gate.astype(np.uint32) << 16).view(np.float32)))
+    cache = om.DecodeAttnCache(L, max_pos, 1e6)
+    for l in range(L):
+        cache.set_norms(l, np.ones(HD, np.float32), np.ones(HD, np.float32))
+    lm = om.Bf16Tensor.synth(V, H, SEED, 2, 0.02)
+    embed_host = om.synth_bf16_host(SEED, 1, (V, H), 0.02)
+    wp = pf.WholePromptPrefill(layers, ones, lambda t: (embed_host[t].astype(np.uint32) << 16).view(np.float32),
+                               cache, 1e-6)
+    om.sync()
+    build_s = time.time() - t0
+    rng = np.random.default_rng(SEED)
+    points = []
+    for m in lengths:
+        prompt = rng.integers(0, V, m).tolist()
+        wp.run(prompt[:8], 0)  # warm: buffers sized, code paths touched
+        pf.stats_reset()
+        t1 = time.perf_counter()
+        hidden = wp.run(prompt, 0)
+        logits, _ = lm.gemv_f32(hidden)
+        tok = int(np.argmax(logits))
+        ttft = time.perf_counter() - t1
+        chip_ns, launches = pf.stats()
+        line = {"workload": "whole_prompt_prefill", "tokens": m, "ttft_s": round(ttft, 4),
+                "chip_ms": round(wp.stats["chip_ns"] / 1e6, 2), "pf_launch_ms": round(chip_ns / 1e6, 2),
+                "pf_launches": launches, "prompt_tok_s": round(m / ttft, 1), "first_token": tok}
+        if args.prefill_decode_ms:
+            line["decode_graph_prompt_s"] = round(m * args.prefill_decode_ms / 1e3, 3)
+        print(json.dumps(line), flush=True)
+        points.append(line)
+    print(json.dumps({
+        "metric": "Qwen3-30B-A3B FP8 whole-prompt prefill, time to first token",
+        "value": points[0]["ttft_s"], "unit": "s", "n_gpus": 1, "higher_is_better": False,
+        "dtype": "fp8 (W8A8: e4m3 weights and activations, fp32 accumulate)",
+        "data": "synthetic random-init weights, seeded prompt",
+        "config": {"workload": "whole-prompt prefill through the omega_gpu_pf_* boundary and the host "
+                               "driver mirror", "lengths": lengths},
+        "points": points, "extra": {"build_s": round(build_s, 1)}}), flush=True)
+    wp.free()
+    cache.free()
+    lm.free()
+    for t in tensors:
+        t.free()
+
+
 # ---------------------------------------------------------------- configuration 3: paged attention
 PAGED_POINTS = [(b, l) for b in (1, 8, 32) for l in (2048, 8192, 32768)]
 
@@ -585,9 +652,10 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill"], default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
-                         "gemv: the q|k|v FP8 GEMV (configuration 1); "
+                         "gemv: the q|k|v FP8 GEMV (configuration 1); prefill: whole-prompt prefill "
+                         "time to first token; "
                          "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
                          "at token batch 1 and 32 (configuration 2); serve: 32 sequences of batched "
                          "decode over long contexts (configuration 5)")
@@ -596,6 +664,9 @@ def main():
     ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--gemv-reps", type=int, default=200)
+    ap.add_argument("--prefill-lengths", default="512,2048")
+    ap.add_argument("--prefill-decode-ms", type=float, default=0.0,
+                    help="bs=1 decode step time, for the token-by-token prompt time beside the prefill")
     ap.add_argument("--no-bs32", action="store_true",
                     help="decode workload: skip the 32-sequence batched figure (configuration 5)")
     ap.add_argument("--bs32-steps", type=int, default=64)
@@ -617,6 +688,9 @@ def main():
         return
     if args.workload == "gemv":
         bench_gemv(om, args)
+        return
+    if args.workload == "prefill":
+        bench_prefill(om, args)
         return
     if args.workload == "paged":
         bench_paged(om, args)
