@@ -284,6 +284,41 @@ __global__ __launch_bounds__(256) void k_pf_combine(const PfCombineArgs a) {
     a.out[(size_t)r * a.h + c] = acc;
 }
 
+// ------------------------------------------------------------------ residual add + RMSNorm (extension)
+// Per row: x += add (when given, in place), then out = x * scale * w with scale = (1 / sqrt(mean
+// of squares + eps)) rounded to f32 and the squares summed in f64 (tensor.rs:94-110), so the
+// driver's residual stays on the device between the GEMMs.
+struct PfNormArgs {
+    uint32_t k = 0;
+    float *x = nullptr;
+    const float *add = nullptr, *w = nullptr;
+    float eps = 1e-6f;
+    float *out = nullptr;
+};
+
+__global__ __launch_bounds__(256) void k_pf_resid_norm(const PfNormArgs a) {
+#pragma clang fp contract(off)  // x + add and x * scale * w each rounded as written
+    __shared__ double red[4];
+    const uint32_t r = blockIdx.x, t = threadIdx.x, lane = lane_id(), wid = t >> 6;
+    float *xr = a.x + (size_t)r * a.k;
+    const float *ar = a.add ? a.add + (size_t)r * a.k : nullptr;
+    double ss = 0.0;
+    for (uint32_t c = t; c < a.k; c += 256) {
+        float v = xr[c];
+        if (ar) {
+            v = v + ar[c];
+            xr[c] = v;
+        }
+        ss += (double)v * (double)v;
+    }
+    ss = wave_sum_f64(ss);
+    if (lane == 0) red[wid] = ss;
+    __syncthreads();
+    const float scale = rms_scale((red[0] + red[1]) + (red[2] + red[3]), a.k, a.eps);
+    float *orow = a.out + (size_t)r * a.k;
+    for (uint32_t c = t; c < a.k; c += 256) orow[c] = xr[c] * scale * a.w[c];
+}
+
 // ------------------------------------------------------------------ session memory and counters
 struct PfState {
     std::mutex mu;
@@ -556,6 +591,29 @@ int omega_gpu_pf_moe_combine(uint32_t h, uint32_t top_k, uint32_t rows, uint64_t
     a.out = reinterpret_cast<float *>(out_va);
     return pf_timed(F_SESSION, 1, ns, [&](hipStream_t st) {
         OMEGA_LAUNCH(k_pf_combine, dim3((h + 255) / 256, rows), dim3(256), 0, st, a);
+        return hipGetLastError();
+    });
+}
+
+int omega_gpu_pf_residual_norm(uint32_t k, uint32_t rows, uint64_t x_va, uint64_t add_va, uint64_t w_va, float eps,
+                               uint64_t out_va, uint64_t *ns) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (k == 0 || k > 65536 || !x_va || !w_va || !out_va || rows > 0x7fffffffu) {
+        set_error(F_SESSION, "pf residual norm: k=%u (1..=65536), non-NULL x, weights and out", k);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    if (ns) *ns = 0;
+    if (rows == 0) return OMEGA_GPU_OK;
+    PfNormArgs a;
+    a.k = k;
+    a.x = reinterpret_cast<float *>(x_va);
+    a.add = reinterpret_cast<const float *>(add_va);
+    a.w = reinterpret_cast<const float *>(w_va);
+    a.eps = eps;
+    a.out = reinterpret_cast<float *>(out_va);
+    return pf_timed(F_SESSION, 1, ns, [&](hipStream_t st) {
+        OMEGA_LAUNCH(k_pf_resid_norm, dim3(rows), dim3(256), 0, st, a);
         return hipGetLastError();
     });
 }

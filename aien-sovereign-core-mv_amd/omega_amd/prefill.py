@@ -182,6 +182,14 @@ def moe_combine(h, top_k, rows, down_va, inv_va, wt_va, out_va):
     return ns.value
 
 
+def residual_norm(k, rows, x_va, add_va, w_va, eps, out_va):
+    """omega_gpu_pf_residual_norm: x += add (add_va 0: no add), out = rmsnorm(x) * w; chip ns"""
+    ns = C.c_uint64()
+    _pf_check(lib().omega_gpu_pf_residual_norm(k, rows, _va(x_va), _va(add_va), _va(w_va), float(eps), _va(out_va),
+                                               C.addressof(ns)), "pf residual norm")
+    return ns.value
+
+
 def copy_va(dst_va, src_va, nbytes):
     _pf_check(lib().omega_gpu_pf_copy_va(_va(dst_va), _va(src_va), nbytes), "pf copy")
 
@@ -287,10 +295,22 @@ class WholePromptPrefill:
             host.host(np.float32)[:] = wq
             copy_va(wq_dev.va, host.va, wq.nbytes)  # (k / 4 + 1) x e x 16 bytes: a 16-byte multiple
             host.free()
-            self.layers.append(dict(ent=ent, wq=wq_dev, input_norm=np.asarray(L["input_norm"], np.float32),
-                                    post_norm=np.asarray(L["post_norm"], np.float32)))
+            self.layers.append(dict(ent=ent, wq=wq_dev, input_norm=self._const(L["input_norm"]),
+                                    post_norm=self._const(L["post_norm"])))
+        self.final_dev = self._const(self.final_norm)
         self.bufs = None
         self.stats = {}
+
+    @staticmethod
+    def _const(v):
+        """an f32 vector uploaded once to a device buffer"""
+        v = np.ascontiguousarray(v, np.float32)
+        nb = (v.nbytes + 15) // 16 * 16
+        dev, host = PfMem(nb), PfMem(nb, host=True)
+        host.host(np.float32)[:v.size] = v
+        copy_va(dev.va, host.va, nb)
+        host.free()
+        return dev
 
     def _ensure(self, m):
         if self.bufs is not None and self.bufs["m"] >= m:
@@ -305,7 +325,7 @@ class WholePromptPrefill:
         # DEVICE buffers, and the copies between them are DMA (omega_gpu_pf_copy_va)
         b = dict(m=m, max_tiles=max_tiles,
                  stage=PfMem(max(mt * max(h, e), m * qkv_n, g * h) * 4 + g * 8, host=True),
-                 xin=PfMem(mt * h * 4), xq=PfMem((m + bm) * kmax), xs=PfMem((m + bm) * (kmax // BLOCK) * 4),
+                 x=PfMem(m * h * 4), xin=PfMem(mt * h * 4), xq=PfMem((m + bm) * kmax), xs=PfMem((m + bm) * (kmax // BLOCK) * 4),
                  qkv=PfMem(m * qkv_n * 4), att=PfMem(m * qd * 4), oproj=PfMem(m * h * 4),
                  logits=PfMem(mt * e * 4), rowidx=PfMem((g + bm) * 4),
                  act=PfMem(g * i * 2), aq=PfMem((g + bm) * i), a_s=PfMem((g + bm) * (i // BLOCK) * 4),
@@ -350,12 +370,15 @@ class WholePromptPrefill:
         h, qd, qkv_n, e, top_k, i, eps = self.h, self.qd, self.qkv_n, self.e, self.top_k, self.i, self.eps
         g = m * top_k
         b = self._ensure(m)
-        x = np.stack([np.asarray(self.embed_row(t), np.float32) for t in tokens])
+        self._up(b["x"], np.stack([np.asarray(self.embed_row(t), np.float32) for t in tokens]))
         chip = 0
         dense = [m]
+        add = 0  # the previous layer's MoE rows, added to the residual by the next norm
         for l, L in enumerate(self.layers):
             ent = L["ent"]
-            self._up(b["xin"], rmsnorm_rows(x, L["input_norm"], eps))
+            chip += residual_norm(h, m, b["x"].va, add, L["input_norm"].va, eps, b["xin"].va)
+            if trace is not None and l > 0:
+                trace.setdefault("x_out", []).append(self._down(b["x"], np.float32, m * h).reshape(m, h))
             chip += quant(h, IN_F32, m, b["xin"].va, b["xq"].va, b["xs"].va)
             tv, nt = self._put_tiles(b, 0, [ent["qkv"][0]], [ent["qkv"][1]], dense)
             chip += qgemm(qkv_n, h, PLAIN, tv, nt, 0, b["xq"].va, b["xs"].va, b["qkv"].va)
@@ -367,15 +390,14 @@ class WholePromptPrefill:
             chip += quant(qd, IN_F32, m, b["att"].va, b["xq"].va, b["xs"].va)
             tv, nt = self._put_tiles(b, 1, [ent["o"][0]], [ent["o"][1]], dense)
             chip += qgemm(h, qd, PLAIN, tv, nt, 0, b["xq"].va, b["xs"].va, b["oproj"].va)
-            x = x + self._down(b["oproj"], np.float32, m * h).reshape(m, h)
-            post = rmsnorm_rows(x, L["post_norm"], eps)
-            self._up(b["xin"], post)  # the post-norm rows: quantiser and router input
+            # x += o_proj, then the post-norm rows: the quantiser's and the router's input
+            chip += residual_norm(h, m, b["x"].va, b["oproj"].va, L["post_norm"].va, eps, b["xin"].va)
             chip += router_logits(h, e, m, b["xin"].va, L["wq"].va, b["logits"].va)
             logits = self._down(b["logits"], np.float32, m * e)
             ids, wts, counts, grouped_token, a2g = moe_plan(logits, m, e, top_k)
             if trace is not None:
-                trace.setdefault("x_mid", []).append(x.copy())
-                trace.setdefault("post", []).append(post.copy())
+                trace.setdefault("x_mid", []).append(self._down(b["x"], np.float32, m * h).reshape(m, h))
+                trace.setdefault("post", []).append(self._down(b["xin"], np.float32, m * h).reshape(m, h))
                 trace.setdefault("ids", []).append(ids.copy())
                 trace.setdefault("wts", []).append(wts.copy())
                 trace.setdefault("a2g", []).append(a2g.copy())
@@ -397,13 +419,18 @@ class WholePromptPrefill:
             if trace is not None:
                 trace.setdefault("act", []).append(self._down(b["act"], np.uint16, g * i).reshape(g, i))
                 trace.setdefault("down", []).append(self._down(b["down"], np.float32, g * h).reshape(g, h))
-            x = x + self._down(b["moe"], np.float32, m * h).reshape(m, h)
-            if trace is not None:
-                trace.setdefault("x_out", []).append(x.copy())
+            add = b["moe"].va
+        # the last MoE add, then the final norm (over every row: one launch either way)
+        chip += residual_norm(h, m, b["x"].va, add, self.final_dev.va, eps, b["xin"].va)
+        if trace is not None:
+            trace.setdefault("x_out", []).append(self._down(b["x"], np.float32, m * h).reshape(m, h))
         self.stats = dict(tokens=m, chip_ns=chip)
-        return rmsnorm_rows(x[-1:], self.final_norm, eps)[0]
+        return self._down(b["xin"], np.float32, m * h)[(m - 1) * h:].copy()
 
     def free(self):
         self.bufs = None
         for L in self.layers:
             L["wq"].free()
+            L["input_norm"].free()
+            L["post_norm"].free()
+        self.final_dev.free()

@@ -543,6 +543,12 @@ int omega_gpu_prefill_attn_dev(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint3
  * Not in the reference ABI: entry points for callers whose inputs already live in HBM (the
  * benchmark and the parity tests at full size). Same kernels as the entries above. */
 
+/* The whole-prompt driver's residual and RMSNorm on the device (not in the reference ABI, whose
+ * driver does both on the host, qwen3_moe_omega_prefill.rs:590-660): per row of k, x += add when
+ * add_va is not 0 (in place), then out = x * scale * w, scale = 1 / sqrt(mean(x^2) + eps) with
+ * an f64 sum of squares rounded to f32 (tensor.rs:94-110). Synchronous; chip ns in *ns. */
+int omega_gpu_pf_residual_norm(uint32_t k, uint32_t rows, uint64_t x_va, uint64_t add_va, uint64_t w_va, float eps,
+                               uint64_t out_va, uint64_t *ns);
 /* Synthetic random-init FP8 tensor generated on the device: W ~ N(0, sigma) per element from
  * the counter-based generator (seed, tensor_id, element index), per 128x128 block
  * s = bf16(absmax / 448), q = e4m3(W / s). Bit-identical to the CPU generator of the tests. */
