@@ -231,10 +231,15 @@ __global__ __launch_bounds__(256) void k_pf_qgemm(const PfGemmArgs a) {
 // ------------------------------------------------------------------ router logits
 // logits[r][ex] = (((-0.0 + w[ex][0] x[r][0]) + w[ex][1] x[r][1]) + ...): each product rounded to
 // f32, then added in index order (no fused multiply-add), the reference's sequential f32 sum. The
-// packed layout wq[g][ex][q] = w[ex][4 g + q] gives each expert's thread 16 contiguous bytes per
-// group, neighbouring experts neighbouring bytes. One thread per (row, expert); rows in tiles of
-// kPfRouterRows (the buffers hold whole tiles).
+// sum cannot be split along k, so the parallelism is (row, expert): one lane per expert, R rows
+// per lane as R independent chains. The packed layout wq[g][ex][q] = w[ex][4 g + q] gives a
+// wavefront of 64 experts one contiguous KiB per group of 4 columns; the R rows of x are staged
+// through LDS in passes of kPfRouterKc columns and read as broadcasts, and the weight groups are
+// loaded kPfRouterNg at a time in two register sets so the next set is in flight while one is
+// summed. Rows come in tiles of kPfRouterRows (the buffers hold whole tiles).
 constexpr uint32_t kPfRouterRows = 4;
+constexpr uint32_t kPfRouterKc = 1024;
+constexpr uint32_t kPfRouterNg = 4;
 
 struct PfRouterArgs {
     uint32_t k = 0, e = 0, rows = 0;
@@ -242,22 +247,70 @@ struct PfRouterArgs {
     float *logits = nullptr;
 };
 
+template <int R>
 __global__ __launch_bounds__(256) void k_pf_router(const PfRouterArgs a) {
 #pragma clang fp contract(off)  // a multiply then an add, never one fused rounding
-    const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t ex = t % a.e, r = t / a.e;
-    if (r >= a.rows) return;
-    const float *xr = a.x + (size_t)r * a.k;
-    float acc = -0.0f;
-    for (uint32_t g = 0; g < a.k / 4; ++g) {
-        const f32x4 wv = *as_global_f32x4(a.wq + ((size_t)g * a.e + ex) * 4);
-        const f32x4 xv = *as_global_f32x4(xr + 4 * g);
-        acc = acc + wv.x * xv.x;
-        acc = acc + wv.y * xv.y;
-        acc = acc + wv.z * xv.z;
-        acc = acc + wv.w * xv.w;
+    constexpr uint32_t NG = kPfRouterNg, KQ = kPfRouterKc / 4;
+    __shared__ f32x4 xs[R][KQ];
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const uint32_t ex = blockIdx.x * nt + tid;
+    const uint32_t exl = ex < a.e ? ex : a.e - 1;  // lanes past the last expert load its weights
+    const uint32_t r0 = blockIdx.y * R;
+    const size_t gs = (size_t)a.e * 4;
+    const float *wp = a.wq + (size_t)exl * 4;
+    float acc[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[j] = -0.0f;
+    auto sum_group = [&](const f32x4 w, uint32_t q) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const f32x4 xv = xs[j][q];
+            acc[j] = acc[j] + w.x * xv.x;
+            acc[j] = acc[j] + w.y * xv.y;
+            acc[j] = acc[j] + w.z * xv.z;
+            acc[j] = acc[j] + w.w * xv.w;
+        }
+    };
+    const uint32_t ng = a.k / 4;
+    for (uint32_t c0 = 0; c0 < ng; c0 += KQ) {
+        const uint32_t cn = ng - c0 < KQ ? ng - c0 : KQ;  // groups in this pass
+        __syncthreads();                                  // the previous pass is read
+        for (uint32_t i = tid; i < R * cn; i += nt) {
+            const uint32_t j = i / cn, q = i - j * cn;
+            xs[j][q] = *as_global_f32x4(a.x + (size_t)(r0 + j) * a.k + 4 * (size_t)(c0 + q));
+        }
+        __syncthreads();
+        const float *wc = wp + (size_t)c0 * gs;
+        auto load = [&](f32x4 (&w)[NG], uint32_t q) {
+#pragma unroll
+            for (uint32_t i = 0; i < NG; ++i) w[i] = *as_global_f32x4(wc + (size_t)(q + i) * gs);
+        };
+        auto sum_set = [&](const f32x4 (&w)[NG], uint32_t q) {
+#pragma unroll
+            for (uint32_t i = 0; i < NG; ++i) sum_group(w[i], q + i);
+        };
+        uint32_t q = 0;
+        if (cn >= 2 * NG) {
+            f32x4 A[NG], B[NG];
+            load(A, 0);
+            for (; q + 2 * NG <= cn; q += 2 * NG) {
+                load(B, q + NG);
+                sum_set(A, q);
+                const uint32_t qa = q + 2 * NG <= cn - NG ? q + 2 * NG : cn - NG;  // stays in the pass
+                load(A, qa);
+                sum_set(B, q + NG);
+            }
+            if (q + NG <= cn) {  // A holds the set at q
+                sum_set(A, q);
+                q += NG;
+            }
+        }
+        for (; q < cn; ++q) sum_group(*as_global_f32x4(wc + (size_t)q * gs), q);
     }
-    a.logits[(size_t)r * a.e + ex] = acc;
+    if (ex < a.e) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) a.logits[(size_t)(r0 + j) * a.e + ex] = acc[j];
+    }
 }
 
 // ------------------------------------------------------------------ MoE combine
@@ -563,10 +616,31 @@ int omega_gpu_pf_router_logits(uint32_t k, uint32_t e, uint32_t rows, uint64_t x
     a.x = reinterpret_cast<const float *>(x_va);
     a.wq = reinterpret_cast<const float *>(wq_va);
     a.logits = reinterpret_cast<float *>(logits_va);
-    const uint64_t threads = (uint64_t)a.rows * e;
-    return pf_timed(F_SESSION, 1, ns, [&](hipStream_t st) {
-        OMEGA_LAUNCH(k_pf_router, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, st, a);
-        return hipGetLastError();
+    // a workgroup spans up to 256 experts; R rows per lane when that still gives one wavefront
+    // per SIMD (1024 on the chip), else fewer
+    const uint32_t waves_e = (e + 63) / 64, ew = waves_e < 4 ? waves_e : 4, nt = 64 * ew;
+    const uint32_t gx = (e + nt - 1) / nt;
+    const uint64_t waves1 = (uint64_t)gx * ew * a.rows;
+    const int r = waves1 >= 4 * 1024ull ? 4 : waves1 >= 2 * 1024ull ? 2 : 1;
+    const uint32_t max_rows = 32768 * (uint32_t)r;  // grid.y stays within 32768 row groups
+    const uint32_t launches = (a.rows + max_rows - 1) / max_rows;
+    return pf_timed(F_SESSION, launches, ns, [&](hipStream_t st) {
+        for (uint32_t r0 = 0; r0 < a.rows; r0 += max_rows) {
+            PfRouterArgs b = a;
+            b.rows = a.rows - r0 < max_rows ? a.rows - r0 : max_rows;
+            b.x = a.x + (size_t)r0 * k;
+            b.logits = a.logits + (size_t)r0 * e;
+            const dim3 grid(gx, b.rows / r);
+            if (r == 4)
+                OMEGA_LAUNCH(k_pf_router<4>, grid, dim3(nt), 0, st, b);
+            else if (r == 2)
+                OMEGA_LAUNCH(k_pf_router<2>, grid, dim3(nt), 0, st, b);
+            else
+                OMEGA_LAUNCH(k_pf_router<1>, grid, dim3(nt), 0, st, b);
+            const hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
+        return hipSuccess;
     });
 }
 

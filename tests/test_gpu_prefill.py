@@ -176,9 +176,21 @@ def test_qgemm_grouped_swiglu_and_down(omega, oracle, pf):
     DN.free()
 
 
-def test_router_logits_are_the_sequential_f32_sum(omega, oracle, pf):
-    rng = np.random.default_rng(6)
-    e, k, rows = 128, 2048, 9
+def sequential_logits(wq_rows, x):
+    """logits[r][ex] = the f32 sum from -0.0, in column order, of f32-rounded products, every
+    row and expert at once (numpy float32 arithmetic rounds each product and each sum)"""
+    acc = np.full((x.shape[0], wq_rows.shape[0]), -0.0, np.float32)
+    for j in range(x.shape[1]):
+        acc = acc + np.outer(x[:, j], wq_rows[:, j]).astype(np.float32)
+    return acc
+
+
+@pytest.mark.parametrize("e,k,rows", [(128, 2048, 9), (72, 100, 5), (300, 3000, 7), (128, 2048, 1100),
+                                      (128, 2048, 2049)])
+def test_router_logits_are_the_sequential_f32_sum(omega, oracle, pf, e, k, rows):
+    # rows 1100 and 2049 take the 2- and 4-row-per-lane launches; e = 72 and 300 leave lanes
+    # past the last expert; k = 100 and 3000 end in partial weight sets and a partial LDS pass
+    rng = np.random.default_rng(6 + rows)
     t = pf.router_rows()
     w = oracle.bf16_to_f32(oracle.f32_to_bf16((rng.standard_normal((e, k)) * 0.02).astype(np.float32)))
     rt = -(-rows // t) * t
@@ -189,9 +201,12 @@ def test_router_logits_are_the_sequential_f32_sum(omega, oracle, pf):
     ld = omega.DeviceBuffer(rt * e * 4)
     pf.router_logits(k, e, rows, xd.ptr, wd.ptr, ld.ptr)
     got = ld.download(np.float32, rows * e).reshape(rows, e)
-    for r in range(rows):
+    for r in range(min(rows, 3)):  # the oracle's sequential router, row by row
         want = oracle.router_logits(oracle.f32_to_bf16(w), x[r], refined=False)
         np.testing.assert_array_equal(got[r].view(np.uint32), want.view(np.uint32))
+    want = sequential_logits(w, x[:rows])
+    np.testing.assert_array_equal(want[:min(rows, 3)].view(np.uint32), got[:min(rows, 3)].view(np.uint32))
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_moe_combine_slot_order(omega, pf):
