@@ -542,6 +542,74 @@ uint32_t omega_gpu_pf_qgemm_tiles_va(uint32_t experts, const uint64_t *w_va, con
     return n;
 }
 
+int omega_gpu_pf_moe_plan(uint32_t tokens, uint32_t experts, uint32_t top_k, const float *logits, uint32_t *topk_ids,
+                          float *topk_weights, uint32_t *counts, uint32_t *grouped_token,
+                          uint32_t *assignment_to_grouped, uint32_t *grouped_to_assignment) {
+    clear_error(F_SESSION);
+    if (experts == 0 || experts > 65536 || top_k == 0 || top_k > experts || top_k > 64 ||
+        (uint64_t)tokens * top_k > 0xffffffffull || !logits || !topk_ids || !topk_weights || !counts ||
+        !grouped_token || !assignment_to_grouped) {
+        set_error(F_SESSION, "pf moe plan: experts=%u, top_k=%u (1..=min(experts, 64)), tokens=%u, non-NULL "
+                  "buffers", experts, top_k, tokens);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    // the total order of f32 (f32::total_cmp) as a signed key: negative values count down
+    auto key = [](float v) {
+        const int32_t b = (int32_t)__builtin_bit_cast(uint32_t, v);
+        return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+    };
+    for (uint32_t e = 0; e < experts; ++e) counts[e] = 0;
+    for (uint32_t t = 0; t < tokens; ++t) {
+        const float *row = logits + (size_t)t * experts;
+        // top_k by (key descending, id ascending): insertion into a sorted list of top_k
+        uint32_t sel[64];
+        int32_t sk[64];
+        uint32_t n = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            if (!std::isfinite(row[e])) {
+                set_error(F_SESSION, "pf moe plan: logit of token %u, expert %u is not finite", t, e);
+                return OMEGA_GPU_BAD_ARGS;
+            }
+            const int32_t k = key(row[e]);
+            if (n == top_k && k <= sk[n - 1]) continue;  // a tie goes to the lower id, already held
+            uint32_t i = n < top_k ? n++ : n - 1;
+            while (i > 0 && sk[i - 1] < k) {
+                sk[i] = sk[i - 1];
+                sel[i] = sel[i - 1];
+                --i;
+            }
+            sk[i] = k;
+            sel[i] = e;
+        }
+        const float mx = row[sel[0]];
+        float prob[64], sum = 0.0f;
+        for (uint32_t j = 0; j < top_k; ++j) {
+            prob[j] = std::exp(row[sel[j]] - mx);
+            sum += prob[j];
+        }
+        for (uint32_t j = 0; j < top_k; ++j) {
+            topk_ids[(size_t)t * top_k + j] = sel[j];
+            topk_weights[(size_t)t * top_k + j] = prob[j] / sum;
+            ++counts[sel[j]];
+        }
+    }
+    // stable counting sort of the assignments by expert
+    std::vector<uint32_t> cursor(experts);
+    uint32_t acc = 0;
+    for (uint32_t e = 0; e < experts; ++e) {
+        cursor[e] = acc;
+        acc += counts[e];
+    }
+    const uint64_t assignments = (uint64_t)tokens * top_k;
+    for (uint64_t a = 0; a < assignments; ++a) {
+        const uint32_t g = cursor[topk_ids[a]]++;
+        assignment_to_grouped[a] = g;
+        grouped_token[g] = (uint32_t)(a / top_k);
+        if (grouped_to_assignment) grouped_to_assignment[g] = (uint32_t)a;
+    }
+    return OMEGA_GPU_OK;
+}
+
 int omega_gpu_pf_qgemm(uint32_t n, uint32_t k, uint32_t layout, uint64_t tiles_va, uint32_t ntiles,
                        uint64_t rowidx_va, uint64_t xq_va, uint64_t xs_va, uint64_t y_va, uint64_t *ns) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());

@@ -240,6 +240,7 @@ SIGNATURES = {
     "omega_gpu_prefill_attn": (i32, [P, u32, u32, u32, P, f32, f32, P, P]),
     "omega_gpu_prefill_attn_dev": (i32, [P, u32, u32, u32, u64, f32, f32, u64, P]),
     "omega_gpu_pf_residual_norm": (i32, [u32, u32, u64, u64, u64, f32, u64, P]),
+    "omega_gpu_pf_moe_plan": (i32, [u32, u32, u32, P, P, P, P, P, P, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),

@@ -237,35 +237,22 @@ def rmsnorm_rows(x, w, eps):
     return (x * scale[..., None]) * np.asarray(w, np.float32)
 
 
-def _total_key(v):
-    b = v.view(np.int32).astype(np.int64)
-    return np.where(b < 0, b ^ 0x7FFFFFFF, b)
-
-
 def moe_plan(logits, tokens, experts, top_k):
-    """MoeBatchPlan::from_logits (moe_plan.rs:86-171): per token the top_k experts by total order
-    (ties to the lower id), weights exp(l - max) / sum over the selected in f32, then the stable
-    counting sort of the (token, slot) assignments by expert. Returns (ids [t][k], weights
-    [t][k], counts [e], grouped_token [t*k], assignment_to_grouped [t*k])."""
-    lg = np.asarray(logits, np.float32).reshape(tokens, experts)
-    if not np.isfinite(lg).all():
-        raise OmegaGpuError(-1, "routing: a logit is not finite")
-    key = _total_key(lg)
-    order = np.argsort(-key, axis=1, kind="stable")[:, :top_k]
-    ids = order.astype(np.uint32)
-    sel = np.take_along_axis(lg, order, axis=1)
-    prob = np.exp(sel - sel[:, :1]).astype(np.float32)
-    s = np.zeros(tokens, np.float32)
-    for j in range(top_k):
-        s = (s + prob[:, j]).astype(np.float32)
-    wts = (prob / s[:, None]).astype(np.float32)
-    flat = ids.reshape(-1)
-    counts = np.bincount(flat, minlength=experts).astype(np.uint32)
-    grouped_of = np.argsort(flat, kind="stable")          # grouped row -> assignment
-    a2g = np.empty_like(grouped_of)
-    a2g[grouped_of] = np.arange(flat.size)
-    grouped_token = (grouped_of // top_k).astype(np.uint32)
-    return ids, wts, counts, grouped_token, a2g.astype(np.uint32)
+    """MoeBatchPlan::from_logits (moe_plan.rs:86-171) in the library (omega_gpu_pf_moe_plan): per
+    token the top_k experts by total order (ties to the lower id), weights exp(l - max) / sum over
+    the selected in f32, then the stable counting sort of the (token, slot) assignments by
+    expert. Returns (ids [t][k], weights [t][k], counts [e], grouped_token [t*k],
+    assignment_to_grouped [t*k])."""
+    lg = np.ascontiguousarray(np.asarray(logits, np.float32).reshape(tokens, experts))
+    ids = np.empty((tokens, top_k), np.uint32)
+    wts = np.empty((tokens, top_k), np.float32)
+    counts = np.empty(experts, np.uint32)
+    grouped_token = np.empty(tokens * top_k, np.uint32)
+    a2g = np.empty(tokens * top_k, np.uint32)
+    _pf_check(lib().omega_gpu_pf_moe_plan(tokens, experts, top_k, lg.ctypes.data, ids.ctypes.data,
+                                          wts.ctypes.data, counts.ctypes.data, grouped_token.ctypes.data,
+                                          a2g.ctypes.data, None), "pf moe plan")
+    return ids, wts, counts, grouped_token, a2g
 
 
 # ------------------------------------------------------------------ the driver

@@ -543,6 +543,16 @@ int omega_gpu_prefill_attn_dev(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint3
  * Not in the reference ABI: entry points for callers whose inputs already live in HBM (the
  * benchmark and the parity tests at full size). Same kernels as the entries above. */
 
+/* The MoE routing plan of the whole-prompt driver on the host (not in the reference ABI: the
+ * reference driver builds it in Rust, MoeBatchPlan::from_logits, moe_plan.rs:86-171, restated
+ * here): per token the top_k experts by f32 total order with ties to the lower id, weights
+ * expf(l - max) / sum in f32 in slot order, then the stable counting sort of the token-major
+ * assignments by expert. Outputs: topk_ids / topk_weights [tokens][top_k], counts [experts],
+ * grouped_token and assignment_to_grouped [tokens * top_k], grouped_to_assignment (may be NULL).
+ * A non-finite logit is refused with BAD_ARGS naming the token and expert. No device work. */
+int omega_gpu_pf_moe_plan(uint32_t tokens, uint32_t experts, uint32_t top_k, const float *logits, uint32_t *topk_ids,
+                          float *topk_weights, uint32_t *counts, uint32_t *grouped_token,
+                          uint32_t *assignment_to_grouped, uint32_t *grouped_to_assignment);
 /* The whole-prompt driver's residual and RMSNorm on the device (not in the reference ABI, whose
  * driver does both on the host, qwen3_moe_omega_prefill.rs:590-660): per row of k, x += add when
  * add_va is not 0 (in place), then out = x * scale * w, scale = 1 / sqrt(mean(x^2) + eps) with

@@ -45,21 +45,42 @@ def test_router_pack_layout(pf):
     assert (wq[(k // 4) * e * 4:] == 0).all()
 
 
-def test_routing_plan_matches_the_oracle(pf, oracle):
-    rng = np.random.default_rng(3)
-    T, E, K = 37, 128, 8
+def total_order_topk(lg, k):
+    """numpy restatement: stable descending sort of the f32 total-order keys (ties: lower id)"""
+    b = lg.view(np.int32).astype(np.int64)
+    key = np.where(b < 0, b ^ 0x7FFFFFFF, b)
+    return np.argsort(-key, axis=1, kind="stable")[:, :k]
+
+
+@pytest.mark.parametrize("T,E,K", [(37, 128, 8), (2048, 128, 8), (19, 60, 4), (3, 8, 8)])
+def test_routing_plan_matches_the_oracle(pf, oracle, T, E, K):
+    rng = np.random.default_rng(3 + T)
     logits = rng.standard_normal((T, E)).astype(np.float32)
-    logits[4, 10] = logits[4, 90] = logits[4].max() + 1.0     # a tie at the top: lower id first
-    logits[5, :] = 0.5                                          # all equal
-    logits[6, 3] = -0.0
-    logits[6, 4] = 0.0                                          # total order: +0.0 above -0.0
+    logits[1, 2] = logits[1, E - 1] = logits[1].max() + 1.0   # a tie at the top: lower id first
+    logits[2, :] = 0.5                                          # all equal
+    logits[0, 3] = -0.0
+    logits[0, 4] = 0.0                                          # total order: +0.0 above -0.0
     ids, wts, counts, gtok, a2g = pf.moe_plan(logits.reshape(-1), T, E, K)
     ref = oracle.moe_plan(logits.reshape(-1), T, E, K)
+    np.testing.assert_array_equal(ids, total_order_topk(logits, K))
     np.testing.assert_array_equal(ids.reshape(-1), ref["topk_experts"])
-    np.testing.assert_allclose(wts.reshape(-1), ref["topk_weights"], rtol=1e-6, atol=0)
+    np.testing.assert_array_equal(wts.reshape(-1).view(np.uint32), ref["topk_weights"].view(np.uint32))
     np.testing.assert_array_equal(counts, np.diff(ref["expert_offsets"]))
     np.testing.assert_array_equal(gtok, ref["grouped_token_ids"])
     np.testing.assert_array_equal(a2g, ref["assignment_to_grouped"])
+    # the grouping is the stable sort of the assignments by expert
+    np.testing.assert_array_equal(np.argsort(np.argsort(ids.reshape(-1), kind="stable"), kind="stable"), a2g)
+
+
+def test_routing_plan_refusals(pf):
+    from omega_amd import OmegaGpuError
+
+    bad = np.zeros((4, 16), np.float32)
+    bad[2, 5] = np.nan
+    with pytest.raises(OmegaGpuError, match="token 2, expert 5"):
+        pf.moe_plan(bad, 4, 16, 4)
+    with pytest.raises(OmegaGpuError):
+        pf.moe_plan(np.zeros((4, 16), np.float32), 4, 16, 17)   # top_k > experts
 
 
 def test_host_rmsnorm_matches_the_oracle(pf, oracle):
