@@ -706,6 +706,92 @@ __global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
     paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
 }
 
+// ---------------------------------------------------------------- KV park / restore (extension)
+// The payload of positions start .. start + len (start a multiple of 16) is the HostPagedPoolV1
+// format of qwen3_moe_omega_kvio.rs:15-40: ceil(len / 16) blocks of [layer][K plane | V plane]
+// [token][kv head][dim] bf16, rows at or past len zero. The fused cache's pages have the same
+// strides with the V plane transposed per page ([kv head][dim][token]), so a K plane moves as it
+// is and a V plane goes through an LDS transpose. One workgroup per (block, layer). The reference
+// builds the payload row by row through cache_read (rows_to_blocks, :102-122).
+constexpr uint32_t kKvioPitch = 17;  // LDS words per (kv head, dim) row of 16 tokens
+
+struct KvioArgs {
+    uint8_t *pool = nullptr;     // the cache's first block of the range
+    uint8_t *payload = nullptr;  // the payload's first block of the range
+    uint64_t block_stride = 0, layer_stride = 0, plane_stride = 0;
+    uint32_t blk0 = 0;           // payload block of blockIdx.x = 0, relative to the payload start
+    uint32_t len = 0;            // positions in the whole payload
+};
+
+__global__ __launch_bounds__(256) void k_kv_export(const KvioArgs a) {
+    __shared__ uint32_t tile[512 * kKvioPitch];  // [kv head * 128 + dim][token], one bf16 per word
+    const uint32_t tid = threadIdx.x, blk = a.blk0 + blockIdx.x, layer = blockIdx.y;
+    const uint64_t off = (uint64_t)blockIdx.x * a.block_stride + (uint64_t)layer * a.layer_stride;
+    const uint8_t *src = a.pool + off;
+    uint8_t *dst = a.payload + off;
+    // K plane: 64 u32x4 per token row
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t i = tid + 256 * j, tok = i >> 6;
+        const u32x4 v = *as_global(src + 16 * (size_t)i);
+        *reinterpret_cast<u32x4 *>(dst + 16 * (size_t)i) = blk * 16 + tok < a.len ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+    // V^T plane word w: row r = w / 8 (kv head * 128 + dim), tokens 2 (w % 8) and + 1
+    const uint32_t *vs = reinterpret_cast<const uint32_t *>(src + a.plane_stride);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t w = tid + 256 * j, r = w >> 3, t = 2 * (w & 7);
+        const uint32_t v = *as_global_u32(vs + w);
+        tile[r * kKvioPitch + t] = v & 0xffffu;
+        tile[r * kKvioPitch + t + 1] = v >> 16;
+    }
+    __syncthreads();
+    // payload V plane word w: token t = w / 256, rows c = 2 (w % 256) and + 1
+    uint32_t *vd = reinterpret_cast<uint32_t *>(dst + a.plane_stride);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t w = tid + 256 * j, t = w >> 8, c = 2 * (w & 255);
+        const uint32_t v = tile[c * kKvioPitch + t] | (tile[(c + 1) * kKvioPitch + t] << 16);
+        vd[w] = blk * 16 + t < a.len ? v : 0u;
+    }
+}
+
+// the reverse: rows at or past len are not written (the cache keeps what it holds there)
+__global__ __launch_bounds__(256) void k_kv_import(const KvioArgs a) {
+    __shared__ uint32_t tile[512 * kKvioPitch];
+    const uint32_t tid = threadIdx.x, blk = a.blk0 + blockIdx.x, layer = blockIdx.y;
+    const uint64_t off = (uint64_t)blockIdx.x * a.block_stride + (uint64_t)layer * a.layer_stride;
+    const uint8_t *src = a.payload + off;
+    uint8_t *dst = a.pool + off;
+    const uint32_t valid = a.len - blk * 16 < 16 ? a.len - blk * 16 : 16;  // tokens of this block
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t i = tid + 256 * j, tok = i >> 6;
+        const u32x4 v = *as_global(src + 16 * (size_t)i);
+        if (tok < valid) *reinterpret_cast<u32x4 *>(dst + 16 * (size_t)i) = v;
+    }
+    const uint32_t *vs = reinterpret_cast<const uint32_t *>(src + a.plane_stride);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t w = tid + 256 * j, t = w >> 8, c = 2 * (w & 255);
+        const uint32_t v = *as_global_u32(vs + w);
+        tile[c * kKvioPitch + t] = v & 0xffffu;
+        tile[(c + 1) * kKvioPitch + t] = v >> 16;
+    }
+    __syncthreads();
+    uint32_t *vd = reinterpret_cast<uint32_t *>(dst + a.plane_stride);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t w = tid + 256 * j, r = w >> 3, t = 2 * (w & 7);
+        const uint32_t v = tile[r * kKvioPitch + t] | (tile[r * kKvioPitch + t + 1] << 16);
+        if (t + 1 < valid) {
+            vd[w] = v;
+        } else if (t < valid) {  // the block's last valid token is the low half of this word
+            vd[w] = (v & 0xffffu) | (*as_global_u32(vd + w) & 0xffff0000u);
+        }
+    }
+}
+
 hipError_t launch_paged_items(const PagedItemsArgs &a, uint32_t runs, hipStream_t st) {
     OMEGA_LAUNCH(k_paged_items, dim3(runs), dim3(256), 0, st, a);
     return hipGetLastError();
@@ -1285,6 +1371,162 @@ int omega_gpu_decode_attn_cache_read(OmegaGpuDecodeAttnCache *c, uint32_t layer,
 }
 
 const char *omega_gpu_decode_attn_last_error(void) { return last_error(F_DATTN); }
+// ---------------------------------------------------------------- KV park / restore (extension)
+extern "C++" {
+static int kvio_check(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, const void *buf, uint64_t bytes,
+                      const char *what) {
+    if (!c || !buf) {
+        set_error(F_DATTN, "kv %s: NULL cache or buffer", what);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    if (len == 0 || start % 16 || start >= c->max_pos || len > c->max_pos - start) {
+        set_error(F_DATTN, "kv %s of positions %u + %u: start a multiple of 16, 1 <= len, inside max_pos %u", what,
+                  start, len, c->max_pos);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    const uint64_t want = (uint64_t)((len + 15) / 16) * c->g.block_stride;
+    if (bytes != want) {
+        set_error(F_DATTN, "kv %s payload of %llu bytes, %u positions need %llu", what, (unsigned long long)bytes, len,
+                  (unsigned long long)want);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    return OMEGA_GPU_OK;
+}
+
+// runs the blocks of [start, start + len) in chunks; per chunk `pre` (a copy in), the kernel, `post`
+// (a copy out), all on the library's stream
+template <class Pre, class Post>
+static int kvio_run(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, bool exporting, uint8_t *payload_dev,
+                    uint64_t chunk_blocks, uint64_t *ns, Pre pre, Post post) {
+    Ctx *cx = ctx(F_DATTN);
+    if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    const uint32_t nblk = (len + 15) / 16;
+    OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev0, cx->stream));
+    for (uint32_t b0 = 0; b0 < nblk; b0 += (uint32_t)chunk_blocks) {
+        const uint32_t nb = (uint32_t)std::min<uint64_t>(chunk_blocks, nblk - b0);
+        uint8_t *pd = payload_dev ? payload_dev + (uint64_t)b0 * c->g.block_stride : static_cast<uint8_t *>(cx->scratch);
+        OMEGA_HIP(F_DATTN, pre(cx->stream, b0, nb, pd));
+        KvioArgs a;
+        a.pool = c->pool + (uint64_t)(start / 16 + b0) * c->g.block_stride;
+        a.payload = pd;
+        a.block_stride = c->g.block_stride;
+        a.layer_stride = c->g.layer_stride;
+        a.plane_stride = c->g.plane_stride;
+        a.blk0 = b0;
+        a.len = len;
+        if (exporting)
+            OMEGA_LAUNCH(k_kv_export, dim3(nb, c->layers), dim3(256), 0, cx->stream, a);
+        else
+            OMEGA_LAUNCH(k_kv_import, dim3(nb, c->layers), dim3(256), 0, cx->stream, a);
+        OMEGA_HIP(F_DATTN, hipGetLastError());
+        OMEGA_HIP(F_DATTN, post(cx->stream, b0, nb, pd));
+    }
+    OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev1, cx->stream));
+    OMEGA_HIP(F_DATTN, hipEventSynchronize(cx->ev1));
+    float ms = 0.f;
+    OMEGA_HIP(F_DATTN, hipEventElapsedTime(&ms, cx->ev0, cx->ev1));
+    if (ns) *ns = (uint64_t)((double)ms * 1e6);
+    return OMEGA_GPU_OK;
+}
+
+static uint64_t kvio_chunk_blocks(const OmegaGpuDecodeAttnCache *c) {
+    const uint64_t by_size = (256ull << 20) / c->g.block_stride;  // 256 MiB of staging
+    return by_size ? by_size : 1;
+}
+
+static hipError_t kvio_none(hipStream_t, uint32_t, uint32_t, uint8_t *) { return hipSuccess; }
+}  // extern "C++"
+
+uint64_t omega_gpu_decode_attn_cache_payload_len(const OmegaGpuDecodeAttnCache *c, uint32_t len) {
+    return c ? (uint64_t)((len + 15) / 16) * c->g.block_stride : 0;
+}
+
+int omega_gpu_decode_attn_cache_export(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, void *out,
+                                       uint64_t out_bytes, uint64_t *ns) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_DATTN);
+    if (int rc = kvio_check(c, start, len, out, out_bytes, "export")) return rc;
+    Ctx *cx = ctx(F_DATTN);
+    if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    const uint64_t chunk = kvio_chunk_blocks(c);
+    if (!ensure_scratch(F_DATTN, cx, chunk * c->g.block_stride)) return OMEGA_GPU_CHIP_FAIL;
+    uint8_t *host = static_cast<uint8_t *>(out);
+    const uint64_t bs = c->g.block_stride;
+    return kvio_run(c, start, len, true, nullptr, chunk, ns, kvio_none,
+                    [&](hipStream_t st, uint32_t b0, uint32_t nb, uint8_t *pd) {
+                        return hipMemcpyAsync(host + (uint64_t)b0 * bs, pd, (uint64_t)nb * bs, hipMemcpyDeviceToHost,
+                                              st);
+                    });
+}
+
+int omega_gpu_decode_attn_cache_export_dev(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, void *out_dev,
+                                           uint64_t out_bytes, uint64_t *ns) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_DATTN);
+    if (int rc = kvio_check(c, start, len, out_dev, out_bytes, "export")) return rc;
+    return kvio_run(c, start, len, true, static_cast<uint8_t *>(out_dev), (len + 15) / 16, ns, kvio_none,
+                    kvio_none);
+}
+
+// the padding rows of the last block (positions len .. 16 ceil(len / 16) - 1 of every layer's K
+// and V plane) must be zero (check_payload, qwen3_moe_omega_kvio.rs:162-186)
+static bool kvio_padding_is_zero(const OmegaGpuDecodeAttnCache *c, uint32_t len, const uint8_t *bytes) {
+    const uint32_t tail = len % 16;
+    if (!tail) return true;
+    const uint8_t *last = bytes + (uint64_t)(len / 16) * c->g.block_stride;
+    for (uint32_t l = 0; l < c->layers; ++l)
+        for (uint32_t v = 0; v < 2; ++v) {
+            const uint8_t *pl = last + (uint64_t)l * c->g.layer_stride + v * c->g.plane_stride;
+            for (uint64_t i = (uint64_t)tail * c->g.token_stride; i < c->g.plane_stride; ++i)
+                if (pl[i]) return false;
+        }
+    return true;
+}
+
+int omega_gpu_decode_attn_cache_import(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, const void *bytes,
+                                       uint64_t nbytes, uint64_t *ns) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_DATTN);
+    if (int rc = kvio_check(c, start, len, bytes, nbytes, "import")) return rc;
+    const uint8_t *host = static_cast<const uint8_t *>(bytes);
+    if (!kvio_padding_is_zero(c, len, host)) {
+        set_error(F_DATTN, "kv import: padding rows past position %u are not zero", len);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    Ctx *cx = ctx(F_DATTN);
+    if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    const uint64_t chunk = kvio_chunk_blocks(c);
+    if (!ensure_scratch(F_DATTN, cx, chunk * c->g.block_stride)) return OMEGA_GPU_CHIP_FAIL;
+    const uint64_t bs = c->g.block_stride;
+    return kvio_run(
+        c, start, len, false, nullptr, chunk, ns,
+        [&](hipStream_t st, uint32_t b0, uint32_t nb, uint8_t *pd) {
+            return hipMemcpyAsync(pd, host + (uint64_t)b0 * bs, (uint64_t)nb * bs, hipMemcpyHostToDevice, st);
+        },
+        kvio_none);
+}
+
+int omega_gpu_decode_attn_cache_import_dev(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len,
+                                           const void *bytes_dev, uint64_t nbytes, uint64_t *ns) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_DATTN);
+    if (int rc = kvio_check(c, start, len, bytes_dev, nbytes, "import")) return rc;
+    // the padding rows come to the host first (at most layers x 2 x 15 KiB)
+    const uint32_t tail = len % 16;
+    if (tail) {
+        std::vector<uint8_t> last(c->g.block_stride);
+        OMEGA_HIP(F_DATTN, hipMemcpy(last.data(), static_cast<const uint8_t *>(bytes_dev) +
+                                                      (uint64_t)(len / 16) * c->g.block_stride,
+                                     c->g.block_stride, hipMemcpyDeviceToHost));
+        if (!kvio_padding_is_zero(c, tail, last.data())) {
+            set_error(F_DATTN, "kv import: padding rows past position %u are not zero", len);
+            return OMEGA_GPU_BAD_ARGS;
+        }
+    }
+    return kvio_run(c, start, len, false, static_cast<uint8_t *>(const_cast<void *>(bytes_dev)), (len + 15) / 16, ns,
+                    kvio_none, kvio_none);
+}
+
 // The prefill attention of m tokens on the fused cache (both entries): qkv_dev [m][5120] and
 // out_dev [m][4096] device rows. Sub-batches of at most 1024 tokens bound the scratch; each runs
 // the preparation (K / V of its tokens appended), the page items and their combine.

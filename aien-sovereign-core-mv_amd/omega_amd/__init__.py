@@ -167,6 +167,11 @@ SIGNATURES = {
     "omega_gpu_decode_attn_test_set_mutant": (None, [i32]),
     "omega_gpu_decode_attn_cache_write": (i32, [P, u32, u32, u32, u32, P, P]),
     "omega_gpu_decode_attn_cache_read": (i32, [P, u32, u32, u32, P, P]),
+    "omega_gpu_decode_attn_cache_payload_len": (u64, [P, u32]),
+    "omega_gpu_decode_attn_cache_export": (i32, [P, u32, u32, P, u64, P]),
+    "omega_gpu_decode_attn_cache_export_dev": (i32, [P, u32, u32, P, u64, P]),
+    "omega_gpu_decode_attn_cache_import": (i32, [P, u32, u32, P, u64, P]),
+    "omega_gpu_decode_attn_cache_import_dev": (i32, [P, u32, u32, P, u64, P]),
     # bf16 (crates/aien-omega-bf16/src/lib.rs:70-101)
     "omega_gpu_bf16_tensor_upload": (i32, [u32, u32, P, C.POINTER(P)]),
     "omega_gpu_bf16_tensor_free": (None, [P]),
@@ -555,6 +560,40 @@ class DecodeAttnCache:
         _check(lib().omega_gpu_decode_attn_cache_write(self.h, layer, kv_head, pos,
                                                        k.size // HEAD_DIM, ptr(k), ptr(v)),
                "decode_attn")
+
+    def payload_len(self, length):
+        """bytes of the HostPagedPoolV1 payload of `length` positions"""
+        return int(lib().omega_gpu_decode_attn_cache_payload_len(self.h, length))
+
+    def export_kv(self, start, length):
+        """the HostPagedPoolV1 payload of positions start .. start + length (qwen3_moe_omega_kvio.rs
+        rows_to_blocks) as a uint8 array; returns (payload, chip ns)"""
+        out = np.empty(self.payload_len(length), np.uint8)
+        ns = C.c_uint64()
+        _check(lib().omega_gpu_decode_attn_cache_export(self.h, start, length, out.ctypes.data, out.nbytes,
+                                                        C.addressof(ns)), "decode_attn")
+        return out, ns.value
+
+    def export_kv_dev(self, start, length, out_dev, nbytes):
+        ns = C.c_uint64()
+        _check(lib().omega_gpu_decode_attn_cache_export_dev(self.h, start, length, out_dev, nbytes,
+                                                            C.addressof(ns)), "decode_attn")
+        return ns.value
+
+    def import_kv(self, start, length, payload):
+        """writes positions start .. start + length from a HostPagedPoolV1 payload (blocks_to_rows);
+        a payload of the wrong size or with non-zero padding rows is refused before any write"""
+        b = np.ascontiguousarray(payload, np.uint8)
+        ns = C.c_uint64()
+        _check(lib().omega_gpu_decode_attn_cache_import(self.h, start, length, b.ctypes.data, b.nbytes,
+                                                        C.addressof(ns)), "decode_attn")
+        return ns.value
+
+    def import_kv_dev(self, start, length, bytes_dev, nbytes):
+        ns = C.c_uint64()
+        _check(lib().omega_gpu_decode_attn_cache_import_dev(self.h, start, length, bytes_dev, nbytes,
+                                                            C.addressof(ns)), "decode_attn")
+        return ns.value
 
     def as_raw(self):
         return self.h

@@ -302,6 +302,47 @@ def bench_prefill(om, args):
         t.free()
 
 
+def bench_kvio(om, args):
+    """KV park / restore of the fused 48-layer cache (the HostPagedPoolV1 payload of
+    qwen3_moe_omega_kvio.rs): export and import of --kvio-positions positions between the cache
+    and a device payload buffer (both resident in HBM; each moves the payload's bytes in and out),
+    then one export and one import through pageable host memory (the PCIe-inclusive rate)."""
+    n = args.kvio_positions
+    cache = om.DecodeAttnCache(L, om.round_max_pos(n), 1e6)
+    nbytes = cache.payload_len(n)
+    buf = om.DeviceBuffer(nbytes)
+    for _ in range(2):
+        cache.export_kv_dev(0, n, buf.ptr, nbytes)
+        cache.import_kv_dev(0, n, buf.ptr, nbytes)
+    ex = [cache.export_kv_dev(0, n, buf.ptr, nbytes) for _ in range(args.kvio_reps)]
+    im = [cache.import_kv_dev(0, n, buf.ptr, nbytes) for _ in range(args.kvio_reps)]
+    t0 = time.perf_counter()
+    host, _ = cache.export_kv(0, n)
+    t_host_ex = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    cache.import_kv(0, n, host)
+    t_host_im = time.perf_counter() - t0
+    ex_us, im_us = np.mean(ex) / 1e3, np.mean(im) / 1e3
+    moved = 2 * nbytes  # payload bytes read and written
+    gbs = moved / (ex_us * 1e3)
+    print(json.dumps({
+        "metric": "KV park / restore of the fused cache (HostPagedPoolV1 payload), achieved HBM GB/s vs peak",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "bf16 bytes (moved, not converted)",
+        "data": "an allocated 48-layer fused cache (contents as allocated)",
+        "config": {"workload": f"export / import of {n} positions x 48 layers x 4 kv heads x 128 dims",
+                   "payload_bytes": nbytes},
+        "roofline": {"bound": "hbm", "kernel": "k_kv_export", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None},
+        "export_us": round(ex_us, 1), "import_us": round(im_us, 1),
+        "import_GBs": round(moved / (im_us * 1e3), 1),
+        "host_export_s": round(t_host_ex, 3), "host_import_s": round(t_host_im, 3),
+        "host_export_GBs": round(nbytes / t_host_ex / 1e9, 2), "host_import_GBs": round(nbytes / t_host_im / 1e9, 2),
+        "reps": args.kvio_reps}), flush=True)
+    buf.free()
+    cache.free()
+
+
 # ---------------------------------------------------------------- configuration 3: paged attention
 PAGED_POINTS = [(b, l) for b in (1, 8, 32) for l in (2048, 8192, 32768)]
 
@@ -652,19 +693,23 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill", "kvio"],
+                    default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
                          "gemv: the q|k|v FP8 GEMV (configuration 1); prefill: whole-prompt prefill "
                          "time to first token; "
                          "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
                          "at token batch 1 and 32 (configuration 2); serve: 32 sequences of batched "
-                         "decode over long contexts (configuration 5)")
+                         "decode over long contexts (configuration 5); kvio: KV park / restore of a "
+                         "fused cache in the HostPagedPoolV1 payload")
     ap.add_argument("--serve-steps", type=int, default=128)
     ap.add_argument("--serve-warmup", type=int, default=4)
     ap.add_argument("--paged-reps", type=int, default=10)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--gemv-reps", type=int, default=200)
     ap.add_argument("--prefill-lengths", default="512,2048")
+    ap.add_argument("--kvio-positions", type=int, default=32768)
+    ap.add_argument("--kvio-reps", type=int, default=10)
     ap.add_argument("--prefill-decode-ms", type=float, default=0.0,
                     help="bs=1 decode step time, for the token-by-token prompt time beside the prefill")
     ap.add_argument("--no-bs32", action="store_true",
@@ -691,6 +736,9 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(om, args)
+        return
+    if args.workload == "kvio":
+        bench_kvio(om, args)
         return
     if args.workload == "paged":
         bench_paged(om, args)

@@ -553,6 +553,25 @@ int omega_gpu_prefill_attn_dev(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint3
 int omega_gpu_pf_moe_plan(uint32_t tokens, uint32_t experts, uint32_t top_k, const float *logits, uint32_t *topk_ids,
                           float *topk_weights, uint32_t *counts, uint32_t *grouped_token,
                           uint32_t *assignment_to_grouped, uint32_t *grouped_to_assignment);
+/* Persistent KV park / restore of the fused decode cache (not in the reference ABI: the reference
+ * builds the HostPagedPoolV1 payload row by row through omega_gpu_decode_attn_cache_read /
+ * _write, qwen3_moe_omega_kvio.rs:102-160). The payload of positions start .. start + len (start
+ * a multiple of 16, start + len <= max_pos) is ceil(len / 16) blocks of [layer][K | V][token]
+ * [kv head][dim] bf16 (qwen3_moe_omega_kvio.rs:17-24), rows at or past len zero; payload_len gives
+ * its size, and a buffer of any other size is refused. Export writes the payload (host memory,
+ * or device memory for _dev); import refuses a payload whose padding rows are not zero before
+ * writing anything, then writes positions start .. start + len - 1 only. Synchronous; *ns (may
+ * be NULL) is the call's chip time including the copies. */
+uint64_t omega_gpu_decode_attn_cache_payload_len(const OmegaGpuDecodeAttnCache *c, uint32_t len);
+int omega_gpu_decode_attn_cache_export(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, void *out,
+                                       uint64_t out_bytes, uint64_t *ns);
+int omega_gpu_decode_attn_cache_export_dev(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, void *out_dev,
+                                           uint64_t out_bytes, uint64_t *ns);
+int omega_gpu_decode_attn_cache_import(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len, const void *bytes,
+                                       uint64_t nbytes, uint64_t *ns);
+int omega_gpu_decode_attn_cache_import_dev(OmegaGpuDecodeAttnCache *c, uint32_t start, uint32_t len,
+                                           const void *bytes_dev, uint64_t nbytes, uint64_t *ns);
+
 /* The whole-prompt driver's residual and RMSNorm on the device (not in the reference ABI, whose
  * driver does both on the host, qwen3_moe_omega_prefill.rs:590-660): per row of k, x += add when
  * add_va is not 0 (in place), then out = x * scale * w, scale = 1 / sqrt(mean(x^2) + eps) with

@@ -320,6 +320,111 @@ def fnv1a64(b: bytes | np.ndarray) -> int:
     return int(lib().oref_fnv1a64(ptr(arr), arr.size))
 
 
+# ------------------------------------------------------------------ KV park / restore payload
+class PoolBlockGeometry:
+    """One HostPagedPoolV1 block for bf16 elements (qwen3_moe_omega_kvio.rs:42-100): per block
+    [layer][K plane | V plane][token][kv head][dim]."""
+
+    def __init__(self, layers: int, kv_heads: int, head_dim: int, block_size: int):
+        self.layers, self.kv_heads, self.head_dim, self.block_size = layers, kv_heads, head_dim, block_size
+
+    @property
+    def head_stride(self):
+        return self.head_dim * 2
+
+    @property
+    def token_stride(self):
+        return self.kv_heads * self.head_stride
+
+    @property
+    def kv_plane_stride(self):
+        return self.block_size * self.token_stride
+
+    @property
+    def layer_stride(self):
+        return 2 * self.kv_plane_stride
+
+    @property
+    def block_stride(self):
+        return self.layers * self.layer_stride
+
+    def payload_len(self, length: int) -> int:
+        return -(-length // self.block_size) * self.block_stride
+
+    def row_offset(self, rel: int, layer: int, value: bool, head: int) -> int:
+        return ((rel // self.block_size) * self.block_stride + layer * self.layer_stride
+                + int(value) * self.kv_plane_stride + (rel % self.block_size) * self.token_stride
+                + head * self.head_stride)
+
+    def check(self, start: int, length: int):
+        if min(self.layers, self.kv_heads, self.head_dim, self.block_size) == 0:
+            raise ValueError("kv export geometry has a zero dimension")
+        if length == 0:
+            raise ValueError("kv export of zero positions")
+        if start % self.block_size:
+            raise ValueError(f"kv export start {start} is not a multiple of the block size")
+
+
+def kv_rows_to_blocks(g: PoolBlockGeometry, start: int, length: int, read_row) -> np.ndarray:
+    """rows_to_blocks (qwen3_moe_omega_kvio.rs:102-122): read_row(layer, head, pos) -> (k, v) of
+    head_dim uint16 each, placed little-endian at row_offset; the rest of the payload is zero."""
+    g.check(start, length)
+    out = np.zeros(g.payload_len(length), np.uint8)
+    for layer in range(g.layers):
+        for head in range(g.kv_heads):
+            for rel in range(length):
+                k, v = read_row(layer, head, start + rel)
+                for value, row in ((False, k), (True, v)):
+                    at = g.row_offset(rel, layer, value, head)
+                    out[at:at + 2 * g.head_dim] = np.asarray(row, "<u2").view(np.uint8)
+    return out
+
+
+def kv_check_payload(g: PoolBlockGeometry, length: int, payload) -> None:
+    """check_payload (qwen3_moe_omega_kvio.rs:162-186): exact size, zero padding rows."""
+    b = np.asarray(payload, np.uint8)
+    if b.size != g.payload_len(length):
+        raise ValueError(f"kv payload of {b.size} bytes, {length} positions need {g.payload_len(length)}")
+    tail = length % g.block_size
+    if tail:
+        last = length - tail
+        for layer in range(g.layers):
+            for value in (False, True):
+                lo = g.row_offset(last + tail, layer, value, 0)
+                hi = g.row_offset(last, layer, value, 0) + g.kv_plane_stride
+                if b[lo:hi].any():
+                    raise ValueError(f"kv payload: padding rows past position {length} of layer {layer} are not zero")
+
+
+def kv_blocks_to_rows(g: PoolBlockGeometry, start: int, length: int, payload, write_rows) -> None:
+    """blocks_to_rows (qwen3_moe_omega_kvio.rs:124-160): refuses a damaged payload before any
+    write, then write_rows(layer, head, k_rows, v_rows) with [length][head_dim] uint16 each."""
+    g.check(start, length)
+    kv_check_payload(g, length, payload)
+    b = np.asarray(payload, np.uint8)
+    for layer in range(g.layers):
+        for head in range(g.kv_heads):
+            k = np.empty((length, g.head_dim), np.uint16)
+            v = np.empty((length, g.head_dim), np.uint16)
+            for rel in range(length):
+                for value, dst in ((False, k), (True, v)):
+                    at = g.row_offset(rel, layer, value, head)
+                    dst[rel] = b[at:at + 2 * g.head_dim].view("<u2")
+            write_rows(layer, head, k, v)
+
+
+def kv_zero_padding(g: PoolBlockGeometry, length: int, payload: np.ndarray) -> None:
+    """zero_padding (qwen3_moe_omega_kvio.rs:188-202), in place"""
+    tail = length % g.block_size
+    if not tail:
+        return
+    last = length - tail
+    for layer in range(g.layers):
+        for value in (False, True):
+            payload[g.row_offset(last + tail, layer, value, 0):
+                    g.row_offset(last, layer, value, 0) + g.kv_plane_stride] = 0
+
+
 class Dattn:
     """The fused decode-attention cache oracle (bf16 rows, f64 attention)."""
 
