@@ -302,6 +302,73 @@ def bench_prefill(om, args):
         t.free()
 
 
+def bench_schedule(om, args):
+    """The beat scheduler (omega_amd.serve) over the batched step of the full 48-layer model: 32
+    slots, --schedule-requests requests arriving two per beat from beat 0 (each waits while every
+    slot is taken), prompts of 32..512 seeded tokens fed one per beat, 128 greedy tokens each.
+    Reports generated tokens / s, all fed tokens / s and the time to first token in beats."""
+    from omega_amd import serve
+
+    slots, new, nreq = SERVE_SEQS, 128, args.schedule_requests
+    rng = np.random.default_rng(SEED + 5)
+    prompts = [rng.integers(0, V, int(n)).tolist() for n in rng.integers(32, 513, nreq)]
+    max_blocks = -(-(512 + new) // 16)
+    blocks = slots * max_blocks
+    lay = om.kv_layout(blocks, 16, L, KVH, HD)
+    pool = om.DeviceBuffer(lay.pool_bytes)
+    router = om.Router(L)
+    ones = np.ones(H, np.float32)
+    layers = []
+    for l in range(L):
+        qkv = om.Fp8Tensor.synth(1, 5120, 2048, SEED, tid(l, 0))
+        o = om.Fp8Tensor.synth(1, 2048, 4096, SEED, tid(l, 1))
+        gu = om.Fp8Tensor.synth(E, 1536, 2048, SEED, tid(l, 2))
+        dn = om.Fp8Tensor.synth(E, 2048, 768, SEED, tid(l, 3))
+        layers.append((qkv, o, gu, dn))
+        router.set_layer(l, om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02), ones)
+        router.set_directory(l, np.zeros(2 * E, np.uint64), np.zeros(2 * E, np.uint64))
+    lm = om.Bf16Tensor.synth(V, H, SEED, 2, 0.02)
+    embed = om.Bf16Tensor.synth(V, H, SEED, 1, 0.02)
+    bd = om.BatchDecode(L, V, slots, max_blocks, max_blocks * 16, 1e-6, 1e6, router, lm, embed, pool.ptr, lay)
+    hd1 = np.ones(HD, np.float32)
+    for l, (qkv, o, gu, dn) in enumerate(layers):
+        bd.set_layer(l, qkv, o, gu, dn, ones, hd1, hd1)
+    bd.set_final_norm(ones)
+    serve.BeatScheduler(bd, blocks, max_blocks, slots=slots).run({0: [("warm", prompts[0][:8], 4, ())]})
+    om.sync()
+    arrivals = {}
+    for i, p in enumerate(prompts):
+        arrivals.setdefault(i // 2, []).append((i, p, new, ()))
+    sch = serve.BeatScheduler(bd, blocks, max_blocks, slots=slots)
+    t0 = time.perf_counter()
+    done = sch.run(arrivals)
+    om.sync()
+    elapsed = time.perf_counter() - t0
+    gen = sum(len(r.tokens) for r in done.values())
+    ttft = np.array([r.first_token_beat - r.joined_beat for r in done.values()])
+    wait = np.array([r.joined_beat - i // 2 for i, r in done.items()])
+    print(json.dumps({
+        "metric": "Qwen3-30B-A3B FP8 serving mode (beat scheduler over the batched step): generated tok/s",
+        "value": round(gen / elapsed, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+        "dtype": "fp8", "data": "synthetic random-init weights, seeded prompts",
+        "config": {"workload": f"{nreq} requests, 2 arriving per beat, prompts 32..512 tokens fed one per beat, "
+                               f"{new} greedy tokens each, {slots} slots",
+                   "slots": slots},
+        "beats": sch.beats, "ms_per_beat": round(elapsed * 1e3 / sch.beats, 3),
+        "fed_tok_s": round(sch.fed_tokens / elapsed, 1), "generated": gen, "elapsed_s": round(elapsed, 2),
+        "mean_rows_per_beat": round(sch.fed_tokens / sch.beats, 2),
+        "first_token_beats_mean": round(float(ttft.mean()), 1), "wait_beats_mean": round(float(wait.mean()), 1)}),
+        flush=True)
+    bd.free()
+    for t in layers:
+        for x in t:
+            x.free()
+    router.free()
+    lm.free()
+    embed.free()
+    pool.free()
+
+
 def bench_kvio(om, args):
     """KV park / restore of the fused 48-layer cache (the HostPagedPoolV1 payload of
     qwen3_moe_omega_kvio.rs): export and import of --kvio-positions positions between the cache
@@ -693,7 +760,7 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill", "kvio"],
+    ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill", "kvio", "schedule"],
                     default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
                          "gemv: the q|k|v FP8 GEMV (configuration 1); prefill: whole-prompt prefill "
@@ -701,7 +768,8 @@ def main():
                          "paged: the paged-attention sweep (configuration 3); moe: the MoE block "
                          "at token batch 1 and 32 (configuration 2); serve: 32 sequences of batched "
                          "decode over long contexts (configuration 5); kvio: KV park / restore of a "
-                         "fused cache in the HostPagedPoolV1 payload")
+                         "fused cache in the HostPagedPoolV1 payload; schedule: the beat scheduler "
+                         "serving staggered requests over the batched step")
     ap.add_argument("--serve-steps", type=int, default=128)
     ap.add_argument("--serve-warmup", type=int, default=4)
     ap.add_argument("--paged-reps", type=int, default=10)
@@ -709,6 +777,7 @@ def main():
     ap.add_argument("--gemv-reps", type=int, default=200)
     ap.add_argument("--prefill-lengths", default="512,2048")
     ap.add_argument("--kvio-positions", type=int, default=32768)
+    ap.add_argument("--schedule-requests", type=int, default=96)
     ap.add_argument("--kvio-reps", type=int, default=10)
     ap.add_argument("--prefill-decode-ms", type=float, default=0.0,
                     help="bs=1 decode step time, for the token-by-token prompt time beside the prefill")
@@ -739,6 +808,9 @@ def main():
         return
     if args.workload == "kvio":
         bench_kvio(om, args)
+        return
+    if args.workload == "schedule":
+        bench_schedule(om, args)
         return
     if args.workload == "paged":
         bench_paged(om, args)
