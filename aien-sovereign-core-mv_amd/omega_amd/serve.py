@@ -16,11 +16,16 @@ tokens are the tokens that request gets alone.
 """
 from __future__ import annotations
 
+import ctypes as C
 from collections import deque
 
 import numpy as np
 
 from . import OmegaGpuError
+
+
+def _addr(p):
+    return (p.value or 0) if isinstance(p, C.c_void_p) else int(p)
 
 
 class SchedulerBusy(OmegaGpuError):
@@ -48,12 +53,47 @@ class Request:
         return self.finish is not None
 
 
+class PromptPrefill:
+    """Prompts that go in whole instead of one token per beat. Positions 0 .. n - 2 of a joining
+    request run through the whole-prompt prefill `wp` (omega_amd.prefill.WholePromptPrefill) into
+    its fused decode cache, leave that cache as the HostPagedPoolV1 payload
+    (omega_gpu_decode_attn_cache_export_dev), whose blocks are the pool's pages byte for byte, and
+    are copied into the request's pages; the last prompt token then goes through the batched step,
+    which gives the first generated token. The prompt's K / V are the prefill's (W8A8) rows, as
+    with the reference engine's whole-prompt mode."""
+
+    def __init__(self, wp, cache, pool_ptr, max_positions, min_tokens=16):
+        from . import DeviceBuffer
+
+        self.wp, self.cache, self.pool_ptr, self.min_tokens = wp, cache, _addr(pool_ptr), min_tokens
+        self.block_bytes = cache.payload_len(16)
+        self.payload = DeviceBuffer(cache.payload_len(max_positions))
+        self.max_positions = max_positions
+
+    def fill(self, tokens, pages):
+        from .prefill import copy_va
+
+        n = len(tokens)
+        if n > self.max_positions:
+            raise OmegaGpuError(-1, f"schedule prefill of {n} tokens > {self.max_positions}")
+        self.wp.run(tokens, 0)
+        nbytes = self.cache.payload_len(n)
+        self.cache.export_kv_dev(0, n, self.payload.ptr, nbytes)
+        base = _addr(self.payload.ptr)
+        for j in range(nbytes // self.block_bytes):
+            copy_va(self.pool_ptr + pages[j] * self.block_bytes, base + j * self.block_bytes, self.block_bytes)
+
+    def free(self):
+        self.payload.free()
+
+
 class BeatScheduler:
     """The beat loop over a BatchDecode whose KV pool has `num_blocks` pages of `block_size`
     tokens and whose tables hold `max_blocks` pages per row."""
 
-    def __init__(self, bd, num_blocks, max_blocks, block_size=16, slots=None):
+    def __init__(self, bd, num_blocks, max_blocks, block_size=16, slots=None, prefill: PromptPrefill | None = None):
         self.bd = bd
+        self.prefill = prefill
         self.block_size = block_size
         self.max_blocks = max_blocks
         self.slots = min(int(bd.cfg.max_seqs), int(slots or bd.cfg.max_seqs))
@@ -102,6 +142,9 @@ class BeatScheduler:
         while self.pending:
             r = self.pending.popleft()
             r.joined_beat = self.beats
+            if self.prefill and len(r.prompt) - 1 >= self.prefill.min_tokens:
+                self.prefill.fill(r.prompt[:-1], r.pages)
+                r.fed = len(r.prompt) - 1
             self.live.append(r)
         for r in [r for r in self.live if r.cancelled]:
             self._leave(r, "cancelled")

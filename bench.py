@@ -306,7 +306,9 @@ def bench_schedule(om, args):
     """The beat scheduler (omega_amd.serve) over the batched step of the full 48-layer model: 32
     slots, --schedule-requests requests arriving two per beat from beat 0 (each waits while every
     slot is taken), prompts of 32..512 seeded tokens fed one per beat, 128 greedy tokens each.
-    Reports generated tokens / s, all fed tokens / s and the time to first token in beats."""
+    With --schedule-prefill a joining prompt goes in whole (the whole-prompt prefill into a fused
+    cache, then its payload blocks into the request's pages). Reports generated tokens / s, all
+    fed tokens / s and the time to first token in beats."""
     from omega_amd import serve
 
     slots, new, nreq = SERVE_SEQS, 128, args.schedule_requests
@@ -334,12 +336,28 @@ def bench_schedule(om, args):
     for l, (qkv, o, gu, dn) in enumerate(layers):
         bd.set_layer(l, qkv, o, gu, dn, ones, hd1, hd1)
     bd.set_final_norm(ones)
-    serve.BeatScheduler(bd, blocks, max_blocks, slots=slots).run({0: [("warm", prompts[0][:8], 4, ())]})
+    pp = fused = wp = None
+    if args.schedule_prefill:
+        from omega_amd import prefill as pf
+
+        fused = om.DecodeAttnCache(L, om.round_max_pos(512), 1e6)
+        for l in range(L):
+            fused.set_norms(l, hd1, hd1)
+        embed_host = om.synth_bf16_host(SEED, 1, (V, H), 0.02)
+        wp = pf.WholePromptPrefill(
+            [dict(qkv=q, o=o, gate_up=g, down=d, input_norm=ones, post_norm=ones,
+                  router=(om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02).astype(np.uint32) << 16).view(np.float32))
+             for l, (q, o, g, d) in enumerate(layers)],
+            ones, lambda t: (embed_host[t].astype(np.uint32) << 16).view(np.float32), fused, 1e-6)
+        pp = serve.PromptPrefill(wp, fused, pool.ptr, 512)
+        wp.run(prompts[0], 0)  # buffers sized for the longest prompt
+    serve.BeatScheduler(bd, blocks, max_blocks, slots=slots, prefill=pp).run(
+        {0: [("warm", prompts[0][:40], 4, ())]})
     om.sync()
     arrivals = {}
     for i, p in enumerate(prompts):
         arrivals.setdefault(i // 2, []).append((i, p, new, ()))
-    sch = serve.BeatScheduler(bd, blocks, max_blocks, slots=slots)
+    sch = serve.BeatScheduler(bd, blocks, max_blocks, slots=slots, prefill=pp)
     t0 = time.perf_counter()
     done = sch.run(arrivals)
     om.sync()
@@ -351,14 +369,19 @@ def bench_schedule(om, args):
         "metric": "Qwen3-30B-A3B FP8 serving mode (beat scheduler over the batched step): generated tok/s",
         "value": round(gen / elapsed, 1), "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
         "dtype": "fp8", "data": "synthetic random-init weights, seeded prompts",
-        "config": {"workload": f"{nreq} requests, 2 arriving per beat, prompts 32..512 tokens fed one per beat, "
-                               f"{new} greedy tokens each, {slots} slots",
+        "config": {"workload": f"{nreq} requests, 2 arriving per beat, prompts 32..512 tokens "
+                               + ("through the whole-prompt prefill at join" if pp else "fed one per beat")
+                               + f", {new} greedy tokens each, {slots} slots",
                    "slots": slots},
         "beats": sch.beats, "ms_per_beat": round(elapsed * 1e3 / sch.beats, 3),
         "fed_tok_s": round(sch.fed_tokens / elapsed, 1), "generated": gen, "elapsed_s": round(elapsed, 2),
         "mean_rows_per_beat": round(sch.fed_tokens / sch.beats, 2),
         "first_token_beats_mean": round(float(ttft.mean()), 1), "wait_beats_mean": round(float(wait.mean()), 1)}),
         flush=True)
+    if pp:
+        pp.free()
+        wp.free()
+        fused.free()
     bd.free()
     for t in layers:
         for x in t:
@@ -778,6 +801,8 @@ def main():
     ap.add_argument("--prefill-lengths", default="512,2048")
     ap.add_argument("--kvio-positions", type=int, default=32768)
     ap.add_argument("--schedule-requests", type=int, default=96)
+    ap.add_argument("--schedule-prefill", action="store_true",
+                    help="schedule: prompts go in through the whole-prompt prefill at join")
     ap.add_argument("--kvio-reps", type=int, default=10)
     ap.add_argument("--prefill-decode-ms", type=float, default=0.0,
                     help="bs=1 decode step time, for the token-by-token prompt time beside the prefill")

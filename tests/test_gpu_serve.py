@@ -82,3 +82,51 @@ def test_stop_cancel_and_refusals(omega, served):
         sch.beat()
     assert b.finish == "length" and len(b.tokens) == 20
     assert len(sch.free_pages) == BLOCKS
+
+
+@pytest.fixture(scope="module")
+def prefill_join(omega, oracle, served):
+    from omega_amd import prefill as pf
+    from omega_amd import serve
+    m, bm = served
+    c = m.cfg
+    layers = [dict(qkv=q, o=o, gate_up=g, down=d, input_norm=m.tensor(l, 5), post_norm=m.tensor(l, 6),
+                   router=oracle.bf16_to_f32(m.tensor(l, 4))) for l, (q, o, g, d) in enumerate(bm.tensors)]
+    cache = omega.DecodeAttnCache(c.layers, 256, c.rope_theta)
+    for l in range(c.layers):
+        cache.set_norms(l, m.tensor(l, 7), m.tensor(l, 8))
+    emb = m.embed()
+    wp = pf.WholePromptPrefill(layers, m.final_norm(), lambda t: oracle.bf16_to_f32(emb[t]), cache, c.eps)
+    pp = serve.PromptPrefill(wp, cache, bm.pool.ptr, 128, min_tokens=4)
+    yield pp
+    pp.free()
+    wp.free()
+    cache.free()
+
+
+def test_whole_prompt_joins(omega, oracle, served, prefill_join):
+    from omega_amd import serve
+    m, bm = served
+    rng = np.random.default_rng(12)
+    reqs = {k: (list(rng.integers(0, 8192, n)), new) for k, (n, new) in
+            {"a": (37, 6), "b": (3, 8), "c": (20, 5), "d": (64, 4)}.items()}   # "b" is fed per beat
+    arrivals = {0: [("a", *reqs["a"], ()), ("b", *reqs["b"], ())], 3: [("c", *reqs["c"], ()), ("d", *reqs["d"], ())]}
+    got = serve.BeatScheduler(bm.bd, BLOCKS, MAX_BLOCKS, slots=4, prefill=prefill_join).run(arrivals)
+    for k, (prompt, new) in reqs.items():
+        r = got[k]
+        assert r.finish == "length" and len(r.tokens) == new
+        solo = serve.BeatScheduler(bm.bd, BLOCKS, MAX_BLOCKS, slots=1, prefill=prefill_join).run(
+            {0: [(k, prompt, new, ())]})[k]
+        assert solo.tokens == r.tokens, k
+    # the pages of a whole-prompt join hold the fused cache's rows byte for byte
+    prompt = reqs["d"][0]
+    sch = serve.BeatScheduler(bm.bd, BLOCKS, MAX_BLOCKS, slots=1, prefill=prefill_join)
+    r = sch.submit(prompt, 4)
+    sch.beat()                                        # the join runs the prefill, then one step
+    want, _ = prefill_join.cache.export_kv(0, len(prompt) - 1)
+    bb = prefill_join.block_bytes
+    pool = bm.pool.download(np.uint8, BLOCKS * bb)
+    for j in range(len(want) // bb - 1):              # whole pages (the last one now holds the step's row)
+        np.testing.assert_array_equal(pool[r.pages[j] * bb:(r.pages[j] + 1) * bb], want[j * bb:(j + 1) * bb])
+    while sch.live:
+        sch.beat()
