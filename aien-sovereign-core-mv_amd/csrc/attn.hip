@@ -1750,6 +1750,34 @@ static int check_layout(const OmegaGpuKvLayout *l, uint32_t layer, uint32_t kvh)
     return OMEGA_GPU_ATTN_OK;
 }
 
+// The buffers of one host-buffer paged call: device scratch q | out | table | lens | partials |
+// staged pages, pinned q | table | lens | staged pages (the output comes back through q).
+struct PagedCallBytes {
+    size_t o_q, o_out, o_tab, o_len, o_part, o_stage, need;
+    size_t p_tab, p_len, p_stage, pin_need;
+};
+static PagedCallBytes paged_call_bytes(uint32_t seqs, uint32_t max_blocks, uint32_t max_ctx, uint32_t qh, uint32_t kvh,
+                                       uint32_t block_size, uint64_t staged) {
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t qf = (size_t)seqs * qh * 128, tab_bytes = (size_t)seqs * max_blocks * 4;
+    uint32_t unit = kAttnTile;
+    const uint32_t splits = paged_splits(max_ctx, seqs, kvh, paged_mfma(qh, kvh, block_size), unit);
+    const size_t part_bytes = (size_t)seqs * qh * splits * kPartStride * 4;
+    PagedCallBytes b;
+    b.o_q = 0;
+    b.o_out = al(qf * 4);
+    b.o_tab = b.o_out + al(qf * 4);
+    b.o_len = b.o_tab + al(tab_bytes);
+    b.o_part = b.o_len + al((size_t)seqs * 4);
+    b.o_stage = b.o_part + al(part_bytes);
+    b.need = b.o_stage + al(staged);
+    b.p_tab = al(qf * 4);
+    b.p_len = b.p_tab + al(tab_bytes);
+    b.p_stage = b.p_len + al((size_t)seqs * 4);
+    b.pin_need = b.p_stage + al(staged);
+    return b;
+}
+
 // Batched paged attention from host buffers. Device pools are read in place; other pools have
 // the layer slice of every referenced page staged into device memory first.
 static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout *layout,
@@ -1813,18 +1841,22 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
         g.layer_stride = 0;
         lay = 0;
     }
+    const ServingState &sv = serving();
+    if (sv.reserved && (seqs > sv.bounds.max_seqs || max_ctx > sv.bounds.max_context || qh != sv.bounds.num_q_heads ||
+                        kvh != sv.bounds.num_kv_heads || layout->block_size != sv.bounds.kv_block_size)) {
+        set_error(F_ATTN, "serving reservation exceeded: %u sequences, context %u, %u/%u heads, block %u against "
+                  "the bounds %u, %u, %u/%u, %u", seqs, max_ctx, qh, kvh, layout->block_size, sv.bounds.max_seqs,
+                  sv.bounds.max_context, sv.bounds.num_q_heads, sv.bounds.num_kv_heads, sv.bounds.kv_block_size);
+        return OMEGA_GPU_ATTN_TOO_LARGE;
+    }
     uint32_t unit = kAttnTile;
     const uint32_t splits = paged_splits(max_ctx, seqs, kvh, paged_mfma(qh, kvh, layout->block_size), unit);
-    const size_t part_bytes = (size_t)seqs * qh * splits * kPartStride * 4;
-    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    // device scratch: q | out | table | lens | partials | staged pages
-    const size_t o_q = 0, o_out = al(qf * 4), o_tab = o_out + al(qf * 4);
-    const size_t o_len = o_tab + al(tab_bytes), o_part = o_len + al((size_t)seqs * 4);
-    const size_t o_stage = o_part + al(part_bytes), need = o_stage + al(staged);
-    // pinned: q | table | lens | staged pages (the output comes back through the q area)
-    const size_t p_tab = al(qf * 4), p_len = p_tab + al(tab_bytes), p_stage = p_len + al((size_t)seqs * 4);
-    if (!ensure_scratch(F_ATTN, cx, need)) return OMEGA_GPU_ATTN_CHIP_FAIL;
-    if (!ensure_pinned(F_ATTN, cx, p_stage + al(staged))) return OMEGA_GPU_ATTN_CHIP_FAIL;
+    const PagedCallBytes pb = paged_call_bytes(seqs, max_blocks, max_ctx, qh, kvh, layout->block_size, staged);
+    const size_t o_q = pb.o_q, o_out = pb.o_out, o_tab = pb.o_tab, o_len = pb.o_len, o_part = pb.o_part,
+                 o_stage = pb.o_stage;
+    const size_t p_tab = pb.p_tab, p_len = pb.p_len, p_stage = pb.p_stage;
+    if (!ensure_scratch(F_ATTN, cx, pb.need)) return OMEGA_GPU_ATTN_CHIP_FAIL;
+    if (!ensure_pinned(F_ATTN, cx, pb.pin_need)) return OMEGA_GPU_ATTN_CHIP_FAIL;
     uint8_t *d = static_cast<uint8_t *>(cx->scratch);
     uint8_t *pin = static_cast<uint8_t *>(cx->pin);
     float *qd = reinterpret_cast<float *>(d + o_q);
@@ -2075,5 +2107,58 @@ const char *omega_gpu_attention_rc_name(int rc) {
     return rc == -5 ? "UNWRITTEN" : rc_name(rc);
 }
 const char *omega_gpu_attention_last_error(void) { return last_error(F_ATTN); }
+
+// ---------------------------------------------------------------- serving reservation
+// omega_gpu_reserve_serving (aien-omega-gpu/src/lib.rs:1129-1160): the bounds a daemon declares at
+// start-up. The host-buffer paged attention's device scratch and pinned staging are sized now for
+// the largest call inside them (max_seqs sequences of max_context tokens, every page staged from
+// a host pool), all before the call returns; afterwards a paged call past the bounds is refused
+// with TOO_LARGE. _seal makes every later growth of the library's scratch or staging a refusal;
+// _release lifts both. The counters of omega_gpu_session_alloc_stats cover those allocations.
+int omega_gpu_reserve_serving(const OmegaGpuServingBounds *b) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_MATMUL);
+    if (!b || b->max_context == 0 || b->max_seqs == 0 || b->head_dim != 128 || b->kv_block_size == 0 ||
+        (b->kv_block_size & (b->kv_block_size - 1)) || b->kernel_slots > 128 || b->num_kv_heads == 0 ||
+        b->num_q_heads % b->num_kv_heads || b->num_q_heads / b->num_kv_heads > 16) {
+        set_error(F_MATMUL, "serving bounds refused: context and sequences >= 1, head_dim 128, a power-of-two "
+                  "block size, q heads a multiple (<= 16) of kv heads, at most 128 kernel slots");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    Ctx *cx = ctx(F_ATTN);
+    if (!cx) {
+        set_error(F_MATMUL, "serving reservation: %s", last_error(F_ATTN));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    const uint32_t bs = b->kv_block_size, max_blocks = (b->max_context + bs - 1) / bs;
+    const uint64_t slice = 2ull * bs * b->num_kv_heads * 256;  // a page's K and V of one layer
+    const uint64_t staged = (uint64_t)b->max_seqs * max_blocks * slice;
+    const PagedCallBytes pb = paged_call_bytes(b->max_seqs, max_blocks, b->max_context, b->num_q_heads,
+                                               b->num_kv_heads, bs, staged);
+    serving().sealed = false;
+    if (!ensure_scratch(F_ATTN, cx, pb.need) || !ensure_pinned(F_ATTN, cx, pb.pin_need)) {
+        set_error(F_MATMUL, "serving reservation of %zu + %zu bytes: %s", pb.need, pb.pin_need, last_error(F_ATTN));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    serving().bounds = *b;
+    serving().reserved = true;
+    return OMEGA_GPU_OK;
+}
+
+void omega_gpu_serving_seal(void) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    serving().sealed = true;
+}
+
+void omega_gpu_serving_release(void) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    serving().sealed = false;
+    serving().reserved = false;
+}
+
+void omega_gpu_session_alloc_stats(OmegaGpuAllocStats *out) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    if (out) *out = alloc_counters();
+}
 
 }  // extern "C"

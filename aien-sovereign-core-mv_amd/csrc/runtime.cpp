@@ -79,35 +79,66 @@ Ctx *ctx(Family f) {
     return &g_ctx;
 }
 
+ServingState &serving() {
+    static ServingState s;
+    return s;
+}
+
+OmegaGpuAllocStats &alloc_counters() {
+    static OmegaGpuAllocStats s{};
+    return s;
+}
+
+static bool sealed_refusal(Family f, const char *what, size_t bytes, size_t held) {
+    if (!serving().sealed) return false;
+    ++alloc_counters().stale_refusals;
+    set_error(f, "serving reservation exceeded: %s of %zu bytes requested after the seal (%zu held)", what,
+              bytes, held);
+    return true;
+}
+
 bool ensure_pinned(Family f, Ctx *c, size_t bytes) {
     if (c->pin_bytes >= bytes) return true;
-    if (c->pin) (void)hipHostFree(c->pin);
+    if (sealed_refusal(f, "pinned staging", bytes, c->pin_bytes)) return false;
+    if (c->pin) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipHostFree(c->pin);
+        ++alloc_counters().frees;
+    }
     c->pin = nullptr;
     c->pin_bytes = 0;
     size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
     hipError_t e = hipHostMalloc(&c->pin, want, hipHostMallocDefault);
     if (e != hipSuccess) {
+        ++alloc_counters().alloc_failures;
         set_error(f, "pinned staging of %zu bytes: %s", want, hipGetErrorString(e));
         return false;
     }
+    ++alloc_counters().allocs;
+    alloc_counters().alloc_bytes += want;
     c->pin_bytes = want;
     return true;
 }
 
 bool ensure_scratch(Family f, Ctx *c, size_t bytes) {
     if (c->scratch_bytes >= bytes) return true;
+    if (sealed_refusal(f, "device scratch", bytes, c->scratch_bytes)) return false;
     if (c->scratch) {
         (void)hipStreamSynchronize(c->stream);
         (void)hipFree(c->scratch);
+        ++alloc_counters().frees;
     }
     c->scratch = nullptr;
     c->scratch_bytes = 0;
     size_t want = bytes < (4u << 20) ? (4u << 20) : bytes;
     hipError_t e = hipMalloc(&c->scratch, want);
     if (e != hipSuccess) {
+        ++alloc_counters().alloc_failures;
         set_error(f, "device scratch of %zu bytes: %s", want, hipGetErrorString(e));
         return false;
     }
+    ++alloc_counters().allocs;
+    alloc_counters().alloc_bytes += want;
     c->scratch_bytes = want;
     return true;
 }

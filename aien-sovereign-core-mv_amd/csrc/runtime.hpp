@@ -48,6 +48,16 @@ Ctx *ctx(Family f);
 bool ensure_pinned(Family f, Ctx *c, size_t bytes);
 bool ensure_scratch(Family f, Ctx *c, size_t bytes);
 
+// The serving reservation (omega_gpu_reserve_serving / _seal / _release): while sealed, the grow
+// helpers above refuse to allocate (counted as stale refusals); the counters cover every
+// allocation they make.
+struct ServingState {
+    bool reserved = false, sealed = false;
+    OmegaGpuServingBounds bounds{};
+};
+ServingState &serving();
+OmegaGpuAllocStats &alloc_counters();
+
 // HIP call check: on failure sets the family error and returns CHIP_FAIL from the caller.
 #define OMEGA_HIP(fam, call)                                                                    \
     do {                                                                                        \

@@ -1,6 +1,6 @@
 // The base-ABI entries of crates/aien-omega-gpu/abi/omega_gpu.manifest that sit outside the
 // FP8 decode step (the bf16 dense matmul family, the elementwise kernels, the dense f32 GQA
-// attention and the serving reservation). They exist so the archive defines every manifest
+// attention). They exist so the archive defines every manifest
 // symbol (crates/aien-abi-conformance/src/build.rs:261-300 links against the full list); each
 // answers BAD_ARGS with an explanation, touches no device and allocates nothing.
 #include <cstring>
@@ -18,7 +18,6 @@ int refuse(Family f) {
     return OMEGA_GPU_BAD_ARGS;
 }
 uint32_t g_cta_budget = OMEGA_GPU_MATMUL_MAX_CTAS;
-OmegaGpuAllocStats g_stats;
 }  // namespace
 
 extern "C" {
@@ -61,16 +60,7 @@ void omega_gpu_matmul_set_cta_budget(uint32_t ctas) {
     g_cta_budget = ctas == 0 ? OMEGA_GPU_MATMUL_MAX_CTAS : ctas;
 }
 uint32_t omega_gpu_matmul_cta_budget(void) { return g_cta_budget; }
-int omega_gpu_reserve_serving(const OmegaGpuServingBounds *b) {
-    if (!b) return refuse(F_MATMUL);
-    return OMEGA_GPU_OK;  // kernels are compiled ahead of time; buffers grow on demand
-}
-void omega_gpu_serving_release(void) {}
 int omega_gpu_matmul_prepare(uint32_t, uint32_t, uint32_t) { return refuse(F_MATMUL); }
-void omega_gpu_serving_seal(void) {}
-void omega_gpu_session_alloc_stats(OmegaGpuAllocStats *out) {
-    if (out) *out = g_stats;
-}
 
 int omega_gpu_rmsnorm_f32(uint32_t, uint32_t, const float *, const float *, float, float *,
                           OmegaGpuEwInfo *) {

@@ -114,6 +114,18 @@ class BatchDecodeConfig(C.Structure):
                 ("layout", KvLayout)]
 
 
+class ServingBounds(C.Structure):
+    """OmegaGpuServingBounds (include/omega_gpu.h), 44 bytes."""
+    _fields_ = [(n, C.c_uint32) for n in ("max_context", "max_seqs", "num_q_heads", "num_kv_heads", "head_dim",
+                                          "kv_block_size", "max_rows", "max_k", "max_n", "max_n_one_row",
+                                          "kernel_slots")]
+
+
+class AllocStats(C.Structure):
+    """OmegaGpuAllocStats (include/omega_gpu.h), 40 bytes."""
+    _fields_ = [(n, C.c_uint64) for n in ("allocs", "alloc_bytes", "alloc_failures", "frees", "stale_refusals")]
+
+
 P = C.c_void_p
 U8P, U16P, U32P, U64P, F32P = (C.POINTER(C.c_uint8), C.POINTER(C.c_uint16),
                                 C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
@@ -194,6 +206,11 @@ SIGNATURES = {
     "omega_gpu_decode_graph_stamps": (i32, [P, U64P, U8P, u32]),
     "omega_gpu_decode_graph_kind_name": (cstr, [C.c_uint8]),
     "omega_gpu_session_last_error": (cstr, []),
+    "omega_gpu_reserve_serving": (i32, [C.POINTER(ServingBounds)]),
+    "omega_gpu_matmul_last_error": (cstr, []),
+    "omega_gpu_serving_seal": (None, []),
+    "omega_gpu_serving_release": (None, []),
+    "omega_gpu_session_alloc_stats": (None, [C.POINTER(AllocStats)]),
     # base ABI (crates/aien-omega-gpu/src/ffi.rs)
     "omega_gpu_session_set_spin_us": (i32, [u32]),
     "omega_gpu_session_spin_us": (u32, []),
@@ -803,6 +820,28 @@ def hip():
         h.hipEventDestroy.argtypes = [P]
         _hip = h
     return _hip
+
+
+def reserve_serving(**bounds):
+    """omega_gpu_reserve_serving (aien-omega-gpu/src/lib.rs:1129-1160) with the named bounds"""
+    b = ServingBounds(**bounds)
+    rc = lib().omega_gpu_reserve_serving(C.byref(b))
+    if rc:
+        raise OmegaGpuError(rc, _s(lib().omega_gpu_matmul_last_error()))
+
+
+def serving_seal():
+    lib().omega_gpu_serving_seal()
+
+
+def serving_release():
+    lib().omega_gpu_serving_release()
+
+
+def alloc_stats():
+    s = AllocStats()
+    lib().omega_gpu_session_alloc_stats(C.byref(s))
+    return {n: getattr(s, n) for n, _ in AllocStats._fields_}
 
 
 class DeviceBuffer:

@@ -91,6 +91,14 @@ def test_host_checks_refuse_before_touching_the_device():
     assert lib.omega_gpu_decode_graph_create(C.byref(cfg), C.byref(out)) == -1
     assert out.value is None
     assert "layers" in om._s(lib.omega_gpu_session_last_error())
+    # serving bounds are checked before the device is opened (head_dim 64, a block of 12)
+    for bad in (dict(head_dim=64), dict(kv_block_size=12), dict(max_seqs=0), dict(kernel_slots=129)):
+        kw = dict(max_context=640, max_seqs=4, num_q_heads=32, num_kv_heads=4, head_dim=128, kv_block_size=16,
+                  max_rows=1, max_k=2048, max_n=2048, max_n_one_row=0, kernel_slots=8)
+        kw.update(bad)
+        with pytest.raises(om.OmegaGpuError, match="serving bounds refused"):
+            om.reserve_serving(**kw)
+    assert C.sizeof(om.ServingBounds) == 44 and C.sizeof(om.AllocStats) == 40
     # NULL handles
     assert lib.omega_gpu_fp8_tensor_entry(None, 0, None, None) == -1
 

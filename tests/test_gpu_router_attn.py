@@ -317,3 +317,51 @@ def test_bf16_lm_head_gemv(omega, oracle):
     t.free()
     td.free()
     t2.free()
+
+
+def test_serving_reservation_bounds_seal_and_counters(omega, oracle):
+    # omega_gpu_reserve_serving sizes the host-buffer paged call's buffers for its bounds; calls
+    # inside them allocate nothing more, a call past them is refused (TOO_LARGE), the seal refuses
+    # any later growth of the library's buffers (a stale refusal), and release lifts both
+    rng = np.random.default_rng(31)
+    layers, nb = 2, 200
+    lay, pool = _paged_pool(oracle, rng, nb, layers)
+    L = _omega_layout(omega, lay)
+    lib = omega.lib()
+
+    def call(seqs, ctx):
+        lens = np.full(seqs, ctx, np.int32)
+        maxb = (ctx + 15) // 16
+        tabs = np.stack([rng.permutation(nb)[:maxb] for _ in range(seqs)]).astype(np.int32)
+        q = rng.standard_normal(seqs * 32 * 128).astype(np.float32)
+        out = np.zeros_like(q)
+        info = omega.AttnInfo()
+        rc = lib.omega_gpu_paged_attention_batch_bf16(omega.ptr(q), omega.ptr(pool), C.byref(L), omega.ptr(tabs),
+                                                      omega.ptr(lens), maxb, seqs, 1, 32, 4, 128, omega.ptr(out),
+                                                      C.byref(info))
+        return rc, omega._s(lib.omega_gpu_attention_last_error())
+
+    with pytest.raises(omega.OmegaGpuError):
+        omega.reserve_serving(max_context=640, max_seqs=4, num_q_heads=32, num_kv_heads=4, head_dim=64,
+                              kv_block_size=16, max_rows=1, max_k=2048, max_n=2048, max_n_one_row=0, kernel_slots=8)
+    try:
+        omega.reserve_serving(max_context=640, max_seqs=4, num_q_heads=32, num_kv_heads=4, head_dim=128,
+                              kv_block_size=16, max_rows=1, max_k=2048, max_n=2048, max_n_one_row=0, kernel_slots=8)
+        s0 = omega.alloc_stats()
+        assert call(4, 640)[0] == 0 and call(2, 100)[0] == 0
+        assert omega.alloc_stats()["allocs"] == s0["allocs"]     # inside the bounds: nothing allocated
+        rc, err = call(5, 64)
+        assert rc == -2 and "reservation exceeded" in err          # past max_seqs
+        assert call(1, 641 + 15)[0] == -2                          # past max_context
+        omega.serving_seal()
+        assert call(3, 600)[0] == 0
+        cache = omega.DecodeAttnCache(2, 16384, 1e6)               # growth of another family's scratch
+        try:
+            with pytest.raises(omega.OmegaGpuError, match="reservation exceeded"):
+                cache.export_kv(0, 16384)
+        finally:
+            cache.free()
+        assert omega.alloc_stats()["stale_refusals"] == s0["stale_refusals"] + 1
+    finally:
+        omega.serving_release()
+    assert call(5, 64)[0] == 0                                     # released: bounds and seal lifted
