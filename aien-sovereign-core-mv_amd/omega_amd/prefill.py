@@ -274,8 +274,12 @@ class WholePromptPrefill:
         self.layers = []
         for L in layers:
             gu, dn = L["gate_up"], L["down"]
-            ent = dict(qkv=L["qkv"].entry(0), o=L["o"].entry(0),
-                       gu=[gu.entry(x) for x in range(experts)], dn=[dn.entry(x) for x in range(experts)])
+            gue = [gu.entry(x) for x in range(experts)]
+            dne = [dn.entry(x) for x in range(experts)]
+            ent = dict(qkv=(np.array([L["qkv"].entry(0)[0]], np.uint64), np.array([L["qkv"].entry(0)[1]], np.uint64)),
+                       o=(np.array([L["o"].entry(0)[0]], np.uint64), np.array([L["o"].entry(0)[1]], np.uint64)),
+                       gu=(np.array([v[0] for v in gue], np.uint64), np.array([v[1] for v in gue], np.uint64)),
+                       dn=(np.array([v[0] for v in dne], np.uint64), np.array([v[1] for v in dne], np.uint64)))
             wq = pack_router(np.asarray(L["router"], np.float32))
             wq_dev = PfMem(wq.nbytes)
             host = PfMem(wq.nbytes, host=True)
@@ -338,13 +342,17 @@ class WholePromptPrefill:
         copy_va(self.bufs["stage"].va, src.va, nb)
         return self.bufs["stage"].host(dtype)[:count].copy()
 
-    def _put_tiles(self, b, region, w, s, counts):
-        tab = build_tiles(self.bm, w, s, counts)
-        if len(tab) > b["max_tiles"]:
-            raise OmegaGpuError(-1, f"tile table of {len(tab)} entries > region of {b['max_tiles']}")
+    def _put_tiles(self, b, region, ws, counts):
+        """the tile table of (weights, scales) addresses `ws` over `counts` rows per expert, built
+        by the library's builder straight into the pinned table region"""
+        w, sc = ws
+        c = np.ascontiguousarray(counts, np.uint32)
         off = region * b["max_tiles"] * TILE_BYTES
-        b["tiles"].host(np.uint8)[off:off + tab.nbytes] = tab.view(np.uint8)
-        return b["tiles"].va + off, len(tab)
+        n = lib().omega_gpu_pf_qgemm_tiles_va(len(c), w.ctypes.data, sc.ctypes.data, c.ctypes.data,
+                                              b["tiles"].host(np.uint8)[off:].ctypes.data, b["max_tiles"])
+        if n == 0:
+            raise OmegaGpuError(-1, f"tile table larger than its region of {b['max_tiles']} entries")
+        return b["tiles"].va + off, n
 
     def run(self, tokens, pos0, trace=None):
         """Tokens at positions pos0 .. pos0 + m - 1 through every layer; returns the last token's
@@ -367,7 +375,7 @@ class WholePromptPrefill:
             if trace is not None and l > 0:
                 trace.setdefault("x_out", []).append(self._down(b["x"], np.float32, m * h).reshape(m, h))
             chip += quant(h, IN_F32, m, b["xin"].va, b["xq"].va, b["xs"].va)
-            tv, nt = self._put_tiles(b, 0, [ent["qkv"][0]], [ent["qkv"][1]], dense)
+            tv, nt = self._put_tiles(b, 0, ent["qkv"], dense)
             chip += qgemm(qkv_n, h, PLAIN, tv, nt, 0, b["xq"].va, b["xs"].va, b["qkv"].va)
             info = self.attn.attend_dev(l, pos0, m, b["qkv"].va, eps, 1.0, b["att"].va)
             chip += info.elapsed_ns
@@ -375,7 +383,7 @@ class WholePromptPrefill:
                 trace.setdefault("qkv", []).append(self._down(b["qkv"], np.float32, m * qkv_n).reshape(m, qkv_n))
                 trace.setdefault("att", []).append(self._down(b["att"], np.float32, m * qd).reshape(m, qd))
             chip += quant(qd, IN_F32, m, b["att"].va, b["xq"].va, b["xs"].va)
-            tv, nt = self._put_tiles(b, 1, [ent["o"][0]], [ent["o"][1]], dense)
+            tv, nt = self._put_tiles(b, 1, ent["o"], dense)
             chip += qgemm(h, qd, PLAIN, tv, nt, 0, b["xq"].va, b["xs"].va, b["oproj"].va)
             # x += o_proj, then the post-norm rows: the quantiser's and the router's input
             chip += residual_norm(h, m, b["x"].va, b["oproj"].va, L["post_norm"].va, eps, b["xin"].va)
@@ -391,14 +399,10 @@ class WholePromptPrefill:
                 trace.setdefault("logits", []).append(logits.reshape(m, e).copy())
             chip += quant(h, IN_F32, m, b["xin"].va, b["xq"].va, b["xs"].va)
             self._up(b["rowidx"], grouped_token)
-            gw = [ent["gu"][x_][0] for x_ in range(e)]
-            gs = [ent["gu"][x_][1] for x_ in range(e)]
-            tv, nt = self._put_tiles(b, 2, gw, gs, counts)
+            tv, nt = self._put_tiles(b, 2, ent["gu"], counts)
             chip += qgemm(2 * i, h, SWIGLU_NAT, tv, nt, b["rowidx"].va, b["xq"].va, b["xs"].va, b["act"].va)
             chip += quant(i, IN_BF16, g, b["act"].va, b["aq"].va, b["a_s"].va)
-            dw = [ent["dn"][x_][0] for x_ in range(e)]
-            ds = [ent["dn"][x_][1] for x_ in range(e)]
-            tv, nt = self._put_tiles(b, 2, dw, ds, counts)
+            tv, nt = self._put_tiles(b, 2, ent["dn"], counts)
             chip += qgemm(h, i, PLAIN, tv, nt, 0, b["aq"].va, b["a_s"].va, b["down"].va)
             self._up(b["inv"], a2g)
             self._up(b["wts"], wts.reshape(-1))
