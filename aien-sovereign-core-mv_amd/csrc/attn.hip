@@ -736,23 +736,36 @@ __global__ __launch_bounds__(256) void k_kv_export(const KvioArgs a) {
         const u32x4 v = *as_global(src + 16 * (size_t)i);
         *reinterpret_cast<u32x4 *>(dst + 16 * (size_t)i) = blk * 16 + tok < a.len ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    // V^T plane word w: row r = w / 8 (kv head * 128 + dim), tokens 2 (w % 8) and + 1
-    const uint32_t *vs = reinterpret_cast<const uint32_t *>(src + a.plane_stride);
+    // V^T plane: 16 bytes x4 per thread; word w holds row r = w / 8 (kv head * 128 + dim),
+    // tokens 2 (w % 8) and + 1, so a thread's four words are tokens t0 .. t0 + 7 of one row
+    const uint8_t *vs = src + a.plane_stride;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t w = tid + 256 * j, r = w >> 3, t = 2 * (w & 7);
-        const uint32_t v = *as_global_u32(vs + w);
-        tile[r * kKvioPitch + t] = v & 0xffffu;
-        tile[r * kKvioPitch + t + 1] = v >> 16;
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t q = tid + 256 * j, r = q >> 1, t0 = 8 * (q & 1);
+        const u32x4 v = *as_global(vs + 16 * (size_t)q);
+        uint32_t *tr = tile + r * kKvioPitch + t0;
+        tr[0] = v.x & 0xffffu;
+        tr[1] = v.x >> 16;
+        tr[2] = v.y & 0xffffu;
+        tr[3] = v.y >> 16;
+        tr[4] = v.z & 0xffffu;
+        tr[5] = v.z >> 16;
+        tr[6] = v.w & 0xffffu;
+        tr[7] = v.w >> 16;
     }
     __syncthreads();
-    // payload V plane word w: token t = w / 256, rows c = 2 (w % 256) and + 1
-    uint32_t *vd = reinterpret_cast<uint32_t *>(dst + a.plane_stride);
+    // payload V plane: token t = q / 64, rows c = 8 (q % 64) .. + 7 per 16-byte store
+    uint8_t *vd = dst + a.plane_stride;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t w = tid + 256 * j, t = w >> 8, c = 2 * (w & 255);
-        const uint32_t v = tile[c * kKvioPitch + t] | (tile[(c + 1) * kKvioPitch + t] << 16);
-        vd[w] = blk * 16 + t < a.len ? v : 0u;
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t q = tid + 256 * j, t = q >> 6, c = 8 * (q & 63);
+        const uint32_t *tc = tile + c * kKvioPitch + t;
+        u32x4 v;
+        v.x = tc[0] | (tc[kKvioPitch] << 16);
+        v.y = tc[2 * kKvioPitch] | (tc[3 * kKvioPitch] << 16);
+        v.z = tc[4 * kKvioPitch] | (tc[5 * kKvioPitch] << 16);
+        v.w = tc[6 * kKvioPitch] | (tc[7 * kKvioPitch] << 16);
+        *reinterpret_cast<u32x4 *>(vd + 16 * (size_t)q) = blk * 16 + t < a.len ? v : u32x4{0u, 0u, 0u, 0u};
     }
 }
 
@@ -770,24 +783,42 @@ __global__ __launch_bounds__(256) void k_kv_import(const KvioArgs a) {
         const u32x4 v = *as_global(src + 16 * (size_t)i);
         if (tok < valid) *reinterpret_cast<u32x4 *>(dst + 16 * (size_t)i) = v;
     }
-    const uint32_t *vs = reinterpret_cast<const uint32_t *>(src + a.plane_stride);
+    const uint8_t *vs = src + a.plane_stride;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t w = tid + 256 * j, t = w >> 8, c = 2 * (w & 255);
-        const uint32_t v = *as_global_u32(vs + w);
-        tile[c * kKvioPitch + t] = v & 0xffffu;
-        tile[(c + 1) * kKvioPitch + t] = v >> 16;
+    for (int j = 0; j < 4; ++j) {  // payload token t = q / 64, rows c = 8 (q % 64) .. + 7
+        const uint32_t q = tid + 256 * j, t = q >> 6, c = 8 * (q & 63);
+        const u32x4 v = *as_global(vs + 16 * (size_t)q);
+        uint32_t *tc = tile + c * kKvioPitch + t;
+        tc[0] = v.x & 0xffffu;
+        tc[kKvioPitch] = v.x >> 16;
+        tc[2 * kKvioPitch] = v.y & 0xffffu;
+        tc[3 * kKvioPitch] = v.y >> 16;
+        tc[4 * kKvioPitch] = v.z & 0xffffu;
+        tc[5 * kKvioPitch] = v.z >> 16;
+        tc[6 * kKvioPitch] = v.w & 0xffffu;
+        tc[7 * kKvioPitch] = v.w >> 16;
     }
     __syncthreads();
-    uint32_t *vd = reinterpret_cast<uint32_t *>(dst + a.plane_stride);
+    uint8_t *vd = dst + a.plane_stride;
+    if (valid == 16) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t w = tid + 256 * j, r = w >> 3, t = 2 * (w & 7);
-        const uint32_t v = tile[r * kKvioPitch + t] | (tile[r * kKvioPitch + t + 1] << 16);
-        if (t + 1 < valid) {
-            vd[w] = v;
-        } else if (t < valid) {  // the block's last valid token is the low half of this word
-            vd[w] = (v & 0xffffu) | (*as_global_u32(vd + w) & 0xffff0000u);
+        for (int j = 0; j < 4; ++j) {  // V^T row r = q / 2, tokens 8 (q % 2) .. + 7
+            const uint32_t q = tid + 256 * j, r = q >> 1, t0 = 8 * (q & 1);
+            const uint32_t *tr = tile + r * kKvioPitch + t0;
+            *reinterpret_cast<u32x4 *>(vd + 16 * (size_t)q) =
+                u32x4{tr[0] | (tr[1] << 16), tr[2] | (tr[3] << 16), tr[4] | (tr[5] << 16), tr[6] | (tr[7] << 16)};
+        }
+    } else {
+        uint32_t *vw = reinterpret_cast<uint32_t *>(vd);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t w = tid + 256 * j, r = w >> 3, t = 2 * (w & 7);
+            const uint32_t v = tile[r * kKvioPitch + t] | (tile[r * kKvioPitch + t + 1] << 16);
+            if (t + 1 < valid) {
+                vw[w] = v;
+            } else if (t < valid) {  // the block's last valid token is the low half of this word
+                vw[w] = (v & 0xffffu) | (*as_global_u32(vw + w) & 0xffff0000u);
+            }
         }
     }
 }
