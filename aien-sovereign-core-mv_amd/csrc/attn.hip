@@ -65,7 +65,9 @@ __device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint3
 // One online-softmax step over a page whose first token is tok0 (< pos). The online state of
 // head n % 8 (m, l) sits in every lane of column n; O[nb][i] is row 4 g + i (head (4 g + i) % 8,
 // hi half for g < 2, lo half otherwise), dim 16 nb + n.
-template <bool FIRST>  // FIRST: no earlier page, so the running state starts here (nothing to rescale)
+// GUARD: the page may hold no valid token for a running state that has seen none either (the
+// prefill's query tiles), so a maximum of -inf is replaced by 0 as the exponent's reference.
+template <bool FIRST, bool GUARD = false>  // FIRST: no earlier page (the running state starts here)
 __device__ __forceinline__ void dattn_page(const DattnPage &T, const bf16x8 (&qop)[4], uint32_t tok0,
                                            uint32_t pos, uint32_t g, uint32_t n, float &m_l, float &l_l,
                                            f32x4 (&O)[8]) {
@@ -81,19 +83,20 @@ __device__ __forceinline__ void dattn_page(const DattnPage &T, const bf16x8 (&qo
     }
     // max and sum over the four lane groups (rows) of a column: row swaps, no LDS
     const float mx = xor_max<32>(xor_max<16>(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))));
-    const float m_new = FIRST ? mx : fmaxf(m_l, mx);  // finite: token tok0 is valid
+    const float m_new = FIRST ? mx : fmaxf(m_l, mx);  // finite unless GUARD: token tok0 is valid
+    const float m_ref = GUARD && m_new == -INFINITY ? 0.f : m_new;
     float pr[4];
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        pr[i] = expf(sc[i] - m_new);
+        pr[i] = expf(sc[i] - m_ref);
         psum += pr[i];
     }
     psum = xor_sum<32>(xor_sum<16>(psum));
     if (FIRST) {
         l_l = psum;
     } else {
-        const float alpha = expf(m_l - m_new);
+        const float alpha = expf(m_l - m_ref);
         l_l = l_l * alpha + psum;
         // accumulator row 4 g + i belongs to head (4 g + i) % 8: head i for even g, 4 + i for
         // odd g, whose alpha every row's lane (head) holds
@@ -630,7 +633,7 @@ struct PattnArgs {
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     float eps = 1e-6f;
     float *qn = nullptr;               // [m][32][128] prepared q
-    const uint32_t *items = nullptr;   // [items][2]: token, chunk
+    const uint32_t *items = nullptr;   // [items][4]: first token of the group, chunk, base, chunks
     float *part = nullptr;             // [items][32][kPartStride]
 };
 
@@ -673,18 +676,36 @@ __global__ __launch_bounds__(64) void k_pattn_prep(const PattnArgs a) {
     *reinterpret_cast<uint16_t *>(vplane + (lane + 64) * 32) = bf16_rne(v1);
 }
 
-// one wavefront per (item, kv head): item = (token t, chunk c), pages [c C, min(pages, (c + 1) C))
-// of positions 0 ..= pos0 + t; the two-set straight-path page loop of paged_pages over the fused
-// cache's pages (K rows token-major, V transposed per page: no staging)
+// one wavefront per (item, kv head): item = (group of TQ consecutive tokens t0 .., chunk c),
+// pages [c C, min(pages, (c + 1) C)) of the group's last token's context; each page is loaded
+// once and serves the group's tokens, token t0 + j masking the positions past its own context
+// pos0 + t0 + j + 1 (a token can see none of a chunk's pages: its state stays empty, m -inf and
+// l 0, and the combine gives it no weight). Item words: t0, c, the group's first partial slot
+// base and its chunk count nch; token j's partial of chunk c is slot base * TQ + j * nch + c, so
+// each token's partials are contiguous for the combine. The work per (page, token) is the same
+// either way (the matrix-core products and the softmax), so tiles pay only where the prefix is
+// long enough for the saved page reads to matter: TQ 4 for contexts of 1024 and more, else 1
+// (which keeps a wavefront per token for the parallelism of short prompts).
+constexpr uint32_t kPattnTqLong = 4, kPattnLongCtx = 1024;
+
+template <uint32_t TQ>
 __global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
-    __shared__ __align__(16) uint16_t qhl[2][8][128];
+    __shared__ __align__(16) uint16_t qhl[TQ][2][8][128];
     const uint32_t lane = threadIdx.x, h = blockIdx.x & 3, it = blockIdx.x >> 2;
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t t = a.items[2 * it], c = a.items[2 * it + 1];
-    const uint32_t ctx = a.pos0 + t + 1, pages = (ctx + 15) / 16;
+    const uint32_t *iw = a.items + 4 * (size_t)it;
+    const uint32_t t0 = iw[0], c = iw[1], base = iw[2], nch = iw[3];
+    const uint32_t valid = a.m - t0 < TQ ? a.m - t0 : TQ;  // tokens of this group
+    const uint32_t pages = (a.pos0 + t0 + valid + 15) / 16;
     const uint32_t p_begin = c * kPattnChunk, p_end = min(pages, p_begin + kPattnChunk), last = p_end - 1;
-    bf16x8 qop[4];
-    paged_q(a.qn + ((size_t)t * 32 + h * 8) * 128, lane, qhl, qop);
+    bf16x8 qop[TQ][4];
+    uint32_t ctx[TQ];
+#pragma unroll
+    for (uint32_t j = 0; j < TQ; ++j) {
+        const uint32_t tj = j < valid ? t0 + j : t0;  // a missing token repeats the first (never stored)
+        paged_q(a.qn + ((size_t)tj * 32 + h * 8) * 128, lane, qhl[j], qop[j]);
+        ctx[j] = j < valid ? a.pos0 + t0 + j + 1 : 0u;
+    }
     DattnArgs d;
     d.pool = a.pool;
     d.g = a.g;
@@ -692,18 +713,30 @@ __global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
     DattnPage A, B;
     dattn_load(d, h, p_begin, lane, A);
     dattn_load(d, h, min(p_begin + 1, last), lane, B);
-    float m_l = -INFINITY, l_l = 0.f;
-    f32x4 O[8];
+    float m_l[TQ], l_l[TQ];
+    f32x4 O[TQ][8];
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t j = 0; j < TQ; ++j) {
+        m_l[j] = -INFINITY;
+        l_l[j] = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) O[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     for (uint32_t p = p_begin; p < p_end; p += 2) {
-        const uint32_t ctx_b = p + 1 < p_end ? ctx : 0u;  // 0: the null page (every score -inf)
-        dattn_page<false>(A, qop, p * 16, ctx, g, n, m_l, l_l, O);
+        const bool has_b = p + 1 < p_end;  // else B is the null page (every score -inf)
+#pragma unroll
+        for (uint32_t j = 0; j < TQ; ++j) dattn_page<false, true>(A, qop[j], p * 16, ctx[j], g, n, m_l[j], l_l[j], O[j]);
         dattn_load(d, h, min(p + 2, last), lane, A);
-        dattn_page<false>(B, qop, (p + 1) * 16, ctx_b, g, n, m_l, l_l, O);
+#pragma unroll
+        for (uint32_t j = 0; j < TQ; ++j)
+            dattn_page<false, true>(B, qop[j], (p + 1) * 16, has_b ? ctx[j] : 0u, g, n, m_l[j], l_l[j], O[j]);
         dattn_load(d, h, min(p + 3, last), lane, B);
     }
-    paged_store(a.part + ((size_t)it * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
+#pragma unroll
+    for (uint32_t j = 0; j < TQ; ++j)
+        if (j < valid)
+            paged_store(a.part + (((size_t)base * TQ + j * nch + c) * 32 + h * 8) * kPartStride, kPartStride, lane,
+                        m_l[j], l_l[j], O[j]);
 }
 
 // ---------------------------------------------------------------- KV park / restore (extension)
@@ -1569,7 +1602,7 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
     constexpr uint32_t kSub = 1024;
     const uint32_t max_chunks = (c->max_pos / 16 + kPattnChunk - 1) / kPattnChunk;
     const size_t qn_bytes = (size_t)kSub * 32 * 128 * 4, max_items = (size_t)kSub * max_chunks;
-    const size_t item_bytes = (max_items * 8 + 255) / 256 * 256, off_bytes = ((kSub + 1) * 4 + 255) / 256 * 256;
+    const size_t item_bytes = (max_items * 16 + 255) / 256 * 256, off_bytes = ((kSub + 1) * 4 + 255) / 256 * 256;
     if (!ensure_scratch(F_DATTN, cx, qn_bytes + item_bytes + off_bytes + max_items * 32 * kPartStride * 4))
         return OMEGA_GPU_CHIP_FAIL;
     uint8_t *base = static_cast<uint8_t *>(cx->scratch);
@@ -1594,17 +1627,26 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
         const uint32_t mm = std::min(kSub, m - t0);
         items.clear();
         off.assign(mm + 1, 0);
-        for (uint32_t t = 0; t < mm; ++t) {
-            const uint32_t pages = (pos0 + t0 + t + 1 + 15) / 16, chunks = (pages + kPattnChunk - 1) / kPattnChunk;
-            off[t] = (uint32_t)(items.size() / 2);
-            for (uint32_t ch = 0; ch < chunks; ++ch) {
-                items.push_back(t);
+        // groups of tq tokens share their page loads; each group's chunks follow its last token's
+        // context, and token j of a group owns the partial slots base * tq + j * nch + chunk (kSub
+        // is a multiple of tq, so a group never spans sub-batches)
+        const uint32_t tq = pos0 + t0 + mm >= kPattnLongCtx ? kPattnTqLong : 1;
+        uint32_t base = 0;
+        for (uint32_t g0 = 0; g0 < mm; g0 += tq) {
+            const uint32_t valid = std::min(tq, mm - g0);
+            const uint32_t pages = (pos0 + t0 + g0 + valid + 15) / 16, nch = (pages + kPattnChunk - 1) / kPattnChunk;
+            for (uint32_t j = 0; j < valid; ++j) off[g0 + j] = base * tq + j * nch;
+            off[mm] = base * tq + valid * nch;
+            for (uint32_t ch = 0; ch < nch; ++ch) {
+                items.push_back(g0);
                 items.push_back(ch);
+                items.push_back(base);
+                items.push_back(nch);
             }
-            widest = std::max(widest, chunks);
+            base += nch;
+            widest = std::max(widest, nch);
         }
-        const uint32_t n = (uint32_t)(items.size() / 2);
-        off[mm] = n;
+        const uint32_t n = (uint32_t)(items.size() / 4);
         total_items += n;
         OMEGA_HIP(F_DATTN, hipMemcpyAsync(ditems, items.data(), items.size() * 4, hipMemcpyHostToDevice, cx->stream));
         OMEGA_HIP(F_DATTN, hipMemcpyAsync(doff, off.data(), off.size() * 4, hipMemcpyHostToDevice, cx->stream));
@@ -1613,7 +1655,10 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
         a.m = mm;
         OMEGA_LAUNCH(k_pattn_prep, dim3(4, mm), dim3(64), 0, cx->stream, a);
         OMEGA_HIP(F_DATTN, hipGetLastError());
-        OMEGA_LAUNCH(k_pattn, dim3(4 * n), dim3(64), 0, cx->stream, a);
+        if (tq == 1)
+            OMEGA_LAUNCH(k_pattn<1>, dim3(4 * n), dim3(64), 0, cx->stream, a);
+        else
+            OMEGA_LAUNCH(k_pattn<kPattnTqLong>, dim3(4 * n), dim3(64), 0, cx->stream, a);
         OMEGA_HIP(F_DATTN, hipGetLastError());
         CombineItemsArgs cb;
         cb.part = a.part;

@@ -492,7 +492,8 @@ typedef struct OmegaGpuPfTile {
     uint32_t row0, cnt;
     uint64_t pad;
 } OmegaGpuPfTile;
-/* lib.rs:362-376 */
+/* lib.rs:362-376. Here chunks counts the call's work items, (tile of consecutive query tokens: 4
+ * from a context of 1024 on, else 1; chunk of 32 pages) pairs, and grid_x = 4 kv heads x chunks */
 typedef struct OmegaGpuPrefillAttnInfo {
     uint32_t layer, pos0, m, chunks, grid_x, grid_y, threads, splits, per_split;
     uint64_t elapsed_ns, call_ns;

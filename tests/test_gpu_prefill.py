@@ -229,14 +229,18 @@ def test_moe_combine_slot_order(omega, pf):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_prefill_attention_equals_the_decode_attention(omega, oracle, pf):
+@pytest.mark.parametrize("N,first", [(300, 100), (1300, 1030)])
+def test_prefill_attention_equals_the_decode_attention(omega, oracle, pf, N, first):
+    # (1300, 1030): contexts past 1024 take the 4-token query tiles, the first call spans two
+    # sub-batches of 1024 + 6 tokens (a partial tile) and the second starts at an unaligned 1030
     rng = np.random.default_rng(8)
-    layers, N, eps = 2, 300, 1e-6
+    layers, eps = 2, 1e-6
     qn = (1 + 0.1 * rng.standard_normal((layers, 128))).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal((layers, 128))).astype(np.float32)
-    a = omega.DecodeAttnCache(layers, 512, 1e6)
-    b = omega.DecodeAttnCache(layers, 512, 1e6)
-    orc = oracle.Dattn(layers, 512, 1e6)
+    max_pos = 512 if N < 500 else 2048
+    a = omega.DecodeAttnCache(layers, max_pos, 1e6)
+    b = omega.DecodeAttnCache(layers, max_pos, 1e6)
+    orc = oracle.Dattn(layers, max_pos, 1e6)
     for l in range(layers):
         a.set_norms(l, qn[l], kn[l])
         b.set_norms(l, qn[l], kn[l])
@@ -245,16 +249,18 @@ def test_prefill_attention_equals_the_decode_attention(omega, oracle, pf):
     layer = 1
     dec = np.stack([a.attend(layer, p, qkv[p], eps)[0] for p in range(N)])
     att = pf.PrefillAttention(b)
-    o1, info = att.attend(layer, 0, 100, qkv[:100], eps, 1.0)
-    assert info.m == 100 and info.chunks >= 100
-    o2, _ = att.attend(layer, 100, N - 100, qkv[100:], eps, 1.0)
+    o1, info = att.attend(layer, 0, first, qkv[:first], eps, 1.0)
+    # work items: (query tile of consecutive tokens, chunk of 32 pages) pairs, one wavefront per kv head
+    assert info.m == first and 1 <= info.chunks <= 4 * first and info.grid_x == 4 * info.chunks
+    o2, _ = att.attend(layer, first, N - first, qkv[first:], eps, 1.0)
     pre = np.vstack([o1, o2])
     want = np.stack([orc.attend(layer, p, qkv[p], eps) for p in range(N)])
-    for p in (0, 1, 15, 16, 17, 99, 100, 101, 250, N - 1):
+    for p in sorted({0, 1, 15, 16, 17, first - 1, first, first + 1, 250, 1023, 1024, 1025, 1027, N - 1} - {
+            q for q in range(N, 2000)}):
         assert rel_err(pre[p], want[p]) <= TOL, p
         assert rel_err(pre[p], dec[p]) <= TOL, p
     for h in range(4):
-        for p in (0, 15, 16, 100, N - 1):
+        for p in (0, 15, 16, first, N - 1):
             ka, va = a.read_row(layer, h, p)
             kb, vb = b.read_row(layer, h, p)
             np.testing.assert_array_equal(ka, kb)
