@@ -1534,10 +1534,8 @@ int omega_gpu_decode_attn_cache_export_dev(OmegaGpuDecodeAttnCache *c, uint32_t 
 
 // the padding rows of the last block (positions len .. 16 ceil(len / 16) - 1 of every layer's K
 // and V plane) must be zero (check_payload, qwen3_moe_omega_kvio.rs:162-186)
-static bool kvio_padding_is_zero(const OmegaGpuDecodeAttnCache *c, uint32_t len, const uint8_t *bytes) {
-    const uint32_t tail = len % 16;
-    if (!tail) return true;
-    const uint8_t *last = bytes + (uint64_t)(len / 16) * c->g.block_stride;
+// `last` is the payload's last block, `tail` = len % 16 its valid positions (1 ..= 15)
+static bool kvio_tail_is_zero(const OmegaGpuDecodeAttnCache *c, uint32_t tail, const uint8_t *last) {
     for (uint32_t l = 0; l < c->layers; ++l)
         for (uint32_t v = 0; v < 2; ++v) {
             const uint8_t *pl = last + (uint64_t)l * c->g.layer_stride + v * c->g.plane_stride;
@@ -1553,7 +1551,7 @@ int omega_gpu_decode_attn_cache_import(OmegaGpuDecodeAttnCache *c, uint32_t star
     clear_error(F_DATTN);
     if (int rc = kvio_check(c, start, len, bytes, nbytes, "import")) return rc;
     const uint8_t *host = static_cast<const uint8_t *>(bytes);
-    if (!kvio_padding_is_zero(c, len, host)) {
+    if (len % 16 && !kvio_tail_is_zero(c, len % 16, host + (uint64_t)(len / 16) * c->g.block_stride)) {
         set_error(F_DATTN, "kv import: padding rows past position %u are not zero", len);
         return OMEGA_GPU_BAD_ARGS;
     }
@@ -1582,7 +1580,7 @@ int omega_gpu_decode_attn_cache_import_dev(OmegaGpuDecodeAttnCache *c, uint32_t 
         OMEGA_HIP(F_DATTN, hipMemcpy(last.data(), static_cast<const uint8_t *>(bytes_dev) +
                                                       (uint64_t)(len / 16) * c->g.block_stride,
                                      c->g.block_stride, hipMemcpyDeviceToHost));
-        if (!kvio_padding_is_zero(c, tail, last.data())) {
+        if (!kvio_tail_is_zero(c, tail, last.data())) {
             set_error(F_DATTN, "kv import: padding rows past position %u are not zero", len);
             return OMEGA_GPU_BAD_ARGS;
         }
