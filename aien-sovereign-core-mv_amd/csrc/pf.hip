@@ -545,6 +545,7 @@ uint32_t omega_gpu_pf_qgemm_tiles_va(uint32_t experts, const uint64_t *w_va, con
 int omega_gpu_pf_moe_plan(uint32_t tokens, uint32_t experts, uint32_t top_k, const float *logits, uint32_t *topk_ids,
                           float *topk_weights, uint32_t *counts, uint32_t *grouped_token,
                           uint32_t *assignment_to_grouped, uint32_t *grouped_to_assignment) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());  // the session's error slot
     clear_error(F_SESSION);
     if (experts == 0 || experts > 65536 || top_k == 0 || top_k > experts || top_k > 64 ||
         (uint64_t)tokens * top_k > 0xffffffffull || !logits || !topk_ids || !topk_weights || !counts ||
