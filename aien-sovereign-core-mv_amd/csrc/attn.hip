@@ -1199,6 +1199,21 @@ KvGeom geom_of(const OmegaGpuKvLayout &l) {
 }  // namespace omega
 
 // ------------------------------------------------------------------------ fused decode cache
+namespace omega {
+constexpr uint32_t kRowsChunk = 8192;  // rows per staged chunk of omega_gpu_decode_attn_cache_write
+// rows [pos, pos + gridDim.x) of one (layer, kv head) of the fused cache: row i's K into the K
+// plane, its V into the transposed V plane (dim d of token t at plane + head * 4096 + d * 32 + t * 2)
+__global__ __launch_bounds__(128) void k_cache_write_rows(uint8_t *pool, KvGeom g, uint32_t layer, uint32_t h,
+                                                          uint32_t pos, const uint16_t *k, const uint16_t *v) {
+    const uint32_t i = blockIdx.x, d = threadIdx.x, p = pos + i;
+    uint8_t *page = pool + (uint64_t)(p >> 4) * g.block_stride + (uint64_t)layer * g.layer_stride;
+    reinterpret_cast<uint16_t *>(page + (uint64_t)(p & 15) * g.token_stride + (uint64_t)h * g.head_stride)[d] =
+        k[(size_t)i * 128 + d];
+    *reinterpret_cast<uint16_t *>(page + g.plane_stride + (uint64_t)h * kVtHead + d * 32 + (p & 15) * 2) =
+        v[(size_t)i * 128 + d];
+}
+}  // namespace omega
+
 struct OmegaGpuDecodeAttnCache {
     uint32_t layers = 0, max_pos = 0;
     double theta = 0;
@@ -1398,17 +1413,21 @@ int omega_gpu_decode_attn_cache_write(OmegaGpuDecodeAttnCache *c, uint32_t layer
     }
     Ctx *cx = ctx(F_DATTN);
     if (!cx) return OMEGA_GPU_CHIP_FAIL;
-    OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
-    for (uint32_t i = 0; i < count; ++i) {
-        const uint32_t p = pos + i;
-        const uint64_t page = (uint64_t)(p / 16) * c->g.block_stride + (uint64_t)layer * c->g.layer_stride;
-        const uint64_t ko = page + (uint64_t)(p % 16) * c->g.token_stride + (uint64_t)kv_head * c->g.head_stride;
-        const uint64_t vo = page + c->g.plane_stride + (uint64_t)kv_head * kVtHead + (p % 16) * 2;
-        OMEGA_HIP(F_DATTN, hipMemcpyAsync(c->pool + ko, k_bf16 + (size_t)i * 128, 256,
-                                          hipMemcpyHostToDevice, cx->stream));
-        // V is stored transposed: one column of the page's [dim][16 tokens] block
-        OMEGA_HIP(F_DATTN, hipMemcpy2DAsync(c->pool + vo, 32, v_bf16 + (size_t)i * 128, 2, 2, 128,
-                                            hipMemcpyHostToDevice, cx->stream));
+    // chunks of rows: K | V staged in pinned memory, one copy to the device, one scatter launch
+    const uint32_t chunk = std::min<uint32_t>(count, kRowsChunk);
+    const size_t bytes = (size_t)chunk * 2 * 256;
+    if (!ensure_pinned(F_DATTN, cx, bytes) || !ensure_scratch(F_DATTN, cx, bytes)) return OMEGA_GPU_CHIP_FAIL;
+    uint8_t *pin = static_cast<uint8_t *>(cx->pin), *dev = static_cast<uint8_t *>(cx->scratch);
+    for (uint32_t i0 = 0; i0 < count; i0 += chunk) {
+        const uint32_t n = std::min(chunk, count - i0);
+        OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));  // the pinned staging is free again
+        memcpy(pin, k_bf16 + (size_t)i0 * 128, (size_t)n * 256);
+        memcpy(pin + (size_t)n * 256, v_bf16 + (size_t)i0 * 128, (size_t)n * 256);
+        OMEGA_HIP(F_DATTN, hipMemcpyAsync(dev, pin, (size_t)n * 512, hipMemcpyHostToDevice, cx->stream));
+        hipLaunchKernelGGL(k_cache_write_rows, dim3(n), dim3(128), 0, cx->stream, c->pool, c->g, layer, kv_head,
+                           pos + i0, reinterpret_cast<const uint16_t *>(dev),
+                           reinterpret_cast<const uint16_t *>(dev + (size_t)n * 256));
+        OMEGA_HIP(F_DATTN, hipGetLastError());
     }
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
     return OMEGA_GPU_OK;

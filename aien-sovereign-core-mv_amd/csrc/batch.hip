@@ -795,25 +795,12 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
     const uint32_t key = seqs | (b->keep_logits ? 256u : 0u);
     auto it = b->exec.find(key);
     if (it == b->exec.end()) {
-        OMEGA_HIP(F_SESSION, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-        int rc = bd_enqueue(b, seqs, c->stream);
+        // built node by node (no stream capture)
         hipGraph_t graph = nullptr;
-        hipError_t e = hipStreamEndCapture(c->stream, &graph);
-        if (rc) {
-            if (graph) (void)hipGraphDestroy(graph);
-            return rc;
-        }
-        if (e != hipSuccess) {
-            set_error(F_SESSION, "batch decode capture: %s", hipGetErrorString(e));
-            return OMEGA_GPU_CODEGEN_FAIL;
-        }
         hipGraphExec_t ex = nullptr;
-        e = hipGraphInstantiate(&ex, graph, nullptr, nullptr, 0);
-        if (e != hipSuccess) {
-            (void)hipGraphDestroy(graph);
-            set_error(F_SESSION, "batch decode instantiate: %s", hipGetErrorString(e));
-            return OMEGA_GPU_CODEGEN_FAIL;
-        }
+        const int rc = build_graph(F_SESSION, "batch decode graph", &graph, &ex,
+                                   [&]() { return bd_enqueue(b, seqs, c->stream); });
+        if (rc) return rc;
         b->graphs.push_back(graph);
         it = b->exec.emplace(key, ex).first;
     }

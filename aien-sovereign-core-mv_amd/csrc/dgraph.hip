@@ -404,24 +404,11 @@ int rebuild(OmegaGpuDecodeGraph *g, Ctx *c, int v) {
         (void)hipGraphDestroy(g->graph_v[v]);
         g->graph_v[v] = nullptr;
     }
-    OMEGA_HIP(F_SESSION, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_token(g, c->stream, g->kinds, nullptr, nullptr, false, v == 1);
-    hipGraph_t graph = nullptr;
-    hipError_t e = hipStreamEndCapture(c->stream, &graph);
-    if (rc) {
-        if (graph) (void)hipGraphDestroy(graph);
-        return rc;
-    }
-    if (e != hipSuccess) {
-        set_error(F_SESSION, "decode graph capture: %s", hipGetErrorString(e));
-        return OMEGA_GPU_CODEGEN_FAIL;
-    }
-    g->graph_v[v] = graph;
-    e = hipGraphInstantiate(&g->exec_v[v], graph, nullptr, nullptr, 0);
-    if (e != hipSuccess) {
-        set_error(F_SESSION, "decode graph instantiate: %s", hipGetErrorString(e));
-        return OMEGA_GPU_CODEGEN_FAIL;
-    }
+    // the graph is built node by node (no stream capture): a chain of the token's kernels
+    const int rc = build_graph(F_SESSION, "decode graph", &g->graph_v[v], &g->exec_v[v], [&]() {
+        return enqueue_token(g, c->stream, g->kinds, nullptr, nullptr, false, v == 1);
+    });
+    if (rc) return rc;
     g->dirty_v[v] = false;
     return OMEGA_GPU_OK;
 }

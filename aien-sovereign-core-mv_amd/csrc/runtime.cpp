@@ -148,6 +148,11 @@ LaunchStamp &launch_stamp() {
     return s;
 }
 
+GraphRecorder *&graph_recorder() {
+    static thread_local GraphRecorder *r = nullptr;
+    return r;
+}
+
 uint64_t event_ns(Ctx *c) {
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, c->ev0, c->ev1) != hipSuccess) return 0;

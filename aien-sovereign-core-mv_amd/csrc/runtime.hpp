@@ -11,6 +11,8 @@
 #include <cstdint>
 #include <cstring>
 #include <mutex>
+#include <tuple>
+#include <type_traits>
 
 #include "omega_gpu.h"
 
@@ -83,10 +85,87 @@ struct LaunchStamp {
 };
 LaunchStamp &launch_stamp();  // per thread
 
+// Graph building without stream capture: while a recorder is set on the thread, a launch made
+// through OMEGA_LAUNCH becomes a kernel node of `graph` that depends on the previous one (a
+// chain), and nothing runs. The node copies the argument values when it is added. Only kernel
+// launches may happen while recording (the launchers the graphs use make no other stream call).
+struct GraphRecorder {
+    hipGraph_t graph = nullptr;
+    hipGraphNode_t last = nullptr;
+    hipError_t err = hipSuccess;
+    uint32_t nodes = 0;
+};
+GraphRecorder *&graph_recorder();  // per thread; null when not recording
+
+template <typename... P, typename... A>
+void record_kernel(void (*kern)(P...), dim3 grid, dim3 block, unsigned shm, A &&...args) {
+    GraphRecorder *r = graph_recorder();
+    static_assert(sizeof...(P) == sizeof...(A), "one value per kernel parameter");
+    std::tuple<std::decay_t<P>...> vals(std::forward<A>(args)...);
+    void *params[sizeof...(P) ? sizeof...(P) : 1];
+    std::apply([&](auto &...v) {
+        size_t i = 0;
+        ((params[i++] = (void *)&v), ...);
+    }, vals);
+    hipKernelNodeParams kp{};
+    kp.func = (void *)kern;
+    kp.gridDim = grid;
+    kp.blockDim = block;
+    kp.sharedMemBytes = shm;
+    kp.kernelParams = params;
+    kp.extra = nullptr;
+    hipGraphNode_t node = nullptr;
+    const hipError_t e =
+        hipGraphAddKernelNode(&node, r->graph, r->last ? &r->last : nullptr, r->last ? 1 : 0, &kp);
+    if (e != hipSuccess) {
+        if (r->err == hipSuccess) r->err = e;
+        return;
+    }
+    r->last = node;
+    ++r->nodes;
+}
+
+// Builds `*exec` from the launches `enqueue()` makes (an int-returning callable: 0 or an ABI
+// return code), as a chain of kernel nodes. On failure sets the family error and destroys what
+// it made; *graph receives the graph the exec was instantiated from (the caller owns both).
+template <typename F>
+int build_graph(Family fam, const char *what, hipGraph_t *graph, hipGraphExec_t *exec, F &&enqueue) {
+    *graph = nullptr;
+    *exec = nullptr;
+    hipError_t e = hipGraphCreate(graph, 0);
+    if (e != hipSuccess) {
+        set_error(fam, "%s: hipGraphCreate: %s", what, hipGetErrorString(e));
+        return OMEGA_GPU_CODEGEN_FAIL;
+    }
+    GraphRecorder rec;
+    rec.graph = *graph;
+    graph_recorder() = &rec;
+    const int rc = enqueue();
+    graph_recorder() = nullptr;
+    if (rc || rec.err != hipSuccess) {
+        (void)hipGraphDestroy(*graph);
+        *graph = nullptr;
+        if (rc) return rc;
+        set_error(fam, "%s: hipGraphAddKernelNode: %s", what, hipGetErrorString(rec.err));
+        return OMEGA_GPU_CODEGEN_FAIL;
+    }
+    e = hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(*graph);
+        *graph = nullptr;
+        *exec = nullptr;
+        set_error(fam, "%s: instantiate: %s", what, hipGetErrorString(e));
+        return OMEGA_GPU_CODEGEN_FAIL;
+    }
+    return OMEGA_GPU_OK;
+}
+
 #define OMEGA_LAUNCH(kern, grid, block, shm, st, ...)                                            \
     do {                                                                                         \
         ::omega::LaunchStamp &ls_ = ::omega::launch_stamp();                                     \
-        if (ls_.start) {                                                                         \
+        if (::omega::graph_recorder()) {                                                         \
+            ::omega::record_kernel(kern, grid, block, shm, __VA_ARGS__);                        \
+        } else if (ls_.start) {                                                                  \
             hipExtLaunchKernelGGL(kern, grid, block, shm, st, ls_.start, ls_.stop, 0, __VA_ARGS__); \
             ls_.start = ls_.stop = nullptr;                                                      \
         } else {                                                                                 \

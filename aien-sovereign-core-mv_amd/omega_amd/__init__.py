@@ -300,10 +300,10 @@ def gpu_count() -> int:
 
 
 def require_gpu():
-    import pytest
-
+    """Raises when no GPU is visible or the library is not built: a caller that needs the device
+    fails loudly rather than passing without it."""
     if gpu_count() == 0:
-        pytest.skip("no GPU")
+        raise RuntimeError("no HIP device is visible: the MI355X path needs a GPU")
     lib()
 
 
@@ -799,6 +799,64 @@ class DecodeGraph:
             self.free()
         except Exception:
             pass
+
+
+QWEN3_30B = dict(layers=48, hidden=2048, q_heads=32, kv_heads=4, head_dim=128, experts=128,
+                 top_k=8, inter=768, vocab=151936, eps=1e-6, rope_theta=1e6)
+
+
+def synth_tensor_id(layer, kind):
+    """Tensor id of the shared counter-based generator for (layer, kind): kinds 0..3 are the
+    q|k|v, o, gate|up and down FP8 projections, 8 the router; the embedding is id 1 and the
+    lm_head id 2 (the CPU oracle's oref_model_synth uses the same ids)."""
+    return 1000 + layer * 16 + kind
+
+
+class SynthDecodeModel:
+    """A random-init Qwen3-MoE model made resident the way OmegaModelUploader does it
+    (qwen3_moe_omega.rs:1231-1598), with every tensor synthesised on the device by the library's
+    generator instead of read from a checkpoint: FP8 projections N(0, sigma) block-quantised,
+    router rows bf16 N(0, sigma), bf16 embedding and lm_head N(0, 0.02), norm weights 1.0; the
+    router directories, the fused decode cache and the decode graph over them. The CPU oracle's
+    oref_model_synth(seed, sigma, norm_sigma = 0) builds the same values."""
+
+    def __init__(self, seed, max_pos, cfg=None, sigma=0.02):
+        c = dict(QWEN3_30B if cfg is None else cfg)
+        self.cfg = c
+        L, H, E, HD = c["layers"], c["hidden"], c["experts"], c["head_dim"]
+        qkv_n = (c["q_heads"] + 2 * c["kv_heads"]) * HD
+        self.router = Router(L, E)
+        self.cache = DecodeAttnCache(L, max_pos, c["rope_theta"])
+        ones = np.ones(H, np.float32)
+        self.layers = []
+        for l in range(L):
+            qkv = Fp8Tensor.synth(1, qkv_n, H, seed, synth_tensor_id(l, 0), sigma)
+            o = Fp8Tensor.synth(1, H, c["q_heads"] * HD, seed, synth_tensor_id(l, 1), sigma)
+            gu = Fp8Tensor.synth(E, 2 * c["inter"], H, seed, synth_tensor_id(l, 2), sigma)
+            dn = Fp8Tensor.synth(E, H, c["inter"], seed, synth_tensor_id(l, 3), sigma)
+            self.layers.append((qkv, o, gu, dn))
+            self.router.set_layer(l, synth_bf16_host(seed, synth_tensor_id(l, 8), (E, H), sigma), ones)
+            self.router.set_directory(l, np.array([gu.entry(e) for e in range(E)], np.uint64),
+                                      np.array([dn.entry(e) for e in range(E)], np.uint64))
+            self.cache.set_norms(l, np.ones(HD, np.float32), np.ones(HD, np.float32))
+        self.lm = Bf16Tensor.synth(c["vocab"], H, seed, 2, 0.02)
+        self.embed = Bf16Tensor.synth(c["vocab"], H, seed, 1, 0.02)
+        self.graph = DecodeGraph(L, c["vocab"], c["eps"], self.router, self.cache, self.lm)
+        for l, (qkv, o, gu, dn) in enumerate(self.layers):
+            self.graph.set_layer(l, qkv, o, gu, dn, ones)
+        self.graph.set_final_norm(ones)
+        self.graph.set_embedding(self.embed)
+
+    def free(self):
+        if self.graph is None:
+            return
+        self.graph.free()
+        for ts in self.layers:
+            for t in ts:
+                t.free()
+        for t in (self.router, self.cache, self.lm, self.embed):
+            t.free()
+        self.graph = None
 
 
 _hip = None

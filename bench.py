@@ -73,31 +73,11 @@ LAYER_KINDS = ["qkv", "attn", "attn_combine", "o_proj", "router", "gate_up", "do
 
 
 def build_model(om, max_pos):
+    """The full 48-layer model synthesised on the device (omega_amd.SynthDecodeModel)."""
     t0 = time.time()
-    router = om.Router(L)
-    cache = om.DecodeAttnCache(L, max_pos, 1e6)
-    ones = np.ones(H, np.float32)
-    layers = []
-    for l in range(L):
-        qkv = om.Fp8Tensor.synth(1, 5120, 2048, SEED, tid(l, 0))
-        o = om.Fp8Tensor.synth(1, 2048, 4096, SEED, tid(l, 1))
-        gu = om.Fp8Tensor.synth(E, 1536, 2048, SEED, tid(l, 2))
-        dn = om.Fp8Tensor.synth(E, 2048, 768, SEED, tid(l, 3))
-        layers.append((qkv, o, gu, dn))
-        router.set_layer(l, om.synth_bf16_host(SEED, tid(l, 8), (E, H), 0.02), ones)
-        router.set_directory(l, np.array([gu.entry(e) for e in range(E)], np.uint64),
-                             np.array([dn.entry(e) for e in range(E)], np.uint64))
-        cache.set_norms(l, np.ones(HD, np.float32), np.ones(HD, np.float32))
-    lm = om.Bf16Tensor.synth(V, H, SEED, 2, 0.02)
-    embed = om.Bf16Tensor.synth(V, H, SEED, 1, 0.02)
-    g = om.DecodeGraph(L, V, 1e-6, router, cache, lm)
-    for l, (qkv, o, gu, dn) in enumerate(layers):
-        g.set_layer(l, qkv, o, gu, dn, ones)
-    g.set_final_norm(ones)
-    g.set_embedding(embed)
+    m = om.SynthDecodeModel(SEED, max_pos)
     om.sync()
-    return dict(graph=g, layers=layers, router=router, cache=cache, lm=lm, embed=embed,
-                seconds=time.time() - t0)
+    return dict(model=m, graph=m.graph, seconds=time.time() - t0)
 
 
 def cpu_baseline(threads):
@@ -956,12 +936,7 @@ def main():
     if not args.no_bs32:
         # the metric's bs32 figure: configuration 5's batched step over the same architecture
         # (its own model build; the bs=1 model is freed first)
-        g.free()
-        for ts in model["layers"]:
-            for t in ts:
-                t.free()
-        for k in ("router", "cache", "lm", "embed"):
-            model[k].free()
+        model["model"].free()
         sargs = argparse.Namespace(serve_steps=args.bs32_steps, serve_warmup=4, no_cpu=True, eager=False,
                                    cpu_threads=args.cpu_threads)
         sl = bench_serve(om, sargs, emit=False)

@@ -732,6 +732,12 @@ static inline size_t da_row(const oref_dattn *c, int layer, int head, int pos) {
     return (((size_t)layer * DA_KVH + head) * c->max_pos + pos) * DA_HD;
 }
 
+/* Planted wiring mistakes for the composition checks (test infrastructure, off by default):
+ * 1 the engine swaps the input and post-attention norm weights, 2 q is rotated at pos + 1 (k at
+ * pos), 3 this token's K/V row is appended one slot late. */
+static int g_mutant = 0;
+void oref_set_mutant(int m) { g_mutant = m; }
+
 void oref_dattn_attend(oref_dattn *c, int layer, int pos, const float *qkv, float eps,
                        float out_scale, float *out) {
     float q[DA_QH * DA_HD], k[DA_KVH * DA_HD];
@@ -739,11 +745,21 @@ void oref_dattn_attend(oref_dattn *c, int layer, int pos, const float *qkv, floa
     oref_rmsnorm_per_head(qkv, c->q_norm + (size_t)layer * DA_HD, eps, DA_QH, DA_HD, q);
     oref_rmsnorm_per_head(qkv + DA_QH * DA_HD, c->k_norm + (size_t)layer * DA_HD, eps, DA_KVH,
                           DA_HD, k);
-    oref_apply_rope(q, k, pos, DA_QH, DA_KVH, DA_HD, c->theta);
+    if (g_mutant == 2) {
+        float kdummy[DA_KVH * DA_HD];
+        memcpy(kdummy, k, sizeof(kdummy));
+        oref_apply_rope(q, kdummy, pos + 1, DA_QH, DA_KVH, DA_HD, c->theta);
+        float qdummy[DA_QH * DA_HD];
+        memcpy(qdummy, q, sizeof(qdummy));
+        oref_apply_rope(qdummy, k, pos, DA_QH, DA_KVH, DA_HD, c->theta);
+    } else {
+        oref_apply_rope(q, k, pos, DA_QH, DA_KVH, DA_HD, c->theta);
+    }
+    const int slot = g_mutant == 3 && pos + 1 < c->max_pos ? pos + 1 : pos;
     for (int h = 0; h < DA_KVH; h++)
         for (int d = 0; d < DA_HD; d++) {
-            c->k[da_row(c, layer, h, pos) + d] = oref_kv_f32_to_bf16(k[h * DA_HD + d]);
-            c->v[da_row(c, layer, h, pos) + d] = oref_kv_f32_to_bf16(v[h * DA_HD + d]);
+            c->k[da_row(c, layer, h, slot) + d] = oref_kv_f32_to_bf16(k[h * DA_HD + d]);
+            c->v[da_row(c, layer, h, slot) + d] = oref_kv_f32_to_bf16(v[h * DA_HD + d]);
         }
     int ctx = pos + 1;
     float *K = malloc(sizeof(float) * (size_t)ctx * DA_KVH * DA_HD);
@@ -929,14 +945,16 @@ int oref_engine_step(oref_engine *e, uint32_t token, float *hidden_out) {
     float *dn = malloc(sizeof(float) * (size_t)K * h);
     uint32_t zero = 0;
     for (int l = 0; l < c->layers; l++) {
-        oref_rmsnorm(x, m->norms[0][l], h, c->eps, xn);
+        const float *in_norm = m->norms[g_mutant == 1 ? 1 : 0][l];
+        const float *post_norm = m->norms[g_mutant == 1 ? 0 : 1][l];
+        oref_rmsnorm(x, in_norm, h, c->eps, xn);
         fp8_grouped_impl(m->w[0][l], m->s[0][l], 1, qkv_n, h, 1, &zero, xn, 1, qkv, e->threads);
         oref_dattn_attend(e->kv, l, e->pos, qkv, c->eps, 1.0f, att);
         fp8_grouped_impl(m->w[1][l], m->s[1][l], 1, h, qd, 1, &zero, att, 1, proj, e->threads);
         for (int j = 0; j < h; j++) x[j] += proj[j];
         uint32_t *ids = e->route_ids + (size_t)l * K;
         float *wts = e->route_w + (size_t)l * K;
-        int rc = oref_route(m->router[l], m->norms[1][l], c->experts, h, K, x, c->eps, e->refined,
+        int rc = oref_route(m->router[l], post_norm, c->experts, h, K, x, c->eps, e->refined,
                             ids, wts, post, logits);
         if (rc != 0) { e->pos = -1; return -3; }
         /* margin between the K-th and (K+1)-th logits */

@@ -201,6 +201,10 @@ int oref_engine_pos(const oref_engine *e);
 void oref_engine_last_routes(const oref_engine *e, uint32_t *ids, float *weights, float *margins);
 /* Residual row after the last step (hidden floats). */
 void oref_engine_last_x(const oref_engine *e, float *x);
+/* Planted wiring mistakes (test infrastructure; 0 = none): 1 input / post-attention norm
+ * weights swapped in oref_engine_step, 2 q rotated at pos + 1 in oref_dattn_attend (k at pos),
+ * 3 the K/V row appended one slot late. Process-wide. */
+void oref_set_mutant(int m);
 
 #ifdef __cplusplus
 }

@@ -112,6 +112,7 @@ def lib():
             "oref_dattn_attend": (None, [P, i32, i32, P, f32, f32, P]),
             "oref_dattn_read_row": (None, [P, i32, i32, i32, P, P]),
             "oref_dattn_write_rows": (None, [P, i32, i32, i32, i32, P, P]),
+            "oref_set_mutant": (None, [i32]),
             "oref_model_synth": (P, [P, u64, f32, f32, i32]),
             "oref_model_free": (None, [P]),
             "oref_model_tensor": (P, [P, i32, i32, P]),
@@ -447,6 +448,11 @@ class Dattn:
         v = np.empty(128, dtype=np.uint16)
         lib().oref_dattn_read_row(self.h, layer, head, pos, ptr(k), ptr(v))
         return k, v
+
+    def write_rows(self, layer, head, pos, k, v):
+        k = np.ascontiguousarray(k, dtype=np.uint16).reshape(-1, 128)
+        v = np.ascontiguousarray(v, dtype=np.uint16).reshape(-1, 128)
+        lib().oref_dattn_write_rows(self.h, layer, head, pos, k.shape[0], ptr(k), ptr(v))
 
     def __del__(self):
         if getattr(self, "h", None):

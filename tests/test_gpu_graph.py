@@ -220,3 +220,34 @@ def test_token_id_gathers_the_embedding_on_the_device(omega, oracle, small):
         assert g.graph.token_id(t, pos)[0] == outs[0][0][pos]
     g.graph.set_embedding(emb)
     emb2.free()
+
+
+def test_argmax_ties_go_to_the_lowest_index(omega, oracle):
+    """The graph's greedy token is the lowest index of the maximum (crates/aien-omega-dgraph/src/
+    lib.rs:347-349, sample_argmax tensor.rs:299-318). Four lm_head rows (3, 100, 5000, 8000) are
+    the same bf16 vector u = bf16(0.05 h), h the oracle's final hidden of the first step, so their
+    logits are exactly tied and far above every other row (u . h is about 0.05 |h|^2, the other
+    logits are about N(0, 1)); two rows hold -u. Identical rows give bit-identical logits on the
+    device (a row's arithmetic does not depend on where it sits), so the token must be 3."""
+    m = oracle.Model(model_config(2, 8192), seed=77, sigma=0.02, norm_sigma=0.1, threads=16)
+    eng = oracle.Engine(m, 256, refined_router=True, threads=16)
+    h0 = eng.step(11)
+    lm = m.lm_head()  # a writable view of the oracle model's buffer, uploaded below
+    u = oracle.f32_to_bf16((0.05 * h0).astype(np.float32))
+    for r in (3, 100, 5000, 8000):
+        lm[r] = u
+    for r in (5, 9):
+        lm[r] = u ^ np.uint16(0x8000)
+    want_logits = eng.logits(h0)
+    assert oracle.argmax(want_logits) == 3
+    g = GpuModel(omega, m, 256)
+    try:
+        tok, _ = g.graph.token(g.x_embed(11), 0)
+        _, _, logits = g.graph.read(logits=True)
+        tied = logits[[3, 100, 5000, 8000]]
+        assert (tied == tied[0]).all(), tied
+        assert logits.max() == tied[0] and np.flatnonzero(logits == logits.max())[0] == 3
+        assert tok == 3, tok
+        assert rel_err(logits, want_logits) <= TOL
+    finally:
+        g.free()

@@ -74,7 +74,11 @@ def oracle_out(oracle, pool, q, table, ctx, layer):
     return want
 
 
-@pytest.mark.parametrize("seqs,ctx,check", [(1, 2048, None), (1, 32768, None), (8, 8192, None),
+# all nine configuration-3 points (batch {1, 8, 32} x context {2048, 8192, 32768}); the oracle
+# checks every sequence up to 8 x 8192 and three sampled sequences beyond
+@pytest.mark.parametrize("seqs,ctx,check", [(1, 2048, None), (1, 8192, None), (1, 32768, None),
+                                            (8, 2048, None), (8, 8192, None), (8, 32768, (0, 3, 7)),
+                                            (32, 2048, None), (32, 8192, (0, 13, 31)),
                                             (32, 32768, (0, 17, 31))])
 def test_config3_shapes(omega, oracle, seqs, ctx, check):
     rng = np.random.default_rng(seqs * 7 + ctx)

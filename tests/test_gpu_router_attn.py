@@ -155,6 +155,46 @@ def test_decode_attention_sequence_matches_the_oracle(omega, oracle):
     c.free()
 
 
+def test_decode_attention_long_contexts_match_the_oracle(omega, oracle):
+    """The fused kernel where each of its 64 splits holds several pages (crates/aien-omega-dattn/
+    src/lib.rs:45-48 allows max_pos up to 131072): positions 0..32767 of one layer filled with
+    random bf16 K/V rows through cache_write (both caches hold the same rows), then attention at
+    the decode benchmark's contexts (517-600), at about 5000 (5 pages per split) and at 32767
+    (32 pages per split); the appended K/V rows bit-exact, outputs within 2e-3."""
+    max_pos, theta, fill = 33024, 1e6, 32767
+    c = omega.DecodeAttnCache(1, max_pos, theta)
+    ref = oracle.Dattn(1, max_pos, theta)
+    rng = np.random.default_rng(12)
+    qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    c.set_norms(0, qn, kn)
+    ref.set_norms(0, qn, kn)
+    for h in range(4):
+        kr = oracle.f32_to_bf16((2 * rng.standard_normal((fill, 128))).astype(np.float32))
+        vr = oracle.f32_to_bf16(rng.standard_normal((fill, 128)).astype(np.float32))
+        c.write_rows(0, h, 0, kr, vr)
+        ref.write_rows(0, h, 0, kr, vr)
+        for p in (0, 15, 16, 4097, fill - 1):
+            k, v = c.read_row(0, h, p)
+            np.testing.assert_array_equal(k, kr[p])
+            np.testing.assert_array_equal(v, vr[p])
+    worst = {}
+    for pos in (517, 520, 531, 544, 559, 600, 4999, 5000, 5003, fill):
+        qkv = _qkv_row(rng)
+        out, info = c.attend(0, pos, qkv, 1e-6)
+        want = ref.attend(0, pos, qkv, 1e-6)
+        worst[pos] = rel_err(out, want)
+        assert info.kv_bytes == 2 * 4 * (pos + 1) * 256
+        for h in range(4):
+            k, v = c.read_row(0, h, pos)
+            wk, wv = ref.read_row(0, h, pos)
+            np.testing.assert_array_equal(k, wk)
+            np.testing.assert_array_equal(v, wv)
+    print("fused attention rel err by position:", {p: f"{e:.1e}" for p, e in worst.items()})
+    assert max(worst.values()) <= TOL, worst
+    c.free()
+
+
 def test_decode_attention_out_scale_and_cache_rows(omega, oracle):
     c = omega.DecodeAttnCache(1, 256, 1e7)
     c.set_norms(0, np.ones(128, np.float32), np.ones(128, np.float32))
