@@ -19,8 +19,8 @@
 //   7. down GEMV: one workgroup = the 8 experts' wavefronts for 8 rows, combined in slot order
 //      in LDS and added into the residual,
 // then the lm_head with the final RMSNorm in its prologue and the argmax folded in: 7L + 1
-// launches captured once as a hipGraph and replayed per token. The position and token id live
-// in device memory, so one graph serves every token.
+// launches built once as a hipGraph (kernel nodes in a chain) and replayed per token. The
+// position and token id live in device memory, so one graph serves every token.
 #include <cstdio>
 #include <vector>
 
@@ -40,6 +40,7 @@ uint32_t cache_layers(const OmegaGpuDecodeAttnCache *c);
 uint32_t cache_max_pos(const OmegaGpuDecodeAttnCache *c);
 
 constexpr uint32_t kHidden = 2048, kInter = 768, kExperts = 128;
+constexpr uint32_t kLaunchesPerLayer = 7;
 
 // ---------------------------------------------------------------- gate|up + SwiGLU
 struct GateUpArgs {
@@ -58,6 +59,7 @@ struct GateUpArgs {
     uint64_t *tab_gu = nullptr, *tab_dn = nullptr;
     uint32_t *log_ids = nullptr;
     float *log_w = nullptr;
+    const uint32_t *forced = nullptr;  // parity tests: the layer's 8 expert ids instead of the ranking
     int graph_mutant = 0;        // 1: gate and up swapped
 };
 
@@ -79,7 +81,8 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     // row's: the row is written to LDS after the ranking)
     if (wid == 0) {
         Route r;
-        route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
+        if (a.forced) route_forced(a.logits, a.forced, r);
+        else route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
         if (lane == 0) {
 #pragma unroll
             for (int s = 0; s < kTopK; ++s) {
@@ -224,14 +227,18 @@ struct OmegaGpuDecodeGraph {
     float *hidden = nullptr, *logits = nullptr;
     GraphIo *io = nullptr;
     uint32_t *route_log = nullptr;  // [layers][8] routed ids of the last token
+    uint32_t *forced = nullptr;     // [layers][8] forced expert ids (parity tests), when force_on
+    bool force_on = false;
     float *route_log_w = nullptr;   // [layers][8] their weights
     GraphIo *pin = nullptr;         // pinned host twin of io
     const OmegaGpuBf16Tensor *embed = nullptr;  // optional: device embedding (token-id entry)
-    // graphs: [0] x from the host, [1] x gathered from the embedding by token id
-    hipGraph_t graph_v[2] = {nullptr, nullptr};
-    hipGraphExec_t exec_v[2] = {nullptr, nullptr};
-    bool dirty_v[2] = {true, true};
-    void mark_dirty() { dirty_v[0] = dirty_v[1] = true; }
+    // graphs: [0] x from the host, [1] x gathered from the embedding by token id; [2], [3] the
+    // same with an event-record node before the first kernel and after every kernel (stamps)
+    hipGraph_t graph_v[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipGraphExec_t exec_v[4] = {nullptr, nullptr, nullptr, nullptr};
+    bool dirty_v[4] = {true, true, true, true};
+    void mark_dirty() { dirty_v[0] = dirty_v[1] = dirty_v[2] = dirty_v[3] = true; }
+    bool stamps_graph = false;  // the last stamped token ran as the stamped graph
     int mutant = 0;
     bool stamps = false;
     int flush_each = 0;  // 1: synchronise after every launch; 2: direct launches, no graph
@@ -259,17 +266,21 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
             k_i += 2;
         }
     };
+    // an event after the launch: a stream record, or an event-record node while a graph is built
+    auto record = [&](hipEvent_t e) -> hipError_t {
+        return graph_recorder() ? record_event_node(e) : hipEventRecord(e, st);
+    };
     auto mark = [&](uint8_t kind) -> hipError_t {
         kinds.push_back(kind);
         if (ev && e_i < ev->size()) {
-            hipError_t r = hipEventRecord((*ev)[e_i++], st);
+            hipError_t r = record((*ev)[e_i++]);
             if (r != hipSuccess) return r;
         }
         if (sync_each) return hipStreamSynchronize(st);
         return hipSuccess;
     };
     if (ev && !ev->empty()) {
-        OMEGA_HIP(F_SESSION, hipEventRecord((*ev)[0], st));
+        OMEGA_HIP(F_SESSION, record((*ev)[0]));
         e_i = 1;
     }
     const uint32_t *pos_dev = &g->io->pos;
@@ -350,6 +361,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         gu.tab_dn = ra.tab_dn;
         gu.log_ids = g->route_log + (size_t)l * 8;
         gu.log_w = g->route_log_w + (size_t)l * 8;
+        gu.forced = g->force_on ? g->forced + (size_t)l * 8 : nullptr;
         gu.graph_mutant = g->mutant;
         arm();
         OMEGA_LAUNCH(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
@@ -404,9 +416,16 @@ int rebuild(OmegaGpuDecodeGraph *g, Ctx *c, int v) {
         (void)hipGraphDestroy(g->graph_v[v]);
         g->graph_v[v] = nullptr;
     }
-    // the graph is built node by node (no stream capture): a chain of the token's kernels
+    // the graph is built node by node (no stream capture): a chain of the token's kernels, with
+    // event-record nodes between them in the stamped variants
+    std::vector<hipEvent_t> *ev = nullptr;
+    if (v >= 2) {
+        const int rc = ensure_events(g->events, (size_t)kLaunchesPerLayer * g->cfg.layers + 2);
+        if (rc) return rc;
+        ev = &g->events;
+    }
     const int rc = build_graph(F_SESSION, "decode graph", &g->graph_v[v], &g->exec_v[v], [&]() {
-        return enqueue_token(g, c->stream, g->kinds, nullptr, nullptr, false, v == 1);
+        return enqueue_token(g, c->stream, g->kinds, ev, nullptr, false, (v & 1) == 1);
     });
     if (rc) return rc;
     g->dirty_v[v] = false;
@@ -483,6 +502,7 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     M((void **)&g->final_norm, kHidden * 4);
     M((void **)&g->route_log, (size_t)cfg->layers * 8 * 4);
     M((void **)&g->route_log_w, (size_t)cfg->layers * 8 * 4);
+    M((void **)&g->forced, (size_t)cfg->layers * 8 * 4);
     for (auto &L : g->layers) M((void **)&L.input_norm, kHidden * 4);
     if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -501,14 +521,14 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *c = ctx(F_SESSION);
     if (c) (void)hipStreamSynchronize(c->stream);
-    for (int v = 0; v < 2; ++v) {
+    for (int v = 0; v < 4; ++v) {
         if (g->exec_v[v]) (void)hipGraphExecDestroy(g->exec_v[v]);
         if (g->graph_v[v]) (void)hipGraphDestroy(g->graph_v[v]);
     }
     for (hipEvent_t e : g->events) (void)hipEventDestroy(e);
     for (hipEvent_t e : g->kevents) (void)hipEventDestroy(e);
     void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
-                  g->final_norm, g->route_log, g->route_log_w};
+                  g->final_norm, g->route_log, g->route_log_w, g->forced};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     for (auto &L : g->layers)
@@ -583,12 +603,13 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     }
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
-    const int v = x_embed ? 0 : 1;
+    // graph variant: x from the host or by token id; stamped (event nodes between kernels) or not
+    const int v = (x_embed ? 0 : 1) + (g->stamps ? 2 : 0);
     g->stamps_valid = false;
     uint64_t record_ns = 0;
-    // stamps and flush_each run the same kernels as direct launches (events between them for
-    // the timeline); otherwise the captured graph is replayed
-    const bool eager = g->flush_each != 0 || g->stamps;
+    // flush_each runs the same kernels as direct launches (with stamps: events between them and
+    // each launch timed by its dispatch); otherwise the graph is replayed
+    const bool eager = g->flush_each != 0;
     if (!eager && (g->dirty_v[v] || !g->exec_v[v])) {
         const uint64_t r0 = now_ns();
         int rc = rebuild(g, c, v);
@@ -610,14 +631,14 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     if (eager) {
         std::vector<hipEvent_t> *ev = nullptr, *kev = nullptr;
         if (g->stamps) {
-            const size_t launches = 7 * (size_t)g->cfg.layers + 1;
+            const size_t launches = (size_t)kLaunchesPerLayer * g->cfg.layers + 1;
             int rc = ensure_events(g->events, launches + 1);
             if (!rc) rc = ensure_events(g->kevents, 2 * launches);
             if (rc) return rc;
             ev = &g->events;
             kev = &g->kevents;
         }
-        int rc = enqueue_token(g, c->stream, g->kinds, ev, kev, g->flush_each == 1, v == 1);
+        int rc = enqueue_token(g, c->stream, g->kinds, ev, kev, g->flush_each == 1, (v & 1) == 1);
         if (rc) return rc;
     } else {
         OMEGA_HIP(F_SESSION, hipGraphLaunch(g->exec_v[v], c->stream));
@@ -629,6 +650,7 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
     *token = argmax_from_slots(pin->argmax);
     g->stamps_valid = g->stamps;
+    g->stamps_graph = g->stamps && !eager;
     if (st) {
         memset(st, 0, sizeof(*st));
         st->launches = launches;
@@ -665,7 +687,7 @@ int omega_gpu_decode_graph_set_embedding(OmegaGpuDecodeGraph *g, const void *emb
         return OMEGA_GPU_BAD_ARGS;
     }
     g->embed = e;
-    g->dirty_v[1] = true;
+    g->dirty_v[1] = g->dirty_v[3] = true;
     return OMEGA_GPU_OK;
 }
 
@@ -762,13 +784,16 @@ int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns,
         return OMEGA_GPU_BAD_ARGS;
     }
     const uint32_t n = (uint32_t)g->kinds.size();
-    if (cap < n || g->kevents.size() < 2 * (size_t)n) {
+    if (cap < n || (!g->stamps_graph && g->kevents.size() < 2 * (size_t)n) || g->events.size() < (size_t)n + 1) {
         set_error(F_SESSION, "decode graph kernel_ns: capacity %u < %u", cap, n);
         return OMEGA_GPU_TOO_LARGE;
     }
     for (uint32_t i = 0; i < n; ++i) {
+        // graph replay: the span between the event nodes around launch i (its launch gap and its
+        // run in the replayed graph); direct launches: the dispatch's own start and end
         float ms = 0.f;
-        hipError_t e = hipEventElapsedTime(&ms, g->kevents[2 * i], g->kevents[2 * i + 1]);
+        hipError_t e = g->stamps_graph ? hipEventElapsedTime(&ms, g->events[i], g->events[i + 1])
+                                       : hipEventElapsedTime(&ms, g->kevents[2 * i], g->kevents[2 * i + 1]);
         if (e != hipSuccess) {
             set_error(F_SESSION, "decode graph kernel_ns: %s", hipGetErrorString(e));
             return OMEGA_GPU_CHIP_FAIL;
@@ -788,6 +813,26 @@ int omega_gpu_decode_graph_read_routes(OmegaGpuDecodeGraph *g, uint32_t *ids, fl
     const size_t n = (size_t)g->cfg.layers * 8;
     if (ids) OMEGA_HIP(F_SESSION, hipMemcpy(ids, g->route_log, n * 4, hipMemcpyDeviceToHost));
     if (weights) OMEGA_HIP(F_SESSION, hipMemcpy(weights, g->route_log_w, n * 4, hipMemcpyDeviceToHost));
+    return OMEGA_GPU_OK;
+}
+
+int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint32_t *ids) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g) return OMEGA_GPU_BAD_ARGS;
+    if (ids) {
+        for (uint32_t i = 0; i < g->cfg.layers * 8; ++i)
+            if (ids[i] >= kExperts) {
+                set_error(F_SESSION, "decode graph force_routes: expert id %u >= %u", ids[i], kExperts);
+                return OMEGA_GPU_BAD_ARGS;
+            }
+        Ctx *c = ctx(F_SESSION);
+        if (!c) return OMEGA_GPU_CHIP_FAIL;
+        OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
+        OMEGA_HIP(F_SESSION, hipMemcpy(g->forced, ids, (size_t)g->cfg.layers * 8 * 4, hipMemcpyHostToDevice));
+    }
+    if (g->force_on != (ids != nullptr)) g->mark_dirty();
+    g->force_on = ids != nullptr;
     return OMEGA_GPU_OK;
 }
 

@@ -106,6 +106,29 @@ __device__ __forceinline__ void route_topk_keys(uint32_t (&k)[Q], const float *l
     }
 }
 
+// Teacher forcing for parity tests: the 8 expert ids come from `forced` (slot order), the weights
+// are the softmax of this launch's own logits over that set (exp(l - max) / sum, as the ranking
+// computes them for its own set). Every lane ends with the same result.
+__device__ __forceinline__ void route_forced(const float *logits, const uint32_t *forced, Route &r) {
+    float v[kTopK];
+#pragma unroll
+    for (int s = 0; s < kTopK; ++s) {
+        r.id[s] = *as_global_u32(forced + s);
+        v[s] = *as_global_f32(logits + r.id[s]);
+    }
+    float mx = v[0];
+#pragma unroll
+    for (int s = 1; s < kTopK; ++s) mx = fmaxf(mx, v[s]);
+    float p[kTopK], sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kTopK; ++s) {
+        p[s] = expf(v[s] - mx);
+        sum += p[s];
+    }
+#pragma unroll
+    for (int s = 0; s < kTopK; ++s) r.w[s] = p[s] / sum;
+}
+
 template <int Q>
 __device__ __forceinline__ void route_topk(const float *logits, uint32_t shared, int norm_topk,
                                            int mutant, Route &r) {

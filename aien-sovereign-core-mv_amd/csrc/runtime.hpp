@@ -160,6 +160,17 @@ int build_graph(Family fam, const char *what, hipGraph_t *graph, hipGraphExec_t 
     return OMEGA_GPU_OK;
 }
 
+// While recording: an event-record node after the chain's last node (the graph's own timeline).
+inline hipError_t record_event_node(hipEvent_t ev) {
+    GraphRecorder *r = graph_recorder();
+    hipGraphNode_t node = nullptr;
+    const hipError_t e = hipGraphAddEventRecordNode(&node, r->graph, r->last ? &r->last : nullptr,
+                                                    r->last ? 1 : 0, ev);
+    if (e == hipSuccess) r->last = node;
+    else if (r->err == hipSuccess) r->err = e;
+    return e;
+}
+
 #define OMEGA_LAUNCH(kern, grid, block, shm, st, ...)                                            \
     do {                                                                                         \
         ::omega::LaunchStamp &ls_ = ::omega::launch_stamp();                                     \

@@ -264,6 +264,7 @@ SIGNATURES = {
     "omega_gpu_pf_residual_norm": (i32, [u32, u32, u64, u64, u64, f32, u64, P]),
     "omega_gpu_pf_moe_plan": (i32, [u32, u32, u32, P, P, P, P, P, P, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
+    "omega_gpu_decode_graph_test_force_routes": (i32, [P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),
     "omega_gpu_decode_graph_token_id": (i32, [P, u32, u32, U32P, C.POINTER(GraphStats)]),
@@ -760,6 +761,16 @@ class DecodeGraph:
         w = np.zeros((self.layers, 8), np.float32)
         self._rc(lib().omega_gpu_decode_graph_read_routes(self.h, ptr(ids), ptr(w)), "read_routes")
         return ids, w
+
+    def force_routes(self, ids):
+        """Teacher forcing for parity tests: [layers][8] expert ids in place of the ranking, or
+        None to turn it off."""
+        if ids is None:
+            self._rc(lib().omega_gpu_decode_graph_test_force_routes(self.h, None), "force_routes")
+            return
+        a = np.ascontiguousarray(ids, dtype=np.uint32)
+        check_len("decode graph forced routes", self.layers * 8, a.size)
+        self._rc(lib().omega_gpu_decode_graph_test_force_routes(self.h, ptr(a)), "force_routes")
 
     def set_stamps(self, on):
         lib().omega_gpu_decode_graph_set_stamps(self.h, int(on))

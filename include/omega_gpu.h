@@ -626,9 +626,16 @@ int omega_gpu_decode_graph_token_id(OmegaGpuDecodeGraph *g, uint32_t token_in, u
 /* the routed expert ids and weights of every layer of the decode graph's last token
  * ([layers][8] each; either pointer may be NULL) — a trace for parity checks */
 int omega_gpu_decode_graph_read_routes(OmegaGpuDecodeGraph *g, uint32_t *ids, float *weights);
-/* with stamps on: the duration (ns) of every launch of the last token, start to end of the
- * dispatch as the hardware recorded it (no launch gaps); returns launches or rc<0 */
+/* with stamps on, the per-launch times (ns) of the last token: replaying the graph, the span
+ * between the event-record nodes around each launch (its share of the replayed token, launch gap
+ * included); with flush_each (direct launches), start to end of each dispatch as the hardware
+ * recorded it (no launch gaps). Returns launches or rc<0 */
 int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap);
+/* Teacher forcing for parity tests (not in the reference ABI): ids [layers][8] expert ids
+ * (< 128) used by the following tokens in place of each layer's top-8 ranking, in slot order,
+ * their weights the softmax of the device's own router logits over that set; NULL turns the
+ * forcing off. Lets a full-size decode be compared with the oracle past a routing near-tie. */
+int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint32_t *ids);
 /* Batched MoE block (not in the reference ABI; the expert FFN of a decode step at token batch
  * T <= 64, the reference's per-token FP8 arm qwen3_moe_omega.rs:4287-4318 batched): for each of
  * `tokens` rows of h [T][2048] f32, RMSNorm with the router's layer weights, router logits, top-8

@@ -536,6 +536,45 @@ def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, 
     return rmsnorm(x[-1], model.final_norm(), eps), out
 
 
+def paged_step(model, pool, lay, table, pos: int, token: int, threads: int = 1):
+    """One token of one sequence through every layer with a paged KV pool as the KV store: the
+    engine step (oref_engine_step, qwen3_moe_omega.rs:4096-4345) on the HostPoolKv arm
+    (qwen3_moe_omega.rs:2925-2941): the token's bf16 K/V row is written at page table[pos / 16],
+    slot pos % 16 (write_token_kv, aien-kv-cache/src/lib.rs:586-622), then paged attention over
+    positions 0..=pos (gather_layer_kv then the f64 SDPA). pool (the aien-kv-cache bytes, uint8)
+    is updated in place. Returns (final-normed hidden, routed ids [layers][top_k], the smallest
+    gap between consecutive ranks of each layer's top top_k + 1 router logits [layers])."""
+    c = model.cfg
+    qh, kvh, hd, eps = c.q_heads, c.kv_heads, c.head_dim, c.eps
+    table = np.ascontiguousarray(table, dtype=np.int32)
+    x = bf16_to_f32(model.embed()[token % c.vocab]).astype(np.float32)
+    routes = np.zeros((c.layers, c.top_k), np.uint32)
+    gaps = np.zeros(c.layers, np.float32)
+    for l in range(c.layers):
+        xn = rmsnorm(x, model.tensor(l, 5), eps)
+        w, s = model.tensor(l, 0)
+        qkv = fp8_grouped(w, s, [0], xn, threads)[0]
+        q = rmsnorm_per_head(qkv[:qh * hd], model.tensor(l, 7), eps, qh, hd)
+        k = rmsnorm_per_head(qkv[qh * hd:(qh + kvh) * hd], model.tensor(l, 8), eps, kvh, hd)
+        v = np.ascontiguousarray(qkv[(qh + kvh) * hd:])
+        q, k = apply_rope(q, k, pos, qh, kvh, hd, c.rope_theta)
+        lib().oref_kv_write_token(ptr(pool), C.byref(lay), int(table[pos // lay.block_size]), l,
+                                  pos % lay.block_size, kvh * hd, ptr(k), ptr(v))
+        att = np.empty(qh * hd, np.float32)
+        lib().oref_paged_attention(ptr(q), ptr(pool), C.byref(lay), ptr(table), pos + 1, l, qh, kvh,
+                                   hd, ptr(att))
+        w, s = model.tensor(l, 1)
+        x = x + fp8_grouped(w, s, [0], att, threads)[0]
+        ids, wts, post, rl = route(model.tensor(l, 4), model.tensor(l, 6), x, eps, c.top_k)
+        routes[l] = ids
+        top = np.sort(rl)[::-1][:c.top_k + 1]
+        gaps[l] = float(np.min(top[:-1] - top[1:]))
+        gw, gs = model.tensor(l, 2)
+        dw, ds = model.tensor(l, 3)
+        x = x + moe_block(gw, gs, dw, ds, ids, wts, post)
+    return rmsnorm(x, model.final_norm(), eps), routes, gaps
+
+
 class Model:
     """Synthetic random-init model and the whole-step engine of the oracle."""
 

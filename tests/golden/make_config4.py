@@ -13,8 +13,11 @@ refined f64 router) runs every prompt token and every generated token one step a
 first generated token is the argmax after the last prompt token. Recorded per generated step:
 the token, the top-2 margin (own30b_check.rs:181-193), the top 16 (index, value) pairs, the
 logits at 1024 seeded vocabulary indices, the smallest rank-8 / rank-9 routing margin over the
-48 layers and its layer; plus the full logits of the first generated step and the routing
-margins of every prompt step. About 15 minutes on 8 host threads and 32 GB of memory.
+48 layers and its layer; plus the full logits of the first generated step. Recorded per processed
+token (the 512 prompt tokens, then the first 63 generated ones), per layer: the routed expert ids
+in slot order and the smallest logit gap between consecutive ranks of the top 9 (the rank-8 /
+rank-9 margin, and ln(w_k / w_k+1) inside the top 8), which bounds how close the routing was to
+changing. About 15 minutes on 8 host threads and 32 GB of memory.
 
 Run from the repository root:  python tests/golden/make_config4.py [--threads 8]
 """
@@ -36,6 +39,14 @@ PROMPT, NEW = 512, 64
 SUBSET = 1024
 
 
+def route_record(eng):
+    """(ids uint8 [48][8], smallest consecutive-rank gap of the top 9 per layer)"""
+    ids, w, m89 = eng.last_routes()
+    with np.errstate(divide="ignore"):
+        inner = np.log(w[:, :-1].astype(np.float64) / w[:, 1:].astype(np.float64)).min(axis=1)
+    return ids.astype(np.uint8), np.minimum(inner, m89.astype(np.float64)).astype(np.float32)
+
+
 def top2(logits):
     order = np.argsort(-logits, kind="stable")
     return int(order[0]), float(logits[order[0]] - logits[order[1]]), order[:16]
@@ -55,11 +66,15 @@ def main():
     prompt = np.random.default_rng(SEED).integers(0, V, PROMPT)
     subset = np.sort(np.random.default_rng(SEED + 1).choice(V, SUBSET, replace=False)).astype(np.int64)
     prompt_margin = np.empty((PROMPT, L), np.float32)
+    steps = PROMPT + NEW - 1
+    step_routes = np.zeros((steps, L, TOPK), np.uint8)
+    step_gap = np.zeros((steps, L), np.float32)
     t1 = time.time()
     hidden = None
     for p, tok in enumerate(prompt.tolist()):
         hidden = eng.step(int(tok))
         prompt_margin[p] = eng.last_routes()[2]
+        step_routes[p], step_gap[p] = route_record(eng)
         if p % 64 == 63:
             print(f"prompt {p + 1}/{PROMPT}, {(time.time() - t1) / (p + 1):.2f} s/step", flush=True)
     tokens = np.empty(NEW, np.int64)
@@ -84,6 +99,7 @@ def main():
         if s + 1 < NEW:
             hidden = eng.step(tok)
             rm = eng.last_routes()[2]
+            step_routes[PROMPT + s], step_gap[PROMPT + s] = route_record(eng)
             gen_margin[s] = rm
             route_min[s] = rm.min()
             route_layer[s] = int(rm.argmin())
@@ -96,7 +112,8 @@ def main():
                         margins=margins, top_idx=top_idx, top_val=top_val, subset=subset,
                         sub_val=sub_val, first_logits=first_logits.astype(np.float32),
                         prompt_route_margin=prompt_margin, gen_route_margin=gen_margin,
-                        route_min=route_min, route_layer=route_layer)
+                        route_min=route_min, route_layer=route_layer, step_routes=step_routes,
+                        step_gap=step_gap)
     print(f"wrote {args.out} in {time.time() - t0:.0f} s", flush=True)
 
 

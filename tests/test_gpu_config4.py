@@ -6,12 +6,25 @@ graph one token per step, then 64 greedy tokens: the workload bench.py times. Th
 values are tests/golden/config4_greedy.npz, written by tests/golden/make_config4.py from the
 oracle engine (oref_engine_step: qwen3_moe_omega.rs:4096-4345 restated).
 
-Bars, in the manner of the reference's own30b_check (crates/aien-inference-abi/src/bin/
-own30b_check.rs:181-193, 986-1006): greedy tokens identical; a first divergence passes only at a
-step whose oracle top-2 margin is below 1e-3 (recorded, not waved: the comparison stops there);
-logits within 2e-3 relative (max |gpu - cpu| over max |cpu|) at 1024 seeded vocabulary indices
-plus the oracle's top 16 at every compared step, and over the whole vocabulary at the first
-generated step; top-2 margins within the logit bar.
+The device and the oracle sum their f32 products in different orders, so their residual rows
+differ by about 1e-6 relative, and a layer whose rank-8 / rank-9 router logits sit closer than
+that can route differently; from there the two histories are different computations. The
+recorded decode has such near ties (gaps down to 6e-7 in the prompt, 3e-6 while generating).
+Hence two tests:
+
+1. Free-running: wherever the graph's routed expert set of a layer differs from the oracle's,
+   the oracle's smallest consecutive-rank gap of that layer's top 9 is below 1e-3 (a near tie);
+   every generated step up to the first routing difference while generating has the oracle's
+   token and logits (the bars of 2). A difference in the prompt only changes a few history rows,
+   and the comparison goes on through it.
+2. Routing forced to the oracle's expert ids at every step (teacher forcing through
+   omega_gpu_decode_graph_test_force_routes; the weights stay the device's own softmax over that
+   set), so both runs compute the same function: all 64 greedy tokens identical (a divergence
+   passes only at an oracle top-2 margin below 1e-3, the 1e-3 floor of the reference's
+   own30b_check, crates/aien-inference-abi/src/bin/own30b_check.rs:181-193, 986-1006), logits
+   within 2e-3 relative (max |gpu - cpu| over max |cpu|) at 1024 seeded vocabulary indices plus
+   the oracle's top 16 at every step and over the whole vocabulary at the first generated step,
+   top-2 margins within 2 x 2e-3 of max |logit|.
 """
 import os
 
@@ -20,6 +33,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+NEAR_TIE = 1e-3
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_greedy.npz")
 
 
@@ -38,48 +52,112 @@ def golden():
     return {k: z[k] for k in z.files}
 
 
-def test_config4_greedy_decode_matches_the_oracle(omega, golden):
-    seed = int(golden["seed"])
-    prompt = golden["prompt"]
-    want = golden["tokens"]
-    model = omega.SynthDecodeModel(seed, omega.round_max_pos(len(prompt) + len(want) + 8))
+@pytest.fixture(scope="module")
+def model(omega, golden):
+    m = omega.SynthDecodeModel(int(golden["seed"]), omega.round_max_pos(len(golden["prompt"]) + 72))
+    yield m
+    m.free()
+
+
+class StepCheck:
+    """The bars of one generated step against the fixture."""
+
+    def __init__(self, golden):
+        self.z = golden
+        self.worst = 0.0
+        self.worst_margin = 0.0
+        self.compared = 0
+
+    def check(self, s, tok, logits):
+        z = self.z
+        got_tok, got_margin = top2(logits)
+        assert got_tok == tok, (s, got_tok, tok)  # the graph's argmax is the lowest index of the max
+        e = max(rel_err(logits[z["subset"]], z["sub_val"][s]),
+                rel_err(logits[z["top_idx"][s]], z["top_val"][s]))
+        if s == 0:
+            e = max(e, rel_err(logits, z["first_logits"]))
+        self.worst = max(self.worst, e)
+        scale = float(np.abs(z["sub_val"][s]).max())
+        self.worst_margin = max(self.worst_margin, abs(got_margin - float(z["margins"][s])) / scale)
+        assert e <= TOL, f"step {s}: logits rel err {e:.2e}"
+        assert self.worst_margin <= 2 * TOL, f"step {s}: top-2 margin off by {self.worst_margin:.2e} of max |logit|"
+        if tok != int(z["tokens"][s]):
+            m = float(z["margins"][s])
+            assert m < NEAR_TIE, (f"greedy token {s} is {tok}, oracle {int(z['tokens'][s])} at oracle "
+                                  f"top-2 margin {m:.4f} (>= {NEAR_TIE})")
+            return False
+        self.compared += 1
+        return True
+
+
+def decode(g, golden, forced, on_step):
+    """The 512 prompt tokens, then the first 63 generated tokens, one decode step each (575
+    processed tokens); on_step(t, tok) after processed token t with the greedy token it produced
+    (generated step t - 511 from t = 511 on) returns whether to go on."""
+    prompt, routes = golden["prompt"], golden["step_routes"].astype(np.uint32)
+    n_gen = len(golden["tokens"])
+    pos, tok = 0, None
+    steps = len(prompt) + n_gen - 1
+    for t in range(steps):
+        if forced:
+            g.force_routes(routes[t])
+        tok_in = int(prompt[t]) if t < len(prompt) else tok
+        tok, _ = g.token_id(tok_in, pos)
+        pos += 1
+        if not on_step(t, tok):
+            return
+
+
+def test_config4_free_running_matches_until_a_near_tie(omega, golden, model):
     g = model.graph
-    try:
-        pos = 0
-        tok = None
-        for t in prompt.tolist():
-            tok, _ = g.token_id(int(t), pos)
-            pos += 1
-        subset = golden["subset"]
-        worst = 0.0
-        worst_margin = 0.0
-        compared = 0
-        for s in range(len(want)):
+    g.force_routes(None)
+    chk = StepCheck(golden)
+    npr = len(golden["prompt"])
+    flips = []
+
+    def on_step(t, tok):
+        ids, _ = g.read_routes()
+        want = golden["step_routes"][t]
+        differs = False
+        for l in range(ids.shape[0]):
+            if set(ids[l].tolist()) != set(want[l].tolist()):
+                gap = float(golden["step_gap"][t, l])
+                flips.append((t, l, gap))
+                assert gap < NEAR_TIE, f"step {t} layer {l}: routing differs at an oracle gap of {gap:.2e}"
+                differs = True
+        if t >= npr - 1:
+            s = t - (npr - 1)
             _, _, logits = g.read(logits=True)
-            got_tok, got_margin = top2(logits)
-            assert got_tok == tok, (s, got_tok, tok)  # the graph's argmax is the lowest index of the max
-            e_sub = rel_err(logits[subset], golden["sub_val"][s])
-            e_top = rel_err(logits[golden["top_idx"][s]], golden["top_val"][s])
-            worst = max(worst, e_sub, e_top)
-            scale = float(np.abs(golden["sub_val"][s]).max())
-            worst_margin = max(worst_margin, abs(got_margin - float(golden["margins"][s])) / scale)
-            if s == 0:
-                e_full = rel_err(logits, golden["first_logits"])
-                assert e_full <= TOL, f"full logits of the first generated step: rel err {e_full:.2e}"
-            if tok != int(want[s]):
-                m = float(golden["margins"][s])
-                assert m < 1e-3, (f"greedy token {s} is {tok}, oracle {int(want[s])} at oracle "
-                                  f"top-2 margin {m:.4f} (>= 1e-3)")
-                print(f"diverged at step {s}, oracle margin {m:.2e} (below the 1e-3 floor)")
-                break
-            compared += 1
-            assert worst <= TOL, f"step {s}: logits rel err {worst:.2e}"
-            assert worst_margin <= 2 * TOL, f"step {s}: top-2 margin off by {worst_margin:.2e} of max |logit|"
-            if s + 1 < len(want):
-                tok, _ = g.token_id(tok, pos)
-                pos += 1
-        print(f"config 4: {compared} greedy tokens identical, logits rel err <= {worst:.2e}, "
-              f"margins within {worst_margin:.2e} of max |logit|; oracle margins min "
-              f"{float(golden['margins'].min()):.3e}")
+            # a routing difference while generating changes the next step's logits: stop there
+            return chk.check(s, tok, logits) and not differs
+        return True
+
+    decode(g, golden, False, on_step)
+    print(f"free-running: routing differences (step, layer, oracle gap) {flips}; "
+          f"{chk.compared} generated steps identical, logits rel err <= {chk.worst:.2e}")
+
+
+def test_config4_forced_routing_matches_every_step(omega, golden, model):
+    g = model.graph
+    chk = StepCheck(golden)
+    npr = len(golden["prompt"])
+    n_gen = len(golden["tokens"])
+    state = {"diverged": None}
+
+    def on_step(t, tok):
+        if t >= npr - 1:
+            s = t - (npr - 1)
+            _, _, logits = g.read(logits=True)
+            if not chk.check(s, tok, logits):
+                state["diverged"] = s
+                return False
+        return True
+
+    try:
+        decode(g, golden, True, on_step)
     finally:
-        model.free()
+        g.force_routes(None)
+    print(f"forced routing: {chk.compared} of {n_gen} greedy tokens identical (divergence at "
+          f"{state['diverged']}), logits rel err <= {chk.worst:.2e}, margins within "
+          f"{chk.worst_margin:.2e} of max |logit|")
+    assert state["diverged"] is not None or chk.compared == n_gen

@@ -248,3 +248,21 @@ def test_paged_attention_against_a_hand_walked_gather(oracle):
     oracle.lib().oref_paged_attention(oracle.ptr(q), oracle.ptr(pool), C.byref(lay),
                                       oracle.ptr(table[::-1].copy()), ctx, layer, QH, KVH, HD, oracle.ptr(alt))
     assert np.abs(alt - want.reshape(-1)).max() > 1e-3
+
+
+def test_paged_step_equals_the_engine_step(oracle, model):
+    """pyoracle.paged_step (the engine step with the paged pool as its KV store, the oracle of the
+    batched serving step) against oref_engine_step (the fused-cache store): the same arithmetic on
+    the same bf16 rows, so hidden rows and routes are bit-identical at every position, whatever
+    pages the table names."""
+    rng = np.random.default_rng(6)
+    blocks = 64
+    lay = oracle.kv_layout(blocks, 16, L, KVH, HD)
+    pool = np.zeros(lay.pool_bytes, np.uint8)
+    table = rng.permutation(blocks)[:4].astype(np.int32)
+    eng = oracle.Engine(model, 64, refined_router=True, threads=8)
+    for pos, tok in enumerate([5, 17, 42, 3, 9, 60, 1, 8191, 600, 77, 5, 5, 13, 21, 34, 55, 89, 144]):
+        want = eng.step(tok)
+        got, routes, _ = oracle.paged_step(model, pool, lay, table, pos, tok, threads=8)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(routes, eng.last_routes()[0])
