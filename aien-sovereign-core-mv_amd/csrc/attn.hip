@@ -128,8 +128,10 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
     uint32_t active, pps;
     attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
-    if (s >= active) return;
-    const uint32_t p_begin = s * pps, p_end = min(pages, p_begin + pps);
+    // splits 0..7 of every kv head stay to merge one q head each, with or without pages
+    if (s >= active && s >= 8) return;
+    const bool holds = s < active;
+    const uint32_t p_begin = holds ? s * pps : 0, p_end = holds ? min(pages, p_begin + pps) : 0;
 
     // Every load below is issued unconditionally, the page stream last: vector-memory waits
     // complete in issue order and merge conservatively at branch joins, so a conditional load
@@ -254,18 +256,73 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
             for (int nb = 0; nb < 4; ++nb) ov[nb][i] = fmaf(pi, vs[16 * (nb + nb_off) + n], ov[nb][i] * ai);
         }
     }
+    const uint32_t epoch = a.epoch_dev ? *as_global_u32(a.epoch_dev) * 64u + a.layer : a.epoch_host;
     float *part = a.part + ((size_t)h * 8 * kDattnSplits + s) * kPartStride;
+    if (holds) {
+        // the partial goes where every CU reads it (agent-scope stores write through the XCD's
+        // L2); once the stores are acknowledged the split's flag carries this launch's epoch
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float *pp = part + (size_t)(4 * hg + i) * kDattnSplits * kPartStride;
+        for (int i = 0; i < 4; ++i) {
+            float *pp = part + (size_t)(4 * hg + i) * kDattnSplits * kPartStride;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) pp[4 + 16 * (nb + nb_off) + n] = ov[nb][i];
+            for (int nb = 0; nb < 4; ++nb)
+                __hip_atomic_store(pp + 4 + 16 * (nb + nb_off) + n, ov[nb][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane < 8) {  // lane r holds head r's running max and sum
+            float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
+            __hip_atomic_store(pp, m_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 1, l_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0) __hip_atomic_store(a.flags + h * kDattnSplits + s, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (lane < 8) {  // lane r holds head r's running max and sum
-        float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
-        pp[0] = m_l;
-        pp[1] = l_l;
+    if (s >= 8) return;
+    // Merge of q head 8 h + s: wait until every split of kv head h has flagged this epoch (every
+    // split is resident: at most 4 x 64 one-wavefront workgroups), with a bounded number of polls
+    // (a wait that runs out is counted and the merge goes on), then the split-order merge
+    // out = sum w_i o_i / sum w_i l_i with w_i = exp(m_i - max m); lane l holds dims l, l + 64.
+    {
+        const uint32_t *fl = a.flags + h * kDattnSplits;
+        uint32_t spins = 0;
+        while (true) {
+            const uint32_t f = lane < active ? __hip_atomic_load(fl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                             : epoch;
+            if (__all(f == epoch)) break;
+            if (++spins >= kDattnMergeSpins) {
+                if (lane == 0) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
     }
+    const uint32_t hq = h * 8 + s;
+    const float *base = a.part + (size_t)hq * kDattnSplits * kPartStride;
+    const uint32_t j = min(lane, active - 1);
+    const float mj = __hip_atomic_load(base + (size_t)j * kPartStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float lj = __hip_atomic_load(base + (size_t)j * kPartStride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float mv = lane < active ? mj : -INFINITY;
+    float M = row16_max(mv);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    const float wj = lane < active ? (a.mutant == 4 ? 1.f : expf(mj - M)) : 0.f;
+    const float L = wave_sum(wj * (lane < active ? lj : 0.f));
+    float o0 = 0.f, o1 = 0.f;
+    for (uint32_t c0 = 0; c0 < active; c0 += 16) {
+        float x0[16], x1[16];
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t si = min(c0 + i, active - 1);
+            x0[i] = __hip_atomic_load(base + (size_t)si * kPartStride + 4 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            x1[i] = __hip_atomic_load(base + (size_t)si * kPartStride + 68 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const float wi = c0 + i < active ? readlane_f32(wj, (int)(c0 + i)) : 0.f;
+            o0 = fmaf(wi, x0[i], o0);
+            o1 = fmaf(wi, x1[i], o1);
+        }
+    }
+    a.out[hq * 128 + lane] = o0 * (a.out_scale / L);
+    a.out[hq * 128 + 64 + lane] = o1 * (a.out_scale / L);
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
@@ -1223,6 +1280,8 @@ struct OmegaGpuDecodeAttnCache {
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_pos][64]
     // call buffers of the standalone entry
     float *qkv = nullptr, *out = nullptr, *part = nullptr;
+    uint32_t *flags = nullptr;  // [4 * 64 split flags][1 error count] of the standalone calls
+    uint32_t epoch = 0;         // of the standalone calls (each call takes the next)
 };
 
 using namespace omega;
@@ -1298,6 +1357,8 @@ int omega_gpu_decode_attn_cache_alloc(uint32_t layers, uint32_t max_pos, double 
     if (e == hipSuccess) e = hipMalloc(&c->qkv, 5120 * 4);
     if (e == hipSuccess) e = hipMalloc(&c->out, 4096 * 4);
     if (e == hipSuccess) e = hipMalloc(&c->part, (size_t)32 * kDattnSplits * kPartStride * 4);
+    if (e == hipSuccess) e = hipMalloc(&c->flags, (4 * kDattnSplits + 1) * 4);
+    if (e == hipSuccess) e = hipMemset(c->flags, 0, (4 * kDattnSplits + 1) * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         set_error(F_DATTN, "decode attn cache alloc (%u layers x %u): %s", layers, max_pos,
@@ -1314,7 +1375,7 @@ void omega_gpu_decode_attn_cache_free(OmegaGpuDecodeAttnCache *c) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *cx = ctx(F_DATTN);
     if (cx) (void)hipStreamSynchronize(cx->stream);
-    void *ps[] = {c->pool, c->q_norm, c->k_norm, c->rope_cos, c->rope_sin, c->qkv, c->out, c->part};
+    void *ps[] = {c->pool, c->q_norm, c->k_norm, c->rope_cos, c->rope_sin, c->qkv, c->out, c->part, c->flags};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     delete c;
@@ -1362,22 +1423,23 @@ int omega_gpu_decode_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t p
     OMEGA_HIP(F_DATTN, hipMemcpyAsync(c->qkv, cx->pin, 5120 * 4, hipMemcpyHostToDevice, cx->stream));
     DattnArgs a = cache_dattn(c, layer, eps, c->qkv, c->part);
     a.pos_host = pos;
-    CombineArgs cb;
-    cb.part = c->part;
-    cb.splits = kDattnSplits;
-    cb.pos_host = pos;
-    cb.tiles_per_split = a.tiles_per_split;
-    cb.tile_tokens = kDattnPage;
-    cb.qh = 32;
-    cb.out_scale = out_scale;
-    cb.out = c->out;
-    cb.mutant = a.mutant;
+    a.flags = c->flags;
+    a.errc = c->flags + 4 * kDattnSplits;
+    a.epoch_host = ++c->epoch == 0 ? ++c->epoch : c->epoch;
+    a.out = c->out;
+    a.out_scale = out_scale;
     OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev0, cx->stream));
     OMEGA_HIP(F_DATTN, launch_dattn(a, cx->stream));
-    OMEGA_HIP(F_DATTN, launch_attn_combine(cb, cx->stream));
     OMEGA_HIP(F_DATTN, hipEventRecord(cx->ev1, cx->stream));
     OMEGA_HIP(F_DATTN, hipMemcpyAsync(cx->pin, c->out, 4096 * 4, hipMemcpyDeviceToHost, cx->stream));
+    uint32_t *errc = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(cx->pin) + 4096 * 4);
+    OMEGA_HIP(F_DATTN, hipMemcpyAsync(errc, a.errc, 4, hipMemcpyDeviceToHost, cx->stream));
     OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
+    if (*errc) {
+        set_error(F_DATTN, "decode attn: the split merge ran out of waits (%u)", *errc);
+        OMEGA_HIP(F_DATTN, hipMemset(a.errc, 0, 4));
+        return OMEGA_GPU_CHIP_FAIL;
+    }
     memcpy(out, cx->pin, 4096 * 4);
     if (info) {
         uint32_t active, tps;

@@ -5,22 +5,23 @@
 // norm, the bf16 lm_head and the argmax; the greedy token is the lowest index of the max. The
 // residual row stays on the device for the whole token.
 //
-// MI355X shape: seven launches per layer, none of which waits on another workgroup of its own
-// launch (every cross-workgroup reduction sits at a launch boundary):
+// MI355X shape: six launches per layer. Every cross-workgroup reduction sits at a launch
+// boundary, except the attention's split merge: eight split workgroups of each kv head wait
+// (bounded) for that head's splits to flag their partials, all splits being resident at once:
 //   1. q|k|v GEMV, the input RMSNorm in its prologue (layer 0 in token-id mode also gathers the
 //      embedding row and publishes it as the residual),
 //   2. matrix-core flash-decoding over the cache: q/k RMSNorm + RoPE in its prologue, this
-//      token's K/V append, one wavefront per (64-token tile range, kv head),
-//   3. the combine of the attention splits,
-//   4. o GEMV whose epilogue adds into the residual row,
-//   5. router logits (post-attention RMSNorm, exact f64 dot products),
-//   6. gate|up GEMV of the 8 routed experts: the top-8 ranking in its prologue (one wavefront
+//      token's K/V append, one wavefront per (16-token page range, kv head), then the split merge,
+//   3. o GEMV whose epilogue adds into the residual row,
+//   4. router logits (post-attention RMSNorm, exact f64 dot products),
+//   5. gate|up GEMV of the 8 routed experts: the top-8 ranking in its prologue (one wavefront
 //      per workgroup ranks, LDS shares), SwiGLU in its epilogue,
-//   7. down GEMV: one workgroup = the 8 experts' wavefronts for 8 rows, combined in slot order
+//   6. down GEMV: one workgroup = the 8 experts' wavefronts for 8 rows, combined in slot order
 //      in LDS and added into the residual,
-// then the lm_head with the final RMSNorm in its prologue and the argmax folded in: 7L + 1
+// then the lm_head with the final RMSNorm in its prologue and the argmax folded in: 6L + 1
 // launches built once as a hipGraph (kernel nodes in a chain) and replayed per token. The
-// position and token id live in device memory, so one graph serves every token.
+// position, token id and epoch live in device memory, so one graph serves every token.
+#include <cstddef>
 #include <cstdio>
 #include <vector>
 
@@ -40,7 +41,7 @@ uint32_t cache_layers(const OmegaGpuDecodeAttnCache *c);
 uint32_t cache_max_pos(const OmegaGpuDecodeAttnCache *c);
 
 constexpr uint32_t kHidden = 2048, kInter = 768, kExperts = 128;
-constexpr uint32_t kLaunchesPerLayer = 7;
+constexpr uint32_t kLaunchesPerLayer = 6;
 
 // ---------------------------------------------------------------- gate|up + SwiGLU
 struct GateUpArgs {
@@ -204,11 +205,15 @@ struct GLayer {
 const char *kKindNames[12] = {"norm", "qkv", "attn", "o_proj", "res_add", "router",
                               "gate_up", "swiglu", "down", "combine_norm", "lm_head", "argmax"};
 
-// device words the host writes before every token: pos, token id, then the argmax slots
+// device words the host writes before every token: pos, token id, the token's epoch (the
+// attention's split flags), then the words it reads back: the count of attention waits that ran
+// out, the argmax slots
 struct GraphIo {
     uint32_t pos;
     uint32_t tok;
-    uint32_t pad[14];
+    uint32_t epoch;
+    uint32_t merge_err;
+    uint32_t pad[12];
     unsigned long long argmax[kArgmaxSlots];
 };
 
@@ -228,6 +233,8 @@ struct OmegaGpuDecodeGraph {
     GraphIo *io = nullptr;
     uint32_t *route_log = nullptr;  // [layers][8] routed ids of the last token
     uint32_t *forced = nullptr;     // [layers][8] forced expert ids (parity tests), when force_on
+    uint32_t *flags = nullptr;      // [4][64] the attention's split flags (epochs)
+    uint32_t epoch = 0;             // of the last token
     bool force_on = false;
     float *route_log_w = nullptr;   // [layers][8] their weights
     GraphIo *pin = nullptr;         // pinned host twin of io
@@ -308,24 +315,16 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         arm();
         OMEGA_HIP(F_SESSION, launch_fp8_rows(a, EPI_STORE, xsrc, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_QKV));
-        // 2. attention (q/k norm + RoPE, K/V append) and 3. the split combine
+        // 2. attention (q/k norm + RoPE, K/V append) with the split merge in the same launch
         DattnArgs da = cache_dattn(g->cache, l, eps, g->qkv, g->part);
         da.pos_dev = pos_dev;
+        da.flags = g->flags;
+        da.errc = &g->io->merge_err;
+        da.epoch_dev = &g->io->epoch;
+        da.out = g->attn;
+        da.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
         arm();
         OMEGA_HIP(F_SESSION, launch_dattn(da, st));
-        OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
-        CombineArgs cb;
-        cb.part = g->part;
-        cb.splits = kDattnSplits;
-        cb.pos_dev = pos_dev;
-        cb.tiles_per_split = da.tiles_per_split;
-        cb.tile_tokens = kDattnPage;
-        cb.qh = 32;
-        cb.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
-        cb.out = g->attn;
-        cb.mutant = da.mutant;
-        arm();
-        OMEGA_HIP(F_SESSION, launch_attn_combine(cb, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));
         // 4. o projection into the residual
         Fp8RowsArgs o;
@@ -503,6 +502,7 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     M((void **)&g->route_log, (size_t)cfg->layers * 8 * 4);
     M((void **)&g->route_log_w, (size_t)cfg->layers * 8 * 4);
     M((void **)&g->forced, (size_t)cfg->layers * 8 * 4);
+    M((void **)&g->flags, 4 * kDattnSplits * 4);
     for (auto &L : g->layers) M((void **)&L.input_norm, kHidden * 4);
     if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -528,7 +528,7 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
     for (hipEvent_t e : g->events) (void)hipEventDestroy(e);
     for (hipEvent_t e : g->kevents) (void)hipEventDestroy(e);
     void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
-                  g->final_norm, g->route_log, g->route_log_w, g->forced};
+                  g->final_norm, g->route_log, g->route_log_w, g->forced, g->flags};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     for (auto &L : g->layers)
@@ -621,6 +621,8 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     memset(pin, 0, sizeof(GraphIo));
     pin->pos = pos;
     pin->tok = token_in;
+    if (++g->epoch >= (1u << 26)) g->epoch = 1;  // epoch * 64 + layer stays a distinct 32-bit word
+    pin->epoch = g->epoch;
     float *xin = reinterpret_cast<float *>(pin + 1);
     OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->io, pin, sizeof(GraphIo), hipMemcpyHostToDevice, c->stream));
     if (x_embed) {
@@ -645,9 +647,14 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     }
     const uint32_t launches = (uint32_t)g->kinds.size();
     OMEGA_HIP(F_SESSION, hipEventRecord(c->ev1, c->stream));
-    OMEGA_HIP(F_SESSION, hipMemcpyAsync(pin->argmax, g->io->argmax, sizeof(pin->argmax),
-                                        hipMemcpyDeviceToHost, c->stream));
+    OMEGA_HIP(F_SESSION, hipMemcpyAsync(&pin->merge_err, &g->io->merge_err,
+                                        sizeof(GraphIo) - offsetof(GraphIo, merge_err), hipMemcpyDeviceToHost,
+                                        c->stream));
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
+    if (pin->merge_err) {
+        set_error(F_SESSION, "decode graph: the attention's split merge ran out of waits (%u)", pin->merge_err);
+        return OMEGA_GPU_CHIP_FAIL;
+    }
     *token = argmax_from_slots(pin->argmax);
     g->stamps_valid = g->stamps;
     g->stamps_graph = g->stamps && !eager;

@@ -143,8 +143,20 @@ struct DattnArgs {
     uint32_t pos_host = 0;
     uint32_t tiles_per_split = 0;    // pages per split; 0: spread over every split
     float *part = nullptr;           // [32][kDattnSplits][kPartStride]
-    int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written
+    // The split merge in the same launch: split s of kv head h, once its partial is stored, sets
+    // flags[h * kDattnSplits + s] to this launch's epoch; splits 0..7 of a kv head then wait for
+    // every split of the head and each merges q head 8 h + s into out. The epoch is unique per
+    // launch among the launches that share `flags` (epoch_dev * 64 + layer, or epoch_host when
+    // epoch_dev is null); *errc counts waits that ran out of spins.
+    uint32_t *flags = nullptr;       // [4 * kDattnSplits]
+    uint32_t *errc = nullptr;
+    const uint32_t *epoch_dev = nullptr;
+    uint32_t epoch_host = 0;
+    float *out = nullptr;            // [32][128]
+    float out_scale = 1.0f;
+    int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written; 4: maxima ignored
 };
+constexpr uint32_t kDattnMergeSpins = 1u << 22;  // bounded wait of the split merge (seconds)
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st);
 
 // Paged flash-decoding over an external pool: grid (splits, kv heads, seqs), one wavefront

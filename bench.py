@@ -51,10 +51,9 @@ def algorithmic_bytes(kind, ctx):
     if kind == "qkv":          # 5120 x 2048 e4m3 + scales + x + norm weights + q|k|v out
         return 5120 * 2048 + 40 * 16 * 4 + 2 * H * 4 + 5120 * 4
     splits = min(64, max(1, -(-(ctx - 1) // 16)))
-    if kind == "attn":         # K and V of 4 heads over ctx positions + q|k|v in + partials out
-        return 2 * KVH * ctx * HD * 2 + 5120 * 4 + QH * splits * 132 * 4
-    if kind == "attn_combine":  # the split partials in, the attention row out
-        return QH * splits * 132 * 4 + 4096 * 4
+    if kind == "attn":         # K and V of 4 heads over ctx positions + q|k|v in + the split
+        # partials out and back in for the merge + the attention row out
+        return 2 * KVH * ctx * HD * 2 + 5120 * 4 + 2 * QH * splits * 132 * 4 + 4096 * 4
     if kind == "o_proj":       # 2048 x 4096 e4m3 + scales + attention row + residual read/write
         return 2048 * 4096 + 16 * 32 * 4 + 4096 * 4 + 2 * H * 4
     if kind == "router":       # bf16 gate + norm weights + x in + x' out + logits
@@ -69,7 +68,7 @@ def algorithmic_bytes(kind, ctx):
 
 
 # the decode graph's launches per layer, in order, then the lm_head
-LAYER_KINDS = ["qkv", "attn", "attn_combine", "o_proj", "router", "gate_up", "down"]
+LAYER_KINDS = ["qkv", "attn", "o_proj", "router", "gate_up", "down"]
 
 
 def build_model(om, max_pos):

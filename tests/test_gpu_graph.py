@@ -111,7 +111,7 @@ def run_both(oracle, m, g, prompt, new_tokens, max_pos=256, log=None):
         if pos >= len(prompt):
             seq.append(gt)
         toks.append(gt)
-        assert st.launches == 7 * m.cfg.layers + 1 and st.submits == 1
+        assert st.launches == 6 * m.cfg.layers + 1 and st.submits == 1
     return toks, margins, worst, flips
 
 
@@ -155,11 +155,11 @@ def test_stamps_time_every_launch(omega, small):
     g.graph.set_stamps(False)
     # every launch's own duration, inside the token's span
     assert len(ns) == len(kinds) and (ns > 0).all() and ns.sum() <= st[-1]
-    assert len(kinds) == 7 * m.cfg.layers + 1
+    assert len(kinds) == 6 * m.cfg.layers + 1
     assert (np.diff(st.astype(np.int64)) >= 0).all()
-    names = [omega.kind_name(int(k)) for k in kinds[:7]]
-    # the attention and its split combine are both "attn"
-    assert names == ["qkv", "attn", "attn", "o_proj", "router", "gate_up", "down"]
+    names = [omega.kind_name(int(k)) for k in kinds[:6]]
+    # the attention merges its splits in the same launch
+    assert names == ["qkv", "attn", "o_proj", "router", "gate_up", "down"]
     assert omega.kind_name(int(kinds[-1])) == "lm_head"
 
 
