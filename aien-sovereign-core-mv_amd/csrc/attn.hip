@@ -2141,19 +2141,58 @@ int omega_gpu_paged_attention_batch_bf16(const float *q, const void *pool,
                        layer_idx, num_q_heads, num_kv_heads, out, info);
 }
 
-int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev,
-                                        const OmegaGpuKvLayout *layout,
-                                        const int32_t *block_tables_dev,
-                                        const int32_t *context_lens_dev,
-                                        uint32_t max_blocks_per_seq, uint32_t num_seqs,
-                                        uint32_t max_context, uint32_t layer_idx,
-                                        uint32_t num_q_heads, uint32_t num_kv_heads,
-                                        uint32_t head_dim, float *out_dev) {
-    std::lock_guard<std::recursive_mutex> lk(big_lock());
-    clear_error(F_ATTN);
+// ------------------------------------------------- the same attention without any allocation
+// For callers that cannot allocate (graph capture, fixed serving loops): the split partials live
+// in `scratch`, a file-scope device array of kNoAllocScratchBytes that every GPU the library runs
+// on holds until the process ends. In host code `scratch` names a host-side stand-in, so the
+// kernels get the device address hipGetSymbolAddress returns for it, fetched once per device
+// (with that device current) on the entry point's first call there. The partials need no
+// clearing: the combine reads only splits that the attention launch of the same call writes.
+namespace omega {
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+}  // namespace omega
+
+static __device__ __align__(256) float scratch[omega::kNoAllocScratchBytes / sizeof(float)];
+
+namespace omega {
+namespace {
+constexpr int kNoAllocDevices = 64;
+static float *g_scratch_dev[kNoAllocDevices];  // device address of `scratch` per device, or null
+
+static int noalloc_scratch(Ctx *cx, float **out) {
+    if (cx->device < 0 || cx->device >= kNoAllocDevices) {
+        set_error(F_ATTN, "paged attention noalloc: device %d outside 0..%d", cx->device, kNoAllocDevices - 1);
+        return OMEGA_GPU_ATTN_CHIP_FAIL;
+    }
+    if (!g_scratch_dev[cx->device]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != cx->device) e = hipSetDevice(cx->device);
+        void *p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur >= 0 && cur != cx->device) (void)hipSetDevice(cur);
+        if (e != hipSuccess || !p) {
+            set_error(F_ATTN, "paged attention noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                      cx->device, hipGetErrorString(e));
+            return OMEGA_GPU_ATTN_CHIP_FAIL;
+        }
+        g_scratch_dev[cx->device] = static_cast<float *>(p);
+    }
+    *out = g_scratch_dev[cx->device];
+    return OMEGA_GPU_ATTN_OK;
+}
+
+// The device-pointer batched attention. Its split partials go to the library's scratch (grown as
+// needed), or with `noalloc` to `scratch`, and then a shape whose partials exceed
+// kNoAllocScratchBytes is refused with TOO_LARGE.
+static int paged_batch_dev(const char *what, const float *q_dev, const void *pool_dev, const OmegaGpuKvLayout *layout,
+                           const int32_t *block_tables_dev, const int32_t *context_lens_dev,
+                           uint32_t max_blocks_per_seq, uint32_t num_seqs, uint32_t max_context,
+                           uint32_t layer_idx, uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                           float *out_dev, bool noalloc) {
     if (!q_dev || !pool_dev || !layout || !block_tables_dev || !context_lens_dev || !out_dev ||
         num_seqs == 0 || max_context == 0) {
-        set_error(F_ATTN, "paged attention dev: NULL pointer or empty batch");
+        set_error(F_ATTN, "%s: NULL pointer or empty batch", what);
         return OMEGA_GPU_ATTN_BAD_ARGS;
     }
     int rc = check_attn_shape(num_q_heads, num_kv_heads, head_dim);
@@ -2165,8 +2204,20 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     uint32_t unit = kAttnTile;
     const uint32_t splits = paged_splits(max_context, num_seqs, num_kv_heads,
                                          paged_mfma(num_q_heads, num_kv_heads, layout->block_size), unit);
-    if (!ensure_scratch(F_ATTN, cx, (size_t)num_seqs * num_q_heads * splits * kPartStride * 4))
-        return OMEGA_GPU_ATTN_CHIP_FAIL;
+    const size_t part_bytes = (size_t)num_seqs * num_q_heads * splits * kPartStride * 4;
+    float *part = nullptr;
+    if (noalloc) {
+        if (part_bytes > kNoAllocScratchBytes) {
+            set_error(F_ATTN, "%s: %u sequences x %u q heads x %u splits need %zu bytes of partials, the "
+                      "static scratch holds %zu", what, num_seqs, num_q_heads, splits, part_bytes, kNoAllocScratchBytes);
+            return OMEGA_GPU_ATTN_TOO_LARGE;
+        }
+        rc = noalloc_scratch(cx, &part);
+        if (rc) return rc;
+    } else {
+        if (!ensure_scratch(F_ATTN, cx, part_bytes)) return OMEGA_GPU_ATTN_CHIP_FAIL;
+        part = static_cast<float *>(cx->scratch);
+    }
     AttnArgs a;
     a.q = q_dev;
     a.pool = static_cast<const uint8_t *>(pool_dev);
@@ -2179,7 +2230,7 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     a.qh = num_q_heads;
     a.kvh = num_kv_heads;
     a.splits = splits;
-    a.part = static_cast<float *>(cx->scratch);
+    a.part = part;
     a.mutant = knobs().dattn_mutant;
     CombineArgs cb;
     cb.part = a.part;
@@ -2193,6 +2244,38 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
     OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
     OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
     return OMEGA_GPU_ATTN_OK;
+}
+}  // namespace
+}  // namespace omega
+
+int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev,
+                                        const OmegaGpuKvLayout *layout,
+                                        const int32_t *block_tables_dev,
+                                        const int32_t *context_lens_dev,
+                                        uint32_t max_blocks_per_seq, uint32_t num_seqs,
+                                        uint32_t max_context, uint32_t layer_idx,
+                                        uint32_t num_q_heads, uint32_t num_kv_heads,
+                                        uint32_t head_dim, float *out_dev) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_ATTN);
+    return paged_batch_dev("paged attention dev", q_dev, pool_dev, layout, block_tables_dev, context_lens_dev,
+                           max_blocks_per_seq, num_seqs, max_context, layer_idx, num_q_heads, num_kv_heads,
+                           head_dim, out_dev, false);
+}
+
+int omega_gpu_paged_attention_batch_dev_noalloc(const float *q_dev, const void *pool_dev,
+                                                const OmegaGpuKvLayout *layout,
+                                                const int32_t *block_tables_dev,
+                                                const int32_t *context_lens_dev,
+                                                uint32_t max_blocks_per_seq, uint32_t num_seqs,
+                                                uint32_t max_context, uint32_t layer_idx,
+                                                uint32_t num_q_heads, uint32_t num_kv_heads,
+                                                uint32_t head_dim, float *out_dev) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_ATTN);
+    return paged_batch_dev("paged attention noalloc", q_dev, pool_dev, layout, block_tables_dev, context_lens_dev,
+                           max_blocks_per_seq, num_seqs, max_context, layer_idx, num_q_heads, num_kv_heads,
+                           head_dim, out_dev, true);
 }
 
 int omega_gpu_paged_attention_items_dev(const float *q_dev, const void *pool_dev, const OmegaGpuKvLayout *layout,

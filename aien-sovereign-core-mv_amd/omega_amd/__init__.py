@@ -242,6 +242,8 @@ SIGNATURES = {
     "omega_gpu_fp8_gemv_dev": (i32, [P, u32, P, P]),
     "omega_gpu_paged_attention_batch_dev": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
                                                   u32, u32, u32, u32, P]),
+    "omega_gpu_paged_attention_batch_dev_noalloc": (i32, [P, P, C.POINTER(KvLayout), P, P, u32, u32, u32,
+                                                          u32, u32, u32, u32, P]),
     "omega_gpu_paged_attention_items_dev": (i32, [P, P, C.POINTER(KvLayout), P, u32, P, u32, u32, P]),
     # whole-prompt prefill (crates/aien-omega-pf/src/lib.rs:384-456, :542-571)
     "omega_gpu_pf_rc_name": (cstr, [i32]),

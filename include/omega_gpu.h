@@ -607,6 +607,23 @@ int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev
                                         uint32_t max_context, uint32_t layer_idx,
                                         uint32_t num_q_heads, uint32_t num_kv_heads,
                                         uint32_t head_dim, float *out_dev);
+/* No counterpart in the reference: omega_gpu_paged_attention_batch_dev for callers that cannot
+ * allocate device memory (code under HIP graph capture, fixed serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results; the split partials live in a static device
+ * array of 16 MiB (per GPU, held until the process ends) instead of the library's growable
+ * scratch, and the call makes no hipMalloc / hipFree. A shape whose partials exceed it
+ * (num_seqs x num_q_heads x splits x 528 bytes) is refused with OMEGA_GPU_ATTN_TOO_LARGE before
+ * any device work. Every call on one GPU shares the array: calls run in order on the library's
+ * stream, but a replay of a graph holding this call that overlaps another such call on the same
+ * GPU races on it. */
+int omega_gpu_paged_attention_batch_dev_noalloc(const float *q_dev, const void *pool_dev,
+                                                const OmegaGpuKvLayout *layout,
+                                                const int32_t *block_tables_dev,
+                                                const int32_t *context_lens_dev,
+                                                uint32_t max_blocks_per_seq, uint32_t num_seqs,
+                                                uint32_t max_context, uint32_t layer_idx,
+                                                uint32_t num_q_heads, uint32_t num_kv_heads,
+                                                uint32_t head_dim, float *out_dev);
 /* The batched serving step's attention on its own (not in the reference ABI; the ragged batch of
  * paged_attention_batch_bf16, crates/aien-omega-gpu/src/lib.rs:910-1041, with GQA 32 q / 4 kv
  * heads of 128 over 16-token pages): sequence s attends over positions 0..=positions[s] (host
