@@ -188,3 +188,80 @@ def test_gemm_is_bit_identical_to_the_gemv_per_row(omega, oracle):
     with pytest.raises(omega.OmegaGpuError):
         t.gemm_f32(eids[::-1].copy(), rows, x)     # unsorted
     t.free()
+
+
+def config2_rows(rng, tokens, experts):
+    """The row table of a batched MoE step: each token's 8 distinct experts, sorted by expert
+    (stable: rows of one expert keep token order)."""
+    eids = np.concatenate([rng.choice(experts, 8, replace=False) for _ in range(tokens)]).astype(np.uint32)
+    toks = np.repeat(np.arange(tokens, dtype=np.uint32), 8)
+    order = np.argsort(eids, kind="stable")
+    return eids[order], toks[order]
+
+
+@pytest.mark.parametrize("n,k", [(1536, 2048), (2048, 768)])
+def test_gemm_config2_row_table_against_the_oracle(omega, oracle, n, k):
+    # configuration 2 at T = 32: 256 rows over ~112 of the 128 experts (gate|up, then down);
+    # one launch that reads each segment's weights once
+    experts = 128
+    w, s = oracle.synth_fp8(23, n + k, experts, n, k)
+    t = omega.Fp8Tensor.upload(experts, n, k, w, s)
+    rng = np.random.default_rng(n * 3 + k)
+    eids, toks = config2_rows(rng, 32, experts)
+    x = np.stack([bf16_row(rng, k, oracle) for _ in range(32)])
+    y, info = t.gemm_f32(eids, toks, x)
+    segs = len(set(eids.tolist()))
+    assert 90 <= segs <= 128 and info.segments == segs and info.rows == 256
+    assert info.passes_max == 1
+    assert info.weight_bytes == segs * n * k and info.streamed_bytes == info.weight_bytes
+    ref = oracle.fp8_grouped(w, s, eids, x[toks], threads=8)
+    for i in range(256):
+        assert rel_err(y[i], ref[i]) <= TOL, (i, int(eids[i]), rel_err(y[i], ref[i]))
+    for i in np.random.default_rng(1).choice(256, 12, replace=False):
+        yi, _ = t.gemv_f32(int(eids[i]), x[toks[i]])
+        np.testing.assert_array_equal(y[i], yi)
+    t.free()
+
+
+def test_gemm_other_width_takes_passes_of_eight_rows(omega, oracle):
+    # k = 384 runs the runtime-shaped kernel: segments of 19, 1, 8 and 9 rows take 3, 1, 1 and 2
+    # passes over their weights
+    experts, n, k = 4, 256, 384
+    w, s = oracle.synth_fp8(24, 9, experts, n, k)
+    t = omega.Fp8Tensor.upload(experts, n, k, w, s)
+    rng = np.random.default_rng(9)
+    eids = np.repeat(np.arange(4, dtype=np.uint32), [19, 1, 8, 9])
+    x = np.stack([bf16_row(rng, k, oracle) for _ in range(6)])
+    toks = rng.integers(0, 6, eids.size).astype(np.uint32)
+    y, info = t.gemm_f32(eids, toks, x)
+    assert info.passes_max == 3 and info.streamed_bytes == 7 * n * k and info.weight_bytes == 4 * n * k
+    ref = oracle.fp8_grouped(w, s, eids, x[toks], threads=8)
+    for i in range(eids.size):
+        assert rel_err(y[i], ref[i]) <= TOL, (i, rel_err(y[i], ref[i]))
+        yi, _ = t.gemv_f32(int(eids[i]), x[toks[i]])
+        np.testing.assert_array_equal(y[i], yi)
+    t.free()
+
+
+@pytest.mark.parametrize("k", [2048, 384])
+@pytest.mark.parametrize("mutant", [1, 2, 3])
+def test_gemm_mutants_are_caught(omega, oracle, mutant, k):
+    # crates/aien-omega-fp8/src/lib.rs:644-645: 1 scale dropped, 2 scale pointer never advances,
+    # 3 neighbour row's x
+    experts, n = 3, 256
+    w, s = oracle.synth_fp8(25, k, experts, n, k)
+    t = omega.Fp8Tensor.upload(experts, n, k, w, s)
+    rng = np.random.default_rng(k + mutant)
+    eids = np.array([0, 0, 1, 1, 1, 2], np.uint32)
+    x = np.stack([bf16_row(rng, k, oracle) for _ in range(6)])
+    toks = np.arange(6, dtype=np.uint32)
+    ref = oracle.fp8_grouped(w, s, eids, x, threads=8)
+    omega.lib().omega_gpu_fp8gemm_test_set_mutant(mutant)
+    try:
+        y, _ = t.gemm_f32(eids, toks, x)
+    finally:
+        omega.lib().omega_gpu_fp8gemm_test_set_mutant(0)
+    assert rel_err(y, ref) > TOL, mutant
+    y, _ = t.gemm_f32(eids, toks, x)
+    assert rel_err(y, ref) <= TOL
+    t.free()
