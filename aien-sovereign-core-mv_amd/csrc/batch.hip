@@ -499,6 +499,8 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         m.gu_s = L.gu->s;
         m.dn_wt = L.dn->wt;
         m.dn_s = L.dn->s;
+        m.gu_w = L.gu->w;
+        m.dn_w = L.dn->w;
         m.h = b->x;
         m.opart = b->o_part;
         m.oslices = kBdAttn / 256;

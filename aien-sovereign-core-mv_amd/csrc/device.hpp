@@ -55,6 +55,15 @@ __device__ __forceinline__ const cu32 *as_const_u32(const void *p) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63; }
+
+// Workgroup barrier after LDS writes, with the wave's own LDS operations completed first. The
+// compiler's wait before s_barrier has been seen missing where the writes sit on a loop's back
+// edge (another wavefront then read the staged row before it landed), so loops that restage LDS
+// use this form.
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+}
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // ------------------------------------------------------------------ reductions

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void k_fp8_gemm(const Fp8GemmArgs a) {
 
     for (uint32_t r = 0; r < rows; ++r) {
         // row r is staged; every wavefront is done with the buffer the next row goes to
-        __syncthreads();
+        lds_sync();
         const bool more = r + 1 < rows;
         if (more) {
             const float *xn = gemm_xrow(a, first + r + 1, K);

@@ -200,6 +200,9 @@ hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st);
 // T tokens (<= kMoeMaxTokens) through RMSNorm, router logits, top-8 and grouping, the grouped
 // gate|up (SwiGLU) and down FP8 GEMMs on the matrix cores, and the slot-order combine.
 constexpr uint32_t kMoeMaxTokens = 64;
+// below this token count the expert projections run as grouped GEMVs on f32 activations (each
+// segment's weights held in registers across its rows); from it on, on the FP8 matrix cores
+constexpr uint32_t kMoeGemvMax = 16;
 struct MoeArgs {
     const float *h = nullptr;          // [T][2048] residual rows
     const float *norm_w = nullptr;     // post-attention RMSNorm weights [2048]
@@ -211,6 +214,8 @@ struct MoeArgs {
     const float *gu_s = nullptr;       // [128][12][16]
     const uint8_t *dn_wt = nullptr;    // [128][2048][768] e4m3, tiled twin
     const float *dn_s = nullptr;       // [128][16][6]
+    const uint8_t *gu_w = nullptr;     // the row-major bytes (the GEMV path, tokens < kMoeGemvMax)
+    const uint8_t *dn_w = nullptr;
     const float *resid = nullptr;      // optional: out = resid + moe
     const float *opart = nullptr;      // optional: h += sum of oslices k-slices [oslices][T][2048]
     uint32_t oslices = 0;              //   (the o projection's partials), stored to hout

@@ -24,6 +24,7 @@
 #include "kernels.hpp"
 #include "mfma.hpp"
 #include "route.hpp"
+#include "rows.hpp"
 #include "runtime.hpp"
 
 namespace omega {
@@ -79,17 +80,31 @@ __global__ __launch_bounds__(64) void k_moe_router(const MoeArgs a) {
     u32x4 g[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) g[j] = *as_global(a.gate + (size_t)e * kMH + 8 * lane + 512 * j);
-    for (uint32_t t = blockIdx.y * 4; t < min(a.tokens, blockIdx.y * 4 + 4); ++t) {
-        const float *x = a.xn + (size_t)t * kMH + 8 * lane;
+    // the rows of all (up to) four tokens in one round trip
+    const uint32_t tb = blockIdx.y * 4, tn = min(a.tokens - tb, 4u);
+    f32x4 xa[4][4][2];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const float *x = a.xn + (size_t)(tb + min(q, tn - 1)) * kMH + 8 * lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xa[q][j][0] = *as_global_f32x4(x + 512 * j);
+            xa[q][j][1] = *as_global_f32x4(x + 512 * j + 4);
+        }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        if (q >= tn) break;
+        const uint32_t t = tb + q;
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const f32x4 x0 = *as_global_f32x4(x + 512 * j), x1 = *as_global_f32x4(x + 512 * j + 4);
+            const f32x4 x0 = xa[q][j][0], x1 = xa[q][j][1];
             const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                acc += (double)bf16_lo(g[j][q]) * (double)xv[2 * q];
-                acc += (double)bf16_hi(g[j][q]) * (double)xv[2 * q + 1];
+            for (int i = 0; i < 4; ++i) {
+                acc += (double)bf16_lo(g[j][i]) * (double)xv[2 * i];
+                acc += (double)bf16_hi(g[j][i]) * (double)xv[2 * i + 1];
             }
         }
         acc = wave_sum_f64(acc);
@@ -333,10 +348,119 @@ __global__ __launch_bounds__(256) void k_moe_split_act(const MoeArgs a) {
     if (live) store_split(a.aq, a.as, row, kMI / 128, b, j, q, sc);
 }
 
+// ------------------------------------------------------------------ 4/6 below kMoeGemvMax tokens: grouped GEMVs
+// The expert projections of a few tokens as GEMVs on the f32 rows (x' and the SwiGLU rows), with
+// the GEMV kernel's arithmetic (rows.hpp: the same lane layout, 16-column e4m3 dots, block-scale
+// fmaf and wavefront reduction): a wavefront holds RPW weight rows of one segment in registers
+// and walks the segment's rows (at most one per token, so fewer than 16), each staged once per
+// workgroup in LDS, the next one's loads in flight during the current dot. The four wavefronts of
+// a workgroup share the segment; workgroups past the plan's segment count leave at once.
+template <int K, int RPW, int NS>  // NS weight slabs per wavefront: 2 = gate and up rows, 1 = down
+struct MoeRows {
+    using S = Fp8Slab<K, RPW>;
+    static constexpr int P = S::P;
+    static constexpr int NX = (K / 4 + 255) / 256;
+    __device__ static void stage_load(const float *x, f32x4 (&xt)[NX]) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i) xt[i] = *as_global_f32x4(x + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
+    }
+    __device__ static void stage_store(float *xs, const f32x4 (&xt)[NX]) {
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            if (threadIdx.x + 256 * i < (uint32_t)K / 4) reinterpret_cast<f32x4 *>(xs)[threadIdx.x + 256 * i] = xt[i];
+    }
+};
+
+// gate|up: the wavefront owns gate rows j0 .. j0+3 and up rows 768+j0 .. +3 of its segment's
+// expert; act[row][j] = SwiGLU(gate_j, up_j) for each of the segment's rows
+__global__ __launch_bounds__(256) void k_moe_gu_rows(const MoeArgs a) {
+    using R = MoeRows<kMH, 4, 2>;
+    using S = R::S;
+    __shared__ __align__(16) float xs[2][kMH];
+    const uint32_t lane = lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    constexpr uint32_t per_seg = kMI / 4;
+    const uint32_t seg = wave / per_seg, j0 = (wave % per_seg) * 4;
+    if (seg >= *as_const_u32(a.plan)) return;  // the whole workgroup: its waves share seg
+    const uint32_t e = as_const_u32(a.seg_expert)[seg], r0 = as_const_u32(a.seg_start)[seg];
+    const uint32_t cnt = as_const_u32(a.seg_count)[seg];  // 1 ..= tokens < 16
+    // lane r holds the token of the segment's row r
+    const uint32_t tok_l = a.row_token[r0 + min(lane, cnt - 1)];
+    const uint8_t *wexp = a.gu_w + (size_t)e * 2 * kMI * kMH;
+    const float *sexp = a.gu_s + (size_t)e * (2 * kMI / 128) * (kMH / 128);
+    f32x4 xt[R::NX];
+    R::stage_load(a.xn + (size_t)__builtin_amdgcn_readfirstlane(tok_l) * kMH, xt);
+    __builtin_amdgcn_sched_barrier(0);
+    float scg[S::P], scu[S::P];
+    S::load_scales(sexp + (size_t)(j0 >> 7) * (kMH / 128), lane, 1.0f, 0, scg);
+    S::load_scales(sexp + (size_t)((kMI + j0) >> 7) * (kMH / 128), lane, 1.0f, 0, scu);
+    S gs, us;
+    gs.load(wexp + (size_t)j0 * kMH, lane);
+    us.load(wexp + (size_t)(kMI + j0) * kMH, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    R::stage_store(xs[0], xt);
+    for (uint32_t r = 0; r < cnt; ++r) {
+        lds_sync();  // row r staged; the other buffer is free
+        const bool more = r + 1 < cnt;
+        if (more) R::stage_load(a.xn + (size_t)__builtin_amdgcn_readlane(tok_l, r + 1) * kMH, xt);
+        float xr[S::P][16];
+        S::load_x_lds(xs[r & 1], lane, xr);
+        float ag[4] = {0.f, 0.f, 0.f, 0.f}, au[4] = {0.f, 0.f, 0.f, 0.f};
+        gs.dot(xr, scg, ag, lane);
+        us.dot(xr, scu, au, lane);
+        float gv = reduce_rows(ag, lane), uv = reduce_rows(au, lane);
+        if (a.mutant == 5) {
+            const float t = gv;
+            gv = uv;
+            uv = t;
+        }
+        if (lane < 4) a.gp[(size_t)(r0 + r) * kMI + j0 + lane] = gv / (1.0f + expf(-gv)) * uv;
+        if (more) R::stage_store(xs[(r + 1) & 1], xt);
+    }
+}
+
+// down: the wavefront owns down rows c0 .. c0+7 of its segment's expert; dp[row][c] for each of
+// the segment's SwiGLU rows (one k-slice)
+__global__ __launch_bounds__(256) void k_moe_dn_rows(const MoeArgs a) {
+    using R = MoeRows<kMI, 8, 1>;
+    using S = R::S;
+    __shared__ __align__(16) float xs[2][kMI];
+    const uint32_t lane = lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    constexpr uint32_t per_seg = kMH / 8;
+    const uint32_t seg = wave / per_seg, c0 = (wave % per_seg) * 8;
+    if (seg >= *as_const_u32(a.plan)) return;
+    const uint32_t e = as_const_u32(a.seg_expert)[seg], r0 = as_const_u32(a.seg_start)[seg];
+    const uint32_t cnt = as_const_u32(a.seg_count)[seg];
+    const uint8_t *wexp = a.dn_w + (size_t)e * kMH * kMI;
+    const float *sexp = a.dn_s + (size_t)e * (kMH / 128) * (kMI / 128);
+    f32x4 xt[R::NX];
+    R::stage_load(a.gp + (size_t)r0 * kMI, xt);
+    __builtin_amdgcn_sched_barrier(0);
+    float sc[S::P];
+    S::load_scales(sexp + (size_t)(c0 >> 7) * (kMI / 128), lane, 1.0f, 0, sc);
+    S ds;
+    ds.load(wexp + (size_t)c0 * kMI, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    R::stage_store(xs[0], xt);
+    for (uint32_t r = 0; r < cnt; ++r) {
+        lds_sync();
+        const bool more = r + 1 < cnt;
+        if (more) R::stage_load(a.gp + (size_t)(r0 + r + 1) * kMI, xt);
+        float xr[S::P][16];
+        S::load_x_lds(xs[r & 1], lane, xr);
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        ds.dot(xr, sc, acc, lane);
+        const float v = reduce_rows(acc, lane);
+        if (lane < 8) a.dp[(size_t)(r0 + r) * kMH + c0 + lane] = v;
+        if (more) R::stage_store(xs[(r + 1) & 1], xt);
+    }
+}
+
 // ------------------------------------------------------------------ 7. combine (slot order from zero) [+ residual]
-// each slot's down row is its k-slices summed in slice order
+// each slot's down row is its SPLITS k-slices summed in slice order
+template <uint32_t SPLITS>
 __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
-    using G = MoeGemm<1>;
     const uint32_t t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
     const size_t slice = (size_t)a.tokens * kTopK * kMH;
     float moe = 0.f;
@@ -346,7 +470,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
         const float w = (a.mutant == 6 && s == kTopK - 1) ? 0.f : a.weights[t * kTopK + s];
         float y = 0.f;
 #pragma unroll
-        for (uint32_t k = 0; k < G::SPLITS; ++k) y += a.dp[k * slice + (size_t)row * kMH + c];
+        for (uint32_t k = 0; k < SPLITS; ++k) y += a.dp[k * slice + (size_t)row * kMH + c];
         moe += w * y;
     }
     const size_t o = (size_t)t * kMH + c;
@@ -359,12 +483,19 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
     OMEGA_LAUNCH(k_moe_prep, dim3(T), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_router, dim3(kME, (T + 3) / 4), dim3(64), 0, st, a);
     OMEGA_LAUNCH(k_moe_plan, dim3(1), dim3(1024), 0, st, a);
+    if (T < kMoeGemvMax) {
+        // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
+        OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);
+        OMEGA_LAUNCH(k_moe_dn_rows, dim3(segs_max * (kMH / 8) / 4), dim3(256), 0, st, a);
+        OMEGA_LAUNCH(k_moe_combine<1>, dim3(T, kMH / 256), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     const uint32_t w0 = segs_max * (MoeGemm<0>::TILES / a.nt[0]) * MoeGemm<0>::SPLITS;
     const uint32_t w1 = segs_max * (MoeGemm<1>::TILES / a.nt[1]) * MoeGemm<1>::SPLITS;
     OMEGA_LAUNCH(k_moe_gemm<0>, dim3((w0 + 3) / 4), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_split_act, dim3((P * (kMI / 128) + 15) / 16), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_gemm<1>, dim3((w1 + 3) / 4), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_moe_combine<MoeGemm<1>::SPLITS>, dim3(T, kMH / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -452,6 +583,8 @@ MoeArgs moe_args(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tenso
     a.gu_s = gu->s;
     a.dn_wt = dn->wt;
     a.dn_s = dn->s;
+    a.gu_w = gu->w;
+    a.dn_w = dn->w;
     a.mutant = knobs().moe_mutant;
     return a;
 }
@@ -467,8 +600,8 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     clear_error(F_GEMM);
     int rc = moe_check(router, layer, gate_up, down, tokens);
-    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
-    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
+    if (!rc && tokens >= kMoeGemvMax) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
+    if (!rc && tokens >= kMoeGemvMax) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
     if (rc) return rc;
     if (!h_dev || !ids_dev || !weights_dev || !out_dev) {
         set_error(F_GEMM, "moe batch dev: NULL pointer");
@@ -496,8 +629,8 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     clear_error(F_GEMM);
     int rc = moe_check(router, layer, gate_up, down, tokens);
-    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
-    if (!rc) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
+    if (!rc && tokens >= kMoeGemvMax) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(gate_up));
+    if (!rc && tokens >= kMoeGemvMax) rc = fp8_ensure_tiled(F_GEMM, const_cast<OmegaGpuFp8Tensor *>(down));
     if (rc) return rc;
     if (!h || !ids || !weights || !moe_out) {
         set_error(F_GEMM, "moe batch: NULL pointer");

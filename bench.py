@@ -581,7 +581,7 @@ def bench_moe(om, args):
         line = {"workload": "moe_block", "tokens": T, "us_per_block": round(us, 2),
                 "distinct_experts": d, "algorithmic_bytes": int(b), "GBs": round(b / (us * 1e3), 1),
                 "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times),
-                "launches": 7}
+                "launches": 6 if T < 16 else 7, "expert_path": "grouped GEMV" if T < 16 else "FP8 MFMA"}
         print(json.dumps(line), flush=True)
         lines.append(line)
         for buf in hs + [od, idd, wd]:

@@ -4,15 +4,18 @@ top-8 by total order, renormalised weights) and the engine's FP8 MoE arm (gate|u
 SwiGLU, down grouped GEMV, slot-order combine).
 
 Bars: expert ids bit-exact, weights within 1e-6 relative, moe_out within 2e-3 relative
-(max abs error over max abs value, per token). The GEMMs run on the FP8 matrix cores with the
-activations split into four e4m3 terms; the one-term mutant (a plain fp8 cast of the
-activations) must fail the 2e-3 bar, which shows the bar resolves the split's precision.
+(max abs error over max abs value, per token). From 16 tokens on the GEMMs run on the FP8 matrix
+cores with the activations split into four e4m3 terms; the one-term mutant (a plain fp8 cast of
+the activations) must fail the 2e-3 bar, which shows the bar resolves the split's precision.
+Below 16 tokens the projections are grouped GEMVs on the f32 rows, held to 1e-4.
 """
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+GEMV_TOL = 1e-4
+GEMV_MAX = 16  # token batches below this take the GEMV path
 SEED = 20261202
 E, H, I = 128, 2048, 768
 
@@ -54,7 +57,7 @@ def bf16_rows(oracle, rng, T):
     return oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32)))
 
 
-@pytest.mark.parametrize("T", [1, 17, 32, 64])
+@pytest.mark.parametrize("T", [1, 4, 15, 16, 17, 32, 64])
 def test_moe_block_matches_the_oracle(omega, oracle, model, T):
     h = bf16_rows(oracle, np.random.default_rng(100 + T), T)
     out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
@@ -62,7 +65,11 @@ def test_moe_block_matches_the_oracle(omega, oracle, model, T):
     np.testing.assert_array_equal(ids, want_ids)
     np.testing.assert_allclose(w, want_w, rtol=1e-6, atol=0)
     errs = [rel_err(out[t], want[t]) for t in range(T)]
-    assert max(errs) <= TOL, (max(errs), int(np.argmax(errs)))
+    # below 16 tokens the projections are GEMVs on the f32 rows: only the f32 summation order
+    # separates them from the oracle
+    bar = GEMV_TOL if T < GEMV_MAX else TOL
+    print(f"T={T}: worst moe_out rel err {max(errs):.2e} (bar {bar:.0e})")
+    assert max(errs) <= bar, (max(errs), int(np.argmax(errs)))
     # deterministic: the same call again gives the same bits
     out2, ids2, _ = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
     np.testing.assert_array_equal(out2, out)
@@ -102,9 +109,9 @@ def test_device_entry_adds_the_residual(omega, oracle, model):
     np.testing.assert_array_equal(got, (h + out).astype(np.float32))
 
 
-@pytest.mark.parametrize("mutant", [1, 2, 5, 6, 7])
-def test_moe_mutants_are_caught(omega, oracle, model, mutant):
-    T = 32
+@pytest.mark.parametrize("T,mutant", [(32, 1), (32, 2), (32, 5), (32, 6), (32, 7),
+                                       (8, 1), (8, 2), (8, 5), (8, 6)])
+def test_moe_mutants_are_caught(omega, oracle, model, T, mutant):
     h = bf16_rows(oracle, np.random.default_rng(11), T)
     want, want_ids, want_w = oracle_block(oracle, model, h)
     lib = omega.lib()
