@@ -1670,20 +1670,41 @@ int omega_gpu_decode_attn_cache_import_dev(OmegaGpuDecodeAttnCache *c, uint32_t 
                     kvio_none, kvio_none);
 }
 
+// Sub-batches of at most kPattnSub tokens bound the prefill attention's scratch.
+constexpr uint32_t kPattnSub = 1024;
+
+// Scratch layout of one prefill attention call of m tokens from pos0: the prepared q rows of a
+// sub-batch, its item plan and token offsets, and the partials of its items. Sized from the
+// call's own last position, so a short prompt on a large cache asks for little.
+struct PattnScratch {
+    size_t qn, items, off, part;
+    size_t total() const { return qn + items + off + part; }
+};
+static PattnScratch pattn_scratch(uint32_t pos0, uint32_t m) {
+    const uint32_t sub = std::min(kPattnSub, m);
+    const uint32_t max_chunks = ((pos0 + m + 15) / 16 + kPattnChunk - 1) / kPattnChunk;
+    const size_t max_items = (size_t)sub * max_chunks;
+    PattnScratch s;
+    s.qn = (size_t)sub * 32 * 128 * 4;
+    s.items = (max_items * 16 + 255) / 256 * 256;
+    s.off = ((sub + 1) * 4 + 255) / 256 * 256;
+    s.part = (max_items * 32 * kPartStride * 4 + 255) / 256 * 256;
+    return s;
+}
+
 // The prefill attention of m tokens on the fused cache (both entries): qkv_dev [m][5120] and
-// out_dev [m][4096] device rows. Sub-batches of at most 1024 tokens bound the scratch; each runs
-// the preparation (K / V of its tokens appended), the page items and their combine.
+// out_dev [m][4096] device rows. Sub-batches of at most kPattnSub tokens; each runs the
+// preparation (K / V of its tokens appended), the page items and their combine. The working set
+// is the first pattn_scratch(pos0, m).total() bytes of the context's scratch.
 static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t pos0, uint32_t m,
                             const float *qkv_dev, float eps, float out_scale, float *out_dev,
                             OmegaGpuPrefillAttnInfo *info, const uint64_t t_call) {
     Ctx *cx = ctx(F_DATTN);
     if (!cx) return OMEGA_GPU_CHIP_FAIL;
-    constexpr uint32_t kSub = 1024;
-    const uint32_t max_chunks = (c->max_pos / 16 + kPattnChunk - 1) / kPattnChunk;
-    const size_t qn_bytes = (size_t)kSub * 32 * 128 * 4, max_items = (size_t)kSub * max_chunks;
-    const size_t item_bytes = (max_items * 16 + 255) / 256 * 256, off_bytes = ((kSub + 1) * 4 + 255) / 256 * 256;
-    if (!ensure_scratch(F_DATTN, cx, qn_bytes + item_bytes + off_bytes + max_items * 32 * kPartStride * 4))
-        return OMEGA_GPU_CHIP_FAIL;
+    constexpr uint32_t kSub = kPattnSub;
+    const PattnScratch sz = pattn_scratch(pos0, m);
+    if (!ensure_scratch(F_DATTN, cx, sz.total())) return OMEGA_GPU_CHIP_FAIL;
+    const size_t qn_bytes = sz.qn, item_bytes = sz.items, off_bytes = sz.off;
     uint8_t *base = static_cast<uint8_t *>(cx->scratch);
     PattnArgs a;
     a.pool = c->pool;
@@ -1796,13 +1817,13 @@ int omega_gpu_prefill_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t 
     if (rc) return rc;
     Ctx *cx = ctx(F_DATTN);
     if (!cx) return OMEGA_GPU_CHIP_FAIL;
+    // the q|k|v and out rows sit in the context's scratch after the run's own working set, so the
+    // serving seal and the allocation counters cover this entry like every other host entry
     const size_t qb = (size_t)m * 5120 * 4, ob = (size_t)m * 4096 * 4;
-    void *d = nullptr;
-    OMEGA_HIP(F_DATTN, hipMalloc(&d, qb + ob));
-    if (!ensure_pinned(F_DATTN, cx, std::max(qb, ob))) {
-        (void)hipFree(d);
-        return OMEGA_GPU_CHIP_FAIL;
-    }
+    const size_t run_bytes = (pattn_scratch(pos0, m).total() + 255) / 256 * 256;
+    if (!ensure_scratch(F_DATTN, cx, run_bytes + qb + ob)) return OMEGA_GPU_CHIP_FAIL;
+    if (!ensure_pinned(F_DATTN, cx, std::max(qb, ob))) return OMEGA_GPU_CHIP_FAIL;
+    void *d = static_cast<uint8_t *>(cx->scratch) + run_bytes;
     memcpy(cx->pin, qkv, qb);
     hipError_t e = hipMemcpyAsync(d, cx->pin, qb, hipMemcpyHostToDevice, cx->stream);
     if (e == hipSuccess) {
@@ -1815,7 +1836,6 @@ int omega_gpu_prefill_attn(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t 
         }
     }
     (void)hipStreamSynchronize(cx->stream);
-    (void)hipFree(d);
     if (e != hipSuccess) {
         set_error(F_DATTN, "prefill attn: %s", hipGetErrorString(e));
         return OMEGA_GPU_CHIP_FAIL;

@@ -44,7 +44,8 @@ class Request:
         self.tokens: list[int] = []   # generated tokens, in order
         self.fed = 0                  # positions fed so far (prompt and generated)
         self.pages: list[int] = []    # pool blocks of positions 0, 16, 32, ...
-        self.finish = None            # "stop", "length" or "cancelled" once it has left
+        self.finish = None            # "stop", "length", "cancelled" or "error" once it has left
+        self.error = None             # the exception that ended it ("error")
         self.joined_beat = self.first_token_beat = self.left_beat = None
         self.cancelled = False
 
@@ -137,13 +138,30 @@ class BeatScheduler:
         self.free_pages.extend(r.pages)
         r.pages = []
 
+    def _prefills(self, r: Request) -> bool:
+        """Whether the joining request's prompt goes through the whole-prompt prefill: long enough
+        to be worth it and within the prefill's capacity (a longer prompt is fed one token per
+        beat like a short one)."""
+        n = len(r.prompt) - 1
+        return bool(self.prefill) and self.prefill.min_tokens <= n <= self.prefill.max_positions
+
     def beat(self):
-        """One step of every live row. Returns the number of rows that stepped."""
+        """One step of every live row. Returns the number of rows that stepped. A request whose
+        prompt prefill fails leaves with finish "error" (its pages returned, `error` set); the
+        other rows go on."""
         while self.pending:
             r = self.pending.popleft()
             r.joined_beat = self.beats
-            if self.prefill and len(r.prompt) - 1 >= self.prefill.min_tokens:
-                self.prefill.fill(r.prompt[:-1], r.pages)
+            if r.cancelled:  # left before it ever ran: no prefill for it
+                self._leave(r, "cancelled")
+                continue
+            if self._prefills(r):
+                try:
+                    self.prefill.fill(r.prompt[:-1], r.pages)
+                except Exception as e:  # noqa: BLE001 - the request ends, the beat goes on
+                    r.error = e
+                    self._leave(r, "error")
+                    continue
                 r.fed = len(r.prompt) - 1
             self.live.append(r)
         for r in [r for r in self.live if r.cancelled]:

@@ -16,8 +16,10 @@ The JSON line also carries:
             library stream); peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
             summary for that kernel when one exists (profiles/), else null.
   cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
-            host cores: a bounded sample of 4 of the 48 layers x 128 tokens plus 4 full-vocab
-            lm_heads (about 10 s of CPU work), scaled to the 48-layer step.
+            host cores at the GPU run's context: 4 of the 48 layers over a cache holding the
+            same number of positions, plus the full-vocab lm_head, scaled to the 48-layer step;
+            timed on one thread and on every core this process may use (nproc reported beside
+            it), about 15 s of CPU work. value is the all-cores figure.
   bs32:     the metric's batch-32 figure, measured after the bs=1 model is freed: configuration
             5's batched step (32 sequences, contexts log-uniform in [1k, 128k], one hipGraph per
             step) for --bs32-steps steps; --no-bs32 skips it. --workload serve prints the full
@@ -79,31 +81,59 @@ def build_model(om, max_pos):
     return dict(model=m, graph=m.graph, seconds=time.time() - t0)
 
 
-def cpu_baseline(threads):
-    """The oracle engine on a bounded sample, scaled to the 48-layer step (see module doc)."""
+def host_cores():
+    """(nproc, cores this process may use): the second is the affinity set, capped by
+    OMP_NUM_THREADS where the box sets it (one GPU's share of the host)."""
+    nproc = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        usable = min(usable, int(cap))
+    return nproc, usable
+
+
+def cpu_baseline(threads, ctx):
+    """The oracle engine (oref_engine_step, the C restatement of the reference's host step) on a
+    bounded sample at the GPU run's context: 4 of the 48 layers with the cache holding `ctx`
+    positions, timed on one host thread and on `threads` threads (per-output-row parallel GEMVs,
+    as the reference's rayon loops), plus the 151936-row lm_head each way; scaled to 48 layers."""
     import pyoracle as orc
 
-    layers, tokens, heads = 4, 128, 4
+    layers = 4
+    nproc, _ = host_cores()
     cfg = dict(layers=layers, hidden=H, q_heads=QH, kv_heads=KVH, head_dim=HD, experts=E,
                top_k=TOPK, inter=I, vocab=V, eps=1e-6, rope_theta=1e6)
     m = orc.Model(cfg, SEED, sigma=0.02, norm_sigma=0.0, threads=threads)
-    eng = orc.Engine(m, 256, refined_router=True, threads=threads)
-    hid = eng.step(1)   # first touch of every weight page
-    t0 = time.perf_counter()
-    for t in range(tokens):
-        hid = eng.step(2 + t)
-    t_layers = (time.perf_counter() - t0) / tokens / layers
-    t1 = time.perf_counter()
-    for _ in range(heads):
-        eng.logits(hid)
-    t_lm = (time.perf_counter() - t1) / heads
-    step = t_layers * L + t_lm
-    return {"value": round(1.0 / step, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"C oracle engine (oracle/oracle.c, {threads} threads, per-output-row "
-                      f"parallel GEMV): {layers} of 48 layers x {tokens} tokens at positions "
-                      f"2-{tokens + 1} ({t_layers * 1e3:.1f} ms/layer) + {heads} 151936-row "
-                      f"lm_heads ({t_lm * 1e3:.1f} ms each), scaled to 48 layers: "
-                      f"{step:.3f} s/token"}
+
+    def timed(nthreads, tokens, heads):
+        eng = orc.Engine(m, ctx + tokens + 2, refined_router=True, threads=nthreads)
+        eng.fill_random(ctx, seed=SEED)
+        hid = eng.step(1)   # first touch of every weight page
+        t0 = time.perf_counter()
+        for t in range(tokens):
+            hid = eng.step(2 + t)
+        t_layer = (time.perf_counter() - t0) / tokens / layers
+        t1 = time.perf_counter()
+        for _ in range(heads):
+            eng.logits(hid)
+        t_lm = (time.perf_counter() - t1) / heads
+        del eng
+        step = t_layer * L + t_lm
+        return dict(s_per_token=round(step, 4), tok_s=round(1.0 / step, 4),
+                    ms_per_layer=round(t_layer * 1e3, 2), ms_lm_head=round(t_lm * 1e3, 1),
+                    sample=f"{tokens} tokens x {layers} layers, {heads} lm_heads")
+
+    one = timed(1, 3, 1)
+    many = timed(threads, 32, 4)
+    return {"value": many["tok_s"], "unit": "tok/s", "cores": threads, "kind": "port",
+            "nproc": nproc, "context": ctx,
+            "single_thread": one, "all_cores": many,
+            "sample": f"C oracle engine (oracle/oracle.c oref_engine_step + oref_engine_logits), "
+                      f"{layers} of 48 layers with {ctx} cached positions, scaled to 48 layers; "
+                      f"all cores = {threads} threads of nproc {nproc} (this process's share): "
+                      f"{many['ms_per_layer']} ms/layer, lm_head {many['ms_lm_head']} ms, "
+                      f"{many['s_per_token']} s/token; one thread: {one['ms_per_layer']} ms/layer, "
+                      f"lm_head {one['ms_lm_head']} ms, {one['s_per_token']} s/token"}
 
 
 def committed_traffic(kind):
@@ -782,7 +812,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=host_cores()[1])
     ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill", "kvio", "schedule"],
                     default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
@@ -926,7 +956,7 @@ def main():
     step_bytes = sum(algorithmic_bytes(k, ctx_mid) * v["launches_per_token"]
                      for k, v in kernels.items())
 
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads, ctx_mid)
     line = {
         "metric": METRIC,
         "value": round(tok_s, 2),

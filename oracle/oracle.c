@@ -918,6 +918,15 @@ void oref_engine_free(oref_engine *e) {
 
 int oref_engine_pos(const oref_engine *e) { return e->pos; }
 
+/* Benchmark support (no reference counterpart): the next step runs at position pos over the
+ * cache rows 0..pos-1 as they stand (written with oref_dattn_write_rows through oref_engine_kv). */
+int oref_engine_seek(oref_engine *e, int pos) {
+    if (pos < 0 || pos >= e->kv->max_pos) return -1;
+    e->pos = pos;
+    return 0;
+}
+oref_dattn *oref_engine_kv(oref_engine *e) { return e->kv; }
+
 /* qwen3_moe_omega.rs:4096-4345 on the arms the decode graph runs: FP8 q|k|v and o, the fused
  * decode attention (bf16 KV), the device router (RMSNorm, logits, top-k), FP8 grouped gate|up,
  * host SwiGLU, FP8 grouped down with a row per slot, combine in slot order, residual adds,

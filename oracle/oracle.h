@@ -197,6 +197,10 @@ int oref_engine_step(oref_engine *e, uint32_t token, float *hidden_out);
 /* lm_head logits of a hidden row (qwen3_moe_omega.rs:4348-4368). */
 void oref_engine_logits(oref_engine *e, const float *hidden, float *logits);
 int oref_engine_pos(const oref_engine *e);
+/* Benchmark support (no reference counterpart): position the engine at pos over the cache rows
+ * 0..pos-1 as written through oref_engine_kv; returns 0 or -1 past the cache. */
+int oref_engine_seek(oref_engine *e, int pos);
+oref_dattn *oref_engine_kv(oref_engine *e);
 /* Per-layer trace of the last step: routed ids/weights and the rank-8 / rank-9 logit margin. */
 void oref_engine_last_routes(const oref_engine *e, uint32_t *ids, float *weights, float *margins);
 /* Residual row after the last step (hidden floats). */

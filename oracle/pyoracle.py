@@ -124,6 +124,8 @@ def lib():
             "oref_engine_step": (i32, [P, u32, P]),
             "oref_engine_logits": (None, [P, P, P]),
             "oref_engine_pos": (i32, [P]),
+            "oref_engine_seek": (i32, [P, i32]),
+            "oref_engine_kv": (P, [P]),
             "oref_engine_last_routes": (None, [P, P, P, P]),
             "oref_engine_last_x": (None, [P, P]),
         }
@@ -654,6 +656,30 @@ class Engine:
         x = np.empty(self.model.cfg.hidden, dtype=np.float32)
         lib().oref_engine_last_x(self.h, ptr(x))
         return x
+
+    def write_kv_rows(self, layer: int, head: int, pos0: int, k, v):
+        """Cache rows pos0 .. pos0 + len(k) - 1 of (layer, kv head): [n][head_dim] bf16 K and V."""
+        k = np.ascontiguousarray(k, dtype=np.uint16).reshape(-1, self.model.cfg.head_dim)
+        v = np.ascontiguousarray(v, dtype=np.uint16).reshape(-1, self.model.cfg.head_dim)
+        lib().oref_dattn_write_rows(lib().oref_engine_kv(self.h), layer, head, pos0, k.shape[0], ptr(k), ptr(v))
+
+    def seek(self, pos: int):
+        """The next step runs at position pos over cache rows 0 .. pos - 1 as they stand
+        (oref_engine_seek)."""
+        if lib().oref_engine_seek(self.h, pos) != 0:
+            raise ValueError(f"seek to {pos} past the cache")
+
+    def fill_random(self, pos: int, seed: int = 0):
+        """Benchmark support: seeded bf16 N(0, 1) K/V rows at positions 0 .. pos - 1 of every layer,
+        then seek(pos)."""
+        c = self.model.cfg
+        rng = np.random.default_rng(seed)
+        for layer in range(c.layers):
+            for head in range(c.kv_heads):
+                k = f32_to_bf16(rng.standard_normal((pos, c.head_dim)).astype(np.float32))
+                v = f32_to_bf16(rng.standard_normal((pos, c.head_dim)).astype(np.float32))
+                self.write_kv_rows(layer, head, 0, k, v)
+        self.seek(pos)
 
     def __del__(self):
         if getattr(self, "h", None):

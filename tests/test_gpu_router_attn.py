@@ -395,14 +395,16 @@ def test_serving_reservation_bounds_seal_and_counters(omega, oracle):
         assert call(1, 641 + 15)[0] == -2                          # past max_context
         omega.serving_seal()
         assert call(3, 600)[0] == 0
-        # growth of the shared scratch by another family: the prefill attention over a cache of
-        # 131072 positions sizes its partials for every chunk (about 4.5 GB), more than any other
-        # call here ever holds, so the sealed library must refuse it whatever ran before
+        # growth of the shared scratch by another family: a prefill attention of 1024 tokens
+        # ending at position 131072 sizes its partials for 256 chunks per token (about 4.4 GB),
+        # more than any other call here ever holds, so the sealed library must refuse it whatever
+        # ran before (and before any of its work reaches the device)
         from omega_amd import prefill as pf
         cache = omega.DecodeAttnCache(2, 131072, 1e6)
         try:
             with pytest.raises(omega.OmegaGpuError, match="reservation exceeded"):
-                pf.PrefillAttention(cache).attend(0, 0, 1, np.zeros((1, 5120), np.float32), 1e-6, 1.0)
+                pf.PrefillAttention(cache).attend(0, 131072 - 1024, 1024, np.zeros((1024, 5120), np.float32),
+                                                  1e-6, 1.0)
         finally:
             cache.free()
         assert omega.alloc_stats()["stale_refusals"] == s0["stale_refusals"] + 1

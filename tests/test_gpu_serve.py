@@ -118,6 +118,28 @@ def test_whole_prompt_joins(omega, oracle, served, prefill_join):
         solo = serve.BeatScheduler(bm.bd, BLOCKS, MAX_BLOCKS, slots=1, prefill=prefill_join).run(
             {0: [(k, prompt, new, ())]})[k]
         assert solo.tokens == r.tokens, k
+    # the joined generation against the oracle engine: the prompt's K / V rows as the prefill
+    # left them (the payload the join copied into the request's pages) written into the oracle's
+    # cache, then the last prompt token at position n - 1 and greedy steps (pins the position and
+    # token of the last prompt step and the page order; the rows themselves are pinned against the
+    # W8A8 oracle stage by stage in test_gpu_prefill)
+    c = m.cfg
+    geo = oracle.PoolBlockGeometry(c.layers, c.kv_heads, c.head_dim, 16)
+    for k in ("a", "c", "d"):
+        prompt, new = reqs[k]
+        n = len(prompt)
+        prefill_join.wp.run(prompt[:-1], 0)
+        payload, _ = prefill_join.cache.export_kv(0, n - 1)
+        eng = oracle.Engine(m, 256, refined_router=True, threads=16)
+        oracle.kv_blocks_to_rows(geo, 0, n - 1, payload,
+                                 lambda layer, head, kr, vr: eng.write_kv_rows(layer, head, 0, kr, vr))
+        eng.seek(n - 1)
+        h = eng.step(prompt[-1])
+        want = []
+        for _ in range(new):
+            want.append(int(oracle.argmax(eng.logits(h))))
+            h = eng.step(want[-1])
+        assert got[k].tokens == want, k
     # the pages of a whole-prompt join hold the fused cache's rows byte for byte
     prompt = reqs["d"][0]
     sch = serve.BeatScheduler(bm.bd, BLOCKS, MAX_BLOCKS, slots=1, prefill=prefill_join)
