@@ -260,13 +260,18 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     float *part = a.part + ((size_t)h * 8 * kDattnSplits + s) * kPartStride;
     if (holds) {
         // the partial goes where every CU reads it (agent-scope stores write through the XCD's
-        // L2); once the stores are acknowledged the split's flag carries this launch's epoch
+        // L2); once the stores are acknowledged the split's flag carries this launch's epoch.
+        // Dims d and d + 64 sit side by side (o at 4 + 2 (d % 64) + d / 64), so the merge's lane l
+        // reads its two dims with one 8-byte load.
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float *pp = part + (size_t)(4 * hg + i) * kDattnSplits * kPartStride;
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                __hip_atomic_store(pp + 4 + 16 * (nb + nb_off) + n, ov[nb][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int nb = 0; nb < 4; ++nb) {
+                const uint32_t d = 16 * (nb + nb_off) + n;
+                __hip_atomic_store(pp + 4 + 2 * (d & 63) + (d >> 6), ov[nb][i], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         if (lane < 8) {  // lane r holds head r's running max and sum
             float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
@@ -297,28 +302,40 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     }
     const uint32_t hq = h * 8 + s;
     const float *base = a.part + (size_t)hq * kDattnSplits * kPartStride;
+    // Every load of the merge goes out at once (one round trip): lane j's (m, l) of split j, and
+    // per split i the (o[l], o[l + 64]) pair of lane l, in chunks of 16 splits up to `active`
+    // (indices past it clamp to the last split and get weight 0).
     const uint32_t j = min(lane, active - 1);
-    const float mj = __hip_atomic_load(base + (size_t)j * kPartStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float lj = __hip_atomic_load(base + (size_t)j * kPartStride + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t mlj = __hip_atomic_load(reinterpret_cast<const uint64_t *>(base + (size_t)j * kPartStride),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t xo[kDattnSplits];
+#pragma unroll
+    for (uint32_t c = 0; c < kDattnSplits / 16; ++c) {
+        if (c * 16 >= active) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t si = min(c * 16 + i, active - 1);
+            xo[c * 16 + i] = __hip_atomic_load(
+                reinterpret_cast<const uint64_t *>(base + (size_t)si * kPartStride + 4 + 2 * lane),
+                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    const float mj = __uint_as_float((uint32_t)mlj), lj = __uint_as_float((uint32_t)(mlj >> 32));
     const float mv = lane < active ? mj : -INFINITY;
     float M = row16_max(mv);
     M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
     const float wj = lane < active ? (a.mutant == 4 ? 1.f : expf(mj - M)) : 0.f;
     const float L = wave_sum(wj * (lane < active ? lj : 0.f));
     float o0 = 0.f, o1 = 0.f;
-    for (uint32_t c0 = 0; c0 < active; c0 += 16) {
-        float x0[16], x1[16];
+#pragma unroll
+    for (uint32_t c = 0; c < kDattnSplits / 16; ++c) {
+        if (c * 16 >= active) break;
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i) {
-            const uint32_t si = min(c0 + i, active - 1);
-            x0[i] = __hip_atomic_load(base + (size_t)si * kPartStride + 4 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            x1[i] = __hip_atomic_load(base + (size_t)si * kPartStride + 68 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-            const float wi = c0 + i < active ? readlane_f32(wj, (int)(c0 + i)) : 0.f;
-            o0 = fmaf(wi, x0[i], o0);
-            o1 = fmaf(wi, x1[i], o1);
+            const uint32_t si = c * 16 + i;
+            const float wi = si < active ? readlane_f32(wj, (int)si) : 0.f;
+            o0 = fmaf(wi, __uint_as_float((uint32_t)xo[si]), o0);
+            o1 = fmaf(wi, __uint_as_float((uint32_t)(xo[si] >> 32)), o1);
         }
     }
     a.out[hq * 128 + lane] = o0 * (a.out_scale / L);

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     // row's: the row is written to LDS after the ranking)
     if (wid == 0) {
         Route r;
-        if (a.forced) route_forced(a.logits, a.forced, r);
+        // parity tests: the layer's forced ids, unless its row asks for the ranking
+        if (a.forced && *as_global_u32(a.forced) != OMEGA_GPU_DGRAPH_RANK) route_forced(a.logits, a.forced, r);
         else route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
         if (lane == 0) {
 #pragma unroll
@@ -235,6 +236,7 @@ struct OmegaGpuDecodeGraph {
     uint32_t *forced = nullptr;     // [layers][8] forced expert ids (parity tests), when force_on
     uint32_t *flags = nullptr;      // [4][64] the attention's split flags (epochs)
     uint32_t epoch = 0;             // of the last token
+    bool sync_stale = false;        // a token failed after its epoch was taken: clear the flags
     bool force_on = false;
     float *route_log_w = nullptr;   // [layers][8] their weights
     GraphIo *pin = nullptr;         // pinned host twin of io
@@ -621,7 +623,13 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     memset(pin, 0, sizeof(GraphIo));
     pin->pos = pos;
     pin->tok = token_in;
-    if (++g->epoch >= (1u << 26)) g->epoch = 1;  // epoch * 64 + layer stays a distinct 32-bit word
+    // The attention's split flags hold epoch * 64 + layer. Before the epoch wraps, or after a token
+    // that failed once its epoch was taken, the flags are cleared and the epochs start again from 1.
+    if (++g->epoch >= (1u << 26) || g->sync_stale) {
+        OMEGA_HIP(F_SESSION, hipMemsetAsync(g->flags, 0, 4 * kDattnSplits * 4, c->stream));
+        g->epoch = 1;
+    }
+    g->sync_stale = true;  // until this token has completed
     pin->epoch = g->epoch;
     float *xin = reinterpret_cast<float *>(pin + 1);
     OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->io, pin, sizeof(GraphIo), hipMemcpyHostToDevice, c->stream));
@@ -655,6 +663,7 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
         set_error(F_SESSION, "decode graph: the attention's split merge ran out of waits (%u)", pin->merge_err);
         return OMEGA_GPU_CHIP_FAIL;
     }
+    g->sync_stale = false;
     *token = argmax_from_slots(pin->argmax);
     g->stamps_valid = g->stamps;
     g->stamps_graph = g->stamps && !eager;
@@ -828,11 +837,14 @@ int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint3
     clear_error(F_SESSION);
     if (!g) return OMEGA_GPU_BAD_ARGS;
     if (ids) {
-        for (uint32_t i = 0; i < g->cfg.layers * 8; ++i)
-            if (ids[i] >= kExperts) {
-                set_error(F_SESSION, "decode graph force_routes: expert id %u >= %u", ids[i], kExperts);
-                return OMEGA_GPU_BAD_ARGS;
-            }
+        for (uint32_t l = 0; l < g->cfg.layers; ++l) {
+            if (ids[l * 8] == OMEGA_GPU_DGRAPH_RANK) continue;  // this layer ranks its own logits
+            for (uint32_t i = l * 8; i < l * 8 + 8; ++i)
+                if (ids[i] >= kExperts) {
+                    set_error(F_SESSION, "decode graph force_routes: expert id %u >= %u", ids[i], kExperts);
+                    return OMEGA_GPU_BAD_ARGS;
+                }
+        }
         Ctx *c = ctx(F_SESSION);
         if (!c) return OMEGA_GPU_CHIP_FAIL;
         OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));

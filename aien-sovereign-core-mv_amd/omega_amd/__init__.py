@@ -691,6 +691,7 @@ class Bf16Tensor:
 
 # ------------------------------------------------------------------ decode graph (aien-omega-dgraph)
 DGRAPH_HIDDEN, DGRAPH_MAX_LAYERS, MAX_VOCAB = 2048, 64, 2048 * 2048
+DGRAPH_RANK = 0xFFFFFFFF  # force_routes: this layer ranks its own logits
 KIND_NAMES = ["norm", "qkv", "attn", "o_proj", "res_add", "router", "gate_up", "swiglu", "down",
               "combine_norm", "lm_head", "argmax"]
 
@@ -766,7 +767,8 @@ class DecodeGraph:
 
     def force_routes(self, ids):
         """Teacher forcing for parity tests: [layers][8] expert ids in place of the ranking, or
-        None to turn it off."""
+        None to turn it off; a row starting with DGRAPH_RANK (0xFFFFFFFF) leaves that layer's own
+        ranking in place."""
         if ids is None:
             self._rc(lib().omega_gpu_decode_graph_test_force_routes(self.h, None), "force_routes")
             return

@@ -650,8 +650,11 @@ int omega_gpu_decode_graph_read_routes(OmegaGpuDecodeGraph *g, uint32_t *ids, fl
 int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap);
 /* Teacher forcing for parity tests (not in the reference ABI): ids [layers][8] expert ids
  * (< 128) used by the following tokens in place of each layer's top-8 ranking, in slot order,
- * their weights the softmax of the device's own router logits over that set; NULL turns the
- * forcing off. Lets a full-size decode be compared with the oracle past a routing near-tie. */
+ * their weights the softmax of the device's own router logits over that set; a layer whose row
+ * starts with OMEGA_GPU_DGRAPH_RANK (0xFFFFFFFF; the rest of the row ignored) ranks its own
+ * logits as usual; NULL turns the forcing off. Lets a full-size decode be compared with the
+ * oracle past a routing near-tie. */
+#define OMEGA_GPU_DGRAPH_RANK 0xFFFFFFFFu
 int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint32_t *ids);
 /* Batched MoE block (not in the reference ABI; the expert FFN of a decode step at token batch
  * T <= 64, the reference's per-token FP8 arm qwen3_moe_omega.rs:4287-4318 batched): for each of

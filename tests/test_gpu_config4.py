@@ -6,25 +6,30 @@ graph one token per step, then 64 greedy tokens: the workload bench.py times. Th
 values are tests/golden/config4_greedy.npz, written by tests/golden/make_config4.py from the
 oracle engine (oref_engine_step: qwen3_moe_omega.rs:4096-4345 restated).
 
-The device and the oracle sum their f32 products in different orders, so their residual rows
-differ by about 1e-6 relative, and a layer whose rank-8 / rank-9 router logits sit closer than
-that can route differently; from there the two histories are different computations. The
-recorded decode has such near ties (gaps down to 6e-7 in the prompt, 3e-6 while generating).
-Hence two tests:
+The device and the oracle sum their f32 products in different orders, so their rows differ by
+about 1e-6 relative; K and V are stored as bf16 (the reference's KV format), and now and then an
+element lands on the other side of a bf16 rounding boundary, a whole bf16 step (2^-8) apart. The
+first such V element (layer 5 of the first token here) moves the residual by about 1e-4, and from
+there the two runs' router logits differ by up to about 1e-3 in the deeper layers (measured:
+1e-6 through layer 4, 2e-4 at layer 8, 1.4e-3 at layer 20), so a layer whose consecutive routing
+ranks sit closer than that can order or pick its experts differently, and from there the two
+histories are different computations. Hence two tests:
 
-1. Free-running: wherever the graph's routed expert set of a layer differs from the oracle's,
-   the oracle's smallest consecutive-rank gap of that layer's top 9 is below 1e-3 (a near tie);
-   every generated step up to the first routing difference while generating has the oracle's
-   token and logits (the bars of 2). A difference in the prompt only changes a few history rows,
-   and the comparison goes on through it.
-2. Routing forced to the oracle's expert ids at every step (teacher forcing through
-   omega_gpu_decode_graph_test_force_routes; the weights stay the device's own softmax over that
-   set), so both runs compute the same function: all 64 greedy tokens identical (a divergence
-   passes only at an oracle top-2 margin below 1e-3, the 1e-3 floor of the reference's
-   own30b_check, crates/aien-inference-abi/src/bin/own30b_check.rs:181-193, 986-1006), logits
-   within 2e-3 relative (max |gpu - cpu| over max |cpu|) at 1024 seeded vocabulary indices plus
-   the oracle's top 16 at every step and over the whole vocabulary at the first generated step,
-   top-2 margins within 2 x 2e-3 of max |logit|.
+1. Free-running, the reference's own full-size bar (own30b_check,
+   crates/aien-inference-abi/src/bin/own30b_check.rs:181-193, 986-1006): the 512 prompt tokens
+   and 64 greedy tokens with nothing forced; every generated token equals the oracle's, or the
+   first divergence sits at an oracle top-2 margin below the 1e-3 floor.
+2. Routing forced only near ties: at every processed token, each layer whose oracle
+   consecutive-rank gap of the top 9 (rank-8 / rank-9 logit margin and ln(w_k / w_k+1) inside the
+   top 8) is below 1e-2, ten times the measured drift, takes the oracle's expert ids (teacher
+   forcing through omega_gpu_decode_graph_test_force_routes; the weights stay the device's own
+   softmax over that set); every other layer ranks its own logits and must route exactly as the
+   oracle did (ids bit-exact in slot order, every layer of all 575 processed tokens). Both runs
+   then compute the same function over the same history: all 64 greedy tokens identical (a
+   divergence passes only at an oracle top-2 margin below 1e-3), logits within 2e-3 relative (max
+   |gpu - cpu| over max |cpu|) at 1024 seeded vocabulary indices plus the oracle's top 16 at every
+   step and over the whole vocabulary at the first generated step, top-2 margins within 2 x 2e-3
+   of max |logit|.
 """
 import os
 
@@ -33,7 +38,8 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
-NEAR_TIE = 1e-3
+NEAR_TIE = 1e-3        # the reference's top-2 margin floor
+ROUTE_NEAR = 1e-2      # routing gaps forced in test 2: ten times the measured drift
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_greedy.npz")
 
 
@@ -108,56 +114,68 @@ def decode(g, golden, forced, on_step):
             return
 
 
-def test_config4_free_running_matches_until_a_near_tie(omega, golden, model):
-    g = model.graph
-    g.force_routes(None)
-    chk = StepCheck(golden)
-    npr = len(golden["prompt"])
-    flips = []
-
-    def on_step(t, tok):
-        ids, _ = g.read_routes()
-        want = golden["step_routes"][t]
-        differs = False
-        for l in range(ids.shape[0]):
-            if set(ids[l].tolist()) != set(want[l].tolist()):
-                gap = float(golden["step_gap"][t, l])
-                flips.append((t, l, gap))
-                assert gap < NEAR_TIE, f"step {t} layer {l}: routing differs at an oracle gap of {gap:.2e}"
-                differs = True
-        if t >= npr - 1:
-            s = t - (npr - 1)
-            _, _, logits = g.read(logits=True)
-            # a routing difference while generating changes the next step's logits: stop there
-            return chk.check(s, tok, logits) and not differs
-        return True
-
-    decode(g, golden, False, on_step)
-    print(f"free-running: routing differences (step, layer, oracle gap) {flips}; "
-          f"{chk.compared} generated steps identical, logits rel err <= {chk.worst:.2e}")
-
-
-def test_config4_forced_routing_matches_every_step(omega, golden, model):
+def test_config4_routes_match_except_at_near_ties(omega, golden, model):
     g = model.graph
     chk = StepCheck(golden)
     npr = len(golden["prompt"])
     n_gen = len(golden["tokens"])
-    state = {"diverged": None}
-
-    def on_step(t, tok):
-        if t >= npr - 1:
-            s = t - (npr - 1)
-            _, _, logits = g.read(logits=True)
-            if not chk.check(s, tok, logits):
-                state["diverged"] = s
-                return False
-        return True
-
+    routes = golden["step_routes"].astype(np.uint32)
+    near = golden["step_gap"] < ROUTE_NEAR                  # [steps][layers]
+    state = {"diverged": None, "ranked": 0, "forced": int(near.sum())}
+    prompt = golden["prompt"]
+    pos, tok = 0, None
     try:
-        decode(g, golden, True, on_step)
+        for t in range(npr + n_gen - 1):
+            sel = routes[t].copy()
+            sel[~near[t], 0] = omega.DGRAPH_RANK                 # these layers rank their own logits
+            g.force_routes(sel)
+            tok_in = int(prompt[t]) if t < npr else tok
+            tok, _ = g.token_id(tok_in, pos)
+            pos += 1
+            ids, _ = g.read_routes()
+            for l in np.flatnonzero(~near[t]):
+                assert ids[l].tolist() == routes[t, l].tolist(), \
+                    f"step {t} layer {l}: routed {ids[l].tolist()}, oracle {routes[t, l].tolist()} " \
+                    f"(oracle gap {float(golden['step_gap'][t, l]):.2e})"
+                state["ranked"] += 1
+            if t >= npr - 1:
+                s = t - (npr - 1)
+                _, _, logits = g.read(logits=True)
+                if not chk.check(s, tok, logits):
+                    state["diverged"] = s
+                    break
     finally:
         g.force_routes(None)
-    print(f"forced routing: {chk.compared} of {n_gen} greedy tokens identical (divergence at "
-          f"{state['diverged']}), logits rel err <= {chk.worst:.2e}, margins within "
+    print(f"routing forced at {state['forced']} near-tie (step, layer) points, {state['ranked']} ranked "
+          f"by the device and equal to the oracle; {chk.compared} of {n_gen} greedy tokens identical "
+          f"(divergence at {state['diverged']}), logits rel err <= {chk.worst:.2e}, margins within "
           f"{chk.worst_margin:.2e} of max |logit|")
     assert state["diverged"] is not None or chk.compared == n_gen
+
+
+def test_config4_free_running_greedy_tokens(omega, golden, model):
+    g = model.graph
+    g.force_routes(None)
+    npr, n_gen = len(golden["prompt"]), len(golden["tokens"])
+    state = {"diverged": None, "worst": 0.0}
+    got = []
+
+    def on_step(t, tok):
+        if t < npr - 1:
+            return True
+        s = t - (npr - 1)
+        got.append(tok)
+        _, _, logits = g.read(logits=True)
+        state["worst"] = max(state["worst"], rel_err(logits[golden["subset"]], golden["sub_val"][s]))
+        if tok != int(golden["tokens"][s]):
+            m = float(golden["margins"][s])
+            assert m < NEAR_TIE, (f"greedy token {s} is {tok}, oracle {int(golden['tokens'][s])} at oracle "
+                                  f"top-2 margin {m:.4f} (>= {NEAR_TIE})")
+            state["diverged"] = s
+            return False
+        return True
+
+    decode(g, golden, False, on_step)
+    print(f"free-running: {len(got) - (state['diverged'] is not None)} of {n_gen} greedy tokens identical "
+          f"(divergence at {state['diverged']}); logits rel err <= {state['worst']:.2e} with the histories apart")
+    assert state["diverged"] is not None or len(got) == n_gen
