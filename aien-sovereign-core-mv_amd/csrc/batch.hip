@@ -11,7 +11,8 @@
 // the lowest-index argmax (tensor.rs:299-318). The sequences share every weight read: the
 // projections are FP8 matrix-core GEMMs over the batch, the experts are grouped by expert
 // (moe.hip), the attention is the ragged paged kernel (attn.hip), the lm_head a bf16 matrix-core
-// GEMM with the argmax folded in. Nothing is exchanged between workgroups inside a launch.
+// GEMM with the argmax folded in. Only the MoE planner exchanges data between the workgroups of
+// one launch (its rankings, then the grouping).
 //
 // Per layer: rows (norm + split) | q|k|v GEMM (k-slice partials) | q/k norm, RoPE, K/V append |
 // paged attention items | combine + split | o GEMM (k-slice partials) | MoE block (7 launches,
@@ -45,9 +46,15 @@ struct BdIo {
     uint32_t tok[kBdMaxSeqs];
     uint32_t pos[kBdMaxSeqs];           // the token's position: its KV slot; context = pos + 1
     ItemPlan plan;                      // the step's attention work items
+    uint32_t moe_late[2];               // [0]: MoE planner waits that ran out this step
     unsigned long long argmax[kBdMaxSeqs][kArgmaxSlots];
 };
 static_assert(offsetof(BdIo, argmax) % 8 == 0, "argmax slots 8-byte aligned");
+static_assert(offsetof(BdIo, argmax) == offsetof(BdIo, moe_late) + 8, "one copy back: moe_late, argmax");
+// the step's results copied back in one transfer: the planner's count, then seqs argmax rows
+constexpr size_t bd_back_bytes(uint32_t seqs) {
+    return 8 + sizeof(unsigned long long) * kArgmaxSlots * seqs;
+}
 
 struct BdArgs {
     uint32_t T = 0;
@@ -510,6 +517,7 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         m.ids = b->route_ids + (size_t)l * kBdMaxSeqs * 8;
         m.weights = b->route_w + (size_t)l * kBdMaxSeqs * 8;
         m.mutant = knobs().moe_mutant;
+        m.errc = &b->io->moe_late[0];
         OMEGA_HIP(F_SESSION, launch_moe_batch(m, st));
     }
     a.norm_w = b->final_norm;
@@ -529,6 +537,18 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
 
 bool fp8_is(const OmegaGpuFp8Tensor *t, uint32_t experts, uint32_t n, uint32_t k) {
     return t && t->experts == experts && t->n == n && t->k == k;
+}
+
+// After the step's copy back: the next tokens, or an error when a MoE planner's wait ran out (its
+// layer added nothing, so the step's logits are not the model's)
+int bd_finish(const BdIo *p, uint32_t seqs, uint32_t *next_tokens) {
+    if (p->moe_late[0]) {
+        set_error(F_SESSION, "batch decode step: %u MoE plans timed out waiting for their rankings",
+                  p->moe_late[0]);
+        return OMEGA_GPU_CHIP_FAIL;
+    }
+    for (uint32_t s = 0; s < seqs; ++s) next_tokens[s] = argmax_from_slots(p->argmax[s]);
+    return OMEGA_GPU_OK;
 }
 
 }  // namespace
@@ -788,11 +808,10 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
         OMEGA_HIP(F_SESSION, hipMemcpyAsync(b->io, p, sizeof(BdIo), hipMemcpyHostToDevice, c->stream));
         int rc = bd_enqueue(b, seqs, c->stream);
         if (rc) return rc;
-        OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->argmax, b->io->argmax, sizeof(p->argmax[0]) * seqs,
+        OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->moe_late, b->io->moe_late, bd_back_bytes(seqs),
                                             hipMemcpyDeviceToHost, c->stream));
         OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
-        for (uint32_t s = 0; s < seqs; ++s) next_tokens[s] = argmax_from_slots(p->argmax[s]);
-        return OMEGA_GPU_OK;
+        return bd_finish(p, seqs, next_tokens);
     }
     const uint32_t key = seqs | (b->keep_logits ? 256u : 0u);
     auto it = b->exec.find(key);
@@ -808,11 +827,10 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
     }
     OMEGA_HIP(F_SESSION, hipMemcpyAsync(b->io, p, sizeof(BdIo), hipMemcpyHostToDevice, c->stream));
     OMEGA_HIP(F_SESSION, hipGraphLaunch(it->second, c->stream));
-    OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->argmax, b->io->argmax, sizeof(p->argmax[0]) * seqs,
+    OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->moe_late, b->io->moe_late, bd_back_bytes(seqs),
                                         hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
-    for (uint32_t s = 0; s < seqs; ++s) next_tokens[s] = argmax_from_slots(p->argmax[s]);
-    return OMEGA_GPU_OK;
+    return bd_finish(p, seqs, next_tokens);
 }
 
 int omega_gpu_batch_decode_read(OmegaGpuBatchDecode *b, uint32_t seqs, float *x, float *hidden, float *logits,

@@ -228,7 +228,8 @@ struct MoeArgs {
     uint8_t *xq = nullptr;             // [T][16][4][128] e4m3 terms of x'
     float *xs = nullptr;               // [T][16][4] their scales
     float *logits = nullptr;           // [T][128]
-    uint32_t *plan = nullptr;          // [0]: segments
+    uint32_t *plan = nullptr;          // [0]: segments, [1]: 1 when the planner's wait ran out
+    uint32_t *errc = nullptr;          // optional: counts the planner's waits that ran out
     uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
     uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row

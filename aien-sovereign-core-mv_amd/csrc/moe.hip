@@ -15,8 +15,9 @@
 // from the exact residual of the previous one (so about 16 significant bits survive against fp8's
 // 4), and the four products are summed in f32 with the weight block scale. A wavefront owns 16
 // output features of one expert segment (gate and up features together for SwiGLU) and all of
-// the segment's rows (16 per MFMA column tile); nothing is exchanged between workgroups inside a
-// launch: the grouping is one workgroup's launch, the combine a launch of its own.
+// the segment's rows (16 per MFMA column tile). The planner is the one launch whose workgroups
+// hand data over: one workgroup per token ranks its experts, the launch's last workgroup waits on
+// their flags and groups the pairs. The GEMMs exchange nothing; the combine is a launch of its own.
 #include <cmath>
 #include <cstdio>
 
@@ -112,42 +113,83 @@ __global__ __launch_bounds__(64) void k_moe_router(const MoeArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ 3. top-8 and the grouping (one workgroup)
+// ------------------------------------------------------------------ 3. top-8 and the grouping
 // Rows of the grouped GEMMs are (token, slot) pairs ordered by expert, then by pair index
 // (t * 8 + s) inside an expert; segments are the experts with rows, in ascending id.
-__global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
+//
+// Workgroups 0 .. T-1 rank one token each (its top-8 on one wavefront, so the 32 rankings of a
+// T = 32 batch run on 32 CUs side by side instead of sharing one CU's four SIMDs), store its ids
+// and weights, and once those stores are acknowledged flag the token with this launch's epoch.
+// Workgroup T, dispatched after every ranking workgroup (so nothing it waits for can be queued
+// behind it), waits (bounded) for the T flags, then groups the pairs: expert masks, counts, the
+// prefix sums and every pair's row. The epoch lives in device memory: each launch reads the word
+// the previous launch's grouping workgroup left and flags with one more; the grouping workgroup
+// writes it back as it finishes, so consecutive launches (one stream, kernel boundaries between
+// them) never mistake an old flag for a new one.
+constexpr uint32_t kPlanSpins = 1u << 22;  // bounded wait (seconds)
+// [0] the last launch's epoch, [32 + t] token t's flag; zero at load, one array per device
+static __device__ __align__(256) uint32_t g_plan_sync[32 + kMoeMaxTokens];
+
+__global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     constexpr uint32_t kWords = kMoeMaxTokens * kTopK / 32;
     __shared__ uint32_t sid[kMoeMaxTokens * kTopK];
     __shared__ uint32_t mask[kME][kWords];  // bit p of expert e: pair p routes to e
     __shared__ uint32_t scan[2][kME];       // count | (count > 0) << 16, prefix-summed
-    __shared__ float lg[kMoeMaxTokens * kME];
-    const uint32_t tid = threadIdx.x, lane = lane_id(), wid = tid >> 6;
-    const uint32_t pairs = a.tokens * kTopK;
-    for (uint32_t i = tid; i < kME * kWords; i += 1024) (&mask[0][0])[i] = 0u;
-    // every token's logits in one round trip, then the rankings from LDS: sixteen wavefronts (four
-    // per SIMD, so the ranking's dependent VALU chains of about 300 instructions per token
-    // overlap) in a rolled loop (small code)
-    for (uint32_t i = tid; i < a.tokens * kME; i += 1024) lg[i] = a.logits[i];
-    __syncthreads();
-    // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
-    const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
-#pragma unroll 1
-    for (uint32_t t = wid; t < a.tokens; t += 16) {
-        uint32_t k[kME / 64];
-#pragma unroll
-        for (uint32_t q = 0; q < kME / 64; ++q) k[q] = ord_key(lg[t * kME + lane + 64 * q]);
+    const uint32_t tid = threadIdx.x, lane = lane_id();
+    const uint32_t T = a.tokens, pairs = T * kTopK;
+    const uint32_t epoch = __hip_atomic_load(&g_plan_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (blockIdx.x < T) {
+        if (tid >= 64) return;
+        const uint32_t t = blockIdx.x;
+        // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
+        const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
         Route r;
-        route_topk_keys<kME / 64>(k, a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
+        route_topk<kME / 64>(a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
 #pragma unroll
         for (int s = 0; s < kTopK; ++s) {
             if (lane == (uint32_t)s) {
-                const uint32_t p = t * kTopK + s;
-                sid[p] = r.id[s];
-                a.ids[p] = r.id[s];
-                a.weights[p] = r.w[s];
-                atomicOr(&mask[r.id[s]][p >> 5], 1u << (p & 31));
+                __hip_atomic_store(a.ids + t * kTopK + s, r.id[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                a.weights[t * kTopK + s] = r.w[s];
             }
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0) __hip_atomic_store(&g_plan_sync[32 + t], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    for (uint32_t i = tid; i < kME * kWords; i += 256) (&mask[0][0])[i] = 0u;
+    __shared__ uint32_t late;
+    if (tid < 64) {
+        uint32_t spins = 0;
+        while (true) {
+            const uint32_t f = lane < T ? __hip_atomic_load(&g_plan_sync[32 + lane], __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT)
+                                        : epoch;
+            if (__all(f == epoch)) break;
+            if (++spins >= kPlanSpins) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (tid == 0) late = spins >= kPlanSpins ? 1u : 0u;
+    }
+    __syncthreads();  // every token flagged (or the wait ran out); the masks cleared
+    if (late) {
+        // no grouping from ids that may be unwritten: an empty plan, every pair on row 0 (the
+        // consumers stay in bounds), the wait counted for the host
+        for (uint32_t p = tid; p < pairs; p += 256) {
+            a.pair_row[p] = 0u;
+            a.row_token[p] = 0u;
+        }
+        if (tid == 0) {
+            a.plan[0] = 0u;
+            a.plan[1] = 1u;
+            if (a.errc) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    for (uint32_t p = tid; p < pairs; p += 256) {
+        const uint32_t e = __hip_atomic_load(a.ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sid[p] = e;
+        atomicOr(&mask[e][p >> 5], 1u << (p & 31));
     }
     __syncthreads();
     // counts and the two prefix sums (rows, segments) over the experts: a log-step scan
@@ -169,7 +211,10 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
         const uint32_t incl = scan[src][tid];
         const uint32_t own = scan[src][tid] - (tid ? scan[src][tid - 1] : 0u);
         const uint32_t c = own & 0xffffu, off = (incl & 0xffffu) - c, sg = (incl >> 16) - (c ? 1u : 0u);
-        if (tid == kME - 1) a.plan[0] = incl >> 16;  // segments
+        if (tid == kME - 1) {
+            a.plan[0] = incl >> 16;  // segments
+            a.plan[1] = 0u;          // the wait ended in time
+        }
         if (c) {
             a.seg_expert[sg] = tid;
             a.seg_start[sg] = off;
@@ -177,7 +222,7 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
         }
     }
     // every pair's row: its expert's offset plus the pairs before it on that expert
-    for (uint32_t p = tid; p < pairs; p += 1024) {
+    for (uint32_t p = tid; p < pairs; p += 256) {
         const uint32_t e = sid[p];
         uint32_t rank = __popc(mask[e][p >> 5] & ((1u << (p & 31)) - 1u));
         for (uint32_t w = 0; w < (p >> 5); ++w) rank += __popc(mask[e][w]);
@@ -187,6 +232,9 @@ __global__ __launch_bounds__(1024) void k_moe_plan(const MoeArgs a) {
         a.pair_row[p] = row;
         a.row_token[row] = p / kTopK;
     }
+    // the epoch this launch used, for the next launch (every wavefront here is past its reads of
+    // the flags; the ranking workgroups are done)
+    if (tid == 0) __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ 4/6. grouped FP8 GEMM on the matrix cores
@@ -482,7 +530,7 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
     const uint32_t segs_max = P < kME ? P : kME;
     OMEGA_LAUNCH(k_moe_prep, dim3(T), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_router, dim3(kME, (T + 3) / 4), dim3(64), 0, st, a);
-    OMEGA_LAUNCH(k_moe_plan, dim3(1), dim3(1024), 0, st, a);
+    OMEGA_LAUNCH(k_moe_plan, dim3(T + 1), dim3(256), 0, st, a);
     if (T < kMoeGemvMax) {
         // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
         OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);
@@ -642,7 +690,7 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     const size_t work = moe_work_bytes(tokens);
     const size_t o_h = work, o_out = o_h + hb, o_ids = o_out + hb, o_w = o_ids + ib;
     if (!ensure_scratch(F_GEMM, c, o_w + ib)) return OMEGA_GPU_CHIP_FAIL;
-    if (!ensure_pinned(F_GEMM, c, hb + 2 * ib)) return OMEGA_GPU_CHIP_FAIL;
+    if (!ensure_pinned(F_GEMM, c, hb + 2 * ib + 4)) return OMEGA_GPU_CHIP_FAIL;
     uint8_t *d = static_cast<uint8_t *>(c->scratch);
     uint8_t *pin = static_cast<uint8_t *>(c->pin);
     MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk);
@@ -656,7 +704,14 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     OMEGA_HIP(F_GEMM, launch_moe_batch(a, c->stream));
     OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin, d + o_out, hb, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin + hb, d + o_ids, 2 * ib, hipMemcpyDeviceToHost, c->stream));
+    OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin + hb + 2 * ib, a.plan + 1, 4, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_GEMM, hipStreamSynchronize(c->stream));
+    uint32_t late = 0;
+    memcpy(&late, pin + hb + 2 * ib, 4);
+    if (late) {
+        set_error(F_GEMM, "moe batch: the plan timed out waiting for the token rankings");
+        return OMEGA_GPU_CHIP_FAIL;
+    }
     memcpy(moe_out, pin, hb);
     memcpy(ids, pin + hb, ib);
     memcpy(weights, pin + hb + ib, ib);
