@@ -233,12 +233,10 @@ struct MoeArgs {
     uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
     uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row
-    float *gp = nullptr;               // [8 k-slices][T * 8][1536] gate|up partial sums
+    float *gp = nullptr;               // [T * 8][768] SwiGLU rows (the GEMV path)
     uint8_t *aq = nullptr;             // [T * 8][6][4][128] split terms of the SwiGLU rows
     float *as = nullptr;               // [T * 8][6][4]
-    float *dp = nullptr;               // [3 k-slices][T * 8][2048] down partial sums
-    float *sink = nullptr;             // [2048]: where the GEMMs' lanes past a segment's rows store
-    uint32_t nt[2] = {16, 8};          // tiles per wavefront (gate|up, down)
+    float *dp = nullptr;               // [T * 8][2048] down rows
     int mutant = 0;  // 1: rank mask id^1; 2: weights not normalised; 5: gate/up swapped;
                      // 6: slot 7 dropped; 7: one activation term
 };

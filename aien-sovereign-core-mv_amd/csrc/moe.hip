@@ -13,11 +13,12 @@
 // weights are the e4m3 bytes as stored; the f32 activations are split per 128-column block into
 // four e4m3 terms with power-of-two scales, x = s1 q1 + s2 q2 + s3 q3 + s4 q4 + r, each term taken
 // from the exact residual of the previous one (so about 16 significant bits survive against fp8's
-// 4), and the four products are summed in f32 with the weight block scale. A wavefront owns 16
-// output features of one expert segment (gate and up features together for SwiGLU) and all of
-// the segment's rows (16 per MFMA column tile). The planner is the one launch whose workgroups
-// hand data over: one workgroup per token ranks its experts, the launch's last workgroup waits on
-// their flags and groups the pairs. The GEMMs exchange nothing; the combine is a launch of its own.
+// 4), and the four products are summed in f32 with the weight block scale. A wavefront owns
+// 16-feature tiles of one expert segment (gate and up tiles together for SwiGLU) over the whole
+// k, for all of the segment's rows (16 per MFMA column tile). The planner is the one launch whose
+// workgroups hand data over: one workgroup per token ranks its experts, the launch's last
+// workgroup waits on their flags and groups the pairs. The gate|up workgroup's wavefronts share
+// only the SwiGLU split's block maxima (LDS); the combine is a launch of its own.
 #include <cmath>
 #include <cstdio>
 
@@ -237,163 +238,238 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     if (tid == 0) __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------------------------------ 4/6. grouped FP8 GEMM on the matrix cores
+// ------------------------------------------------------------------ 4/6. grouped FP8 GEMMs on the matrix cores
+// Both expert projections run over the whole k in one wavefront per (segment, output tiles):
+// each k-block's weights come from the tiled twin (each load instruction 1 KiB contiguous: a
+// 16-rows x 64-bytes operand pattern on row-major weights streams at about 4.8 TB/s against 6
+// TB/s contiguous), the next k-block's in flight while the current one's products run, and the
+// sums stay in registers until the epilogue stores the finished rows. Splitting k over
+// wavefronts instead would write and re-read f32 partial rows (25 MB per gate|up launch at
+// T = 32) and need a launch to add them.
 
-
-// Grouped GEMM on the matrix cores, one independent wavefront per (expert segment, run of NT
-// tiles, k-slice). A tile is 16 gate features j0..j0+15 and their 16 up features (gate|up) or 32
-// down features (down); a k-slice is KBW 128-column blocks. The wavefront loads its slice of the
-// segment's activation terms once per 16-row column tile, then streams its tiles' weights from
-// the tiled twin (each load instruction 1 KiB contiguous: a 16-rows x 64-bytes operand pattern on
-// row-major weights streams at about 4.8 TB/s against 6 TB/s contiguous), the next tile's in flight
-// while the current tile's products run, and stores the slice's partial sums. No wavefront waits for
-// another (HBM's tail latency would set every tile's pace through a barrier); the consumer adds
-// the k-slices in slice order: the SwiGLU + split kernel for gate|up, the combine for down.
-template <int EPI>  // 0: gate|up, 1: down
-struct MoeGemm {
-    static constexpr int KB = EPI == 0 ? kMH / 128 : kMI / 128;
-    static constexpr int KBW = 2;
-    static constexpr uint32_t SPLITS = KB / KBW;
-    static constexpr uint32_t K = KB * 128;
-    static constexpr uint32_t TILES = EPI == 0 ? kMI / 16 : kMH / 32;
-    static constexpr uint32_t NOUT = EPI == 0 ? 2 * kMI : kMH;  // partial row width
-    static_assert(KB % KBW == 0, "whole k-blocks per slice");
+// gate|up over the whole k on the matrix cores, with SwiGLU and the 4-term split of the SwiGLU
+// rows in the epilogue. A workgroup is (expert segment, 128-value block b of the SwiGLU row):
+// each of its WAVES wavefronts owns TPW 16-row tiles of the block's gate features and the
+// matching up features, and walks the 16 k-blocks for the segment's rows (16 per MFMA column
+// tile), the next k-block's weights (from the tiled twin) and activation terms in flight while
+// the current one's products run. The sum over k stays in registers, so no partial sums leave
+// the chip; the wavefronts meet only to share each split term's block maximum.
+struct MoeGu {
+    static constexpr uint32_t KB = kMH / 128;     // 16 k-blocks
+    static constexpr uint32_t BLOCKS = kMI / 128;  // 6 SwiGLU blocks per row
+    static constexpr uint32_t TPW = 2;             // 16-feature tiles per wavefront
+    static constexpr uint32_t WAVES = 8 / TPW;     // a 128-value block is 8 tiles
+    // one k-block's operands: [tile][gate, up] weights and the column tile's 4 activation terms
+    struct Stage {
+        i32x8 A[TPW][2];
+        i32x8 B[kTerms];
+        f32x4 bs;  // the terms' power-of-two scales
+    };
+    // tg: the wavefront's first gate tile (16 rows each); the up tile of gate tile t is kMI / 16 + t
+    __device__ static void load(Stage &st, const uint8_t *wb, uint32_t tg, uint32_t kb, const uint8_t *xr,
+                                const float *sr, uint32_t lane) {
+#pragma unroll
+        for (uint32_t i = 0; i < TPW; ++i) {
+            st.A[i][0] = ld_tile(wb + ((size_t)(tg + i) * KB + kb) * 2048, lane);
+            st.A[i][1] = ld_tile(wb + ((size_t)(kMI / 16 + tg + i) * KB + kb) * 2048, lane);
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < kTerms; ++t) st.B[t] = ld32_cached(xr + (kb * kTerms + t) * 128);
+        st.bs = *as_global_f32x4(sr + 4 * kb);
+    }
+    // acc[tile][gate, up] += (sum over the terms of A x 2^sbe B) x the k-block's weight scale
+    __device__ static void products(const Stage &st, float wg, float wu, f32x4 (&acc)[TPW][2]) {
+        const int sbe[kTerms] = {e8m0_of(st.bs.x), e8m0_of(st.bs.y), e8m0_of(st.bs.z), e8m0_of(st.bs.w)};
+#pragma unroll
+        for (uint32_t i = 0; i < TPW; ++i) {
+            f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t t = 0; t < kTerms; ++t) {
+                c0 = mfma_fp8_sb(st.A[i][0], st.B[t], c0, sbe[t]);
+                c1 = mfma_fp8_sb(st.A[i][1], st.B[t], c1, sbe[t]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[i][0][q] = fmaf(c0[q], wg, acc[i][0][q]);
+                acc[i][1][q] = fmaf(c1[q], wu, acc[i][1][q]);
+            }
+        }
+    }
 };
 
-
-template <int EPI>
-__global__ __launch_bounds__(256) void k_moe_gemm(const MoeArgs a) {
-    using G = MoeGemm<EPI>;
-    constexpr int KBW = G::KBW;
-    const uint32_t lane = lane_id(), g = lane >> 4, n = lane & 15;
-    const uint32_t nt = a.nt[EPI], groups = G::TILES / nt;
-    const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    const uint32_t split = item % G::SPLITS, rest = item / G::SPLITS;
-    const uint32_t grp = rest % groups, seg = rest / groups;
-    if (seg >= *as_const_u32(a.plan)) return;
-    // wave-uniform words through scalar loads: the weight addresses stay in SGPRs
+__global__ __launch_bounds__(64 * MoeGu::WAVES) void k_moe_gu(const MoeArgs a) {
+    using G = MoeGu;
+    constexpr uint32_t TPW = G::TPW;
+    __shared__ float bmax[2][G::WAVES][16];  // per term parity, wavefront, row of the column tile
+    const uint32_t lane = lane_id(), w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+    const uint32_t b = blockIdx.x % G::BLOCKS, seg = blockIdx.x / G::BLOCKS;
+    if (seg >= *as_const_u32(a.plan)) return;  // the whole workgroup: its waves share seg
     const uint32_t e = as_const_u32(a.seg_expert)[seg], r0 = as_const_u32(a.seg_start)[seg];
     const uint32_t cnt = as_const_u32(a.seg_count)[seg];
-    const uint32_t kb0 = split * KBW, t0 = grp * nt;
-    // the expert's tiled twin: (N / 16) row tiles of KB 2 KiB blocks
-    const uint8_t *wb = EPI == 0 ? a.gu_wt + (size_t)e * 2 * kMI * kMH : a.dn_wt + (size_t)e * kMH * kMI;
-    const float *sb = EPI == 0 ? a.gu_s + (size_t)e * (2 * kMI / 128) * G::KB
-                               : a.dn_s + (size_t)e * (kMH / 128) * G::KB;
-    const uint8_t *xq = EPI == 0 ? a.xq : a.aq;
-    const float *xs = EPI == 0 ? a.xs : a.as;
-    // first feature of the tile's two 16-row halves
-    auto f0 = [&](uint32_t t) { return EPI == 0 ? t * 16 : t * 32; };
-    auto f1 = [&](uint32_t t) { return EPI == 0 ? kMI + t * 16 : t * 32 + 16; };
-    // block (row tile of feature f, the slice's first k-block)
-    auto blk = [&](uint32_t f) { return wb + ((size_t)(f >> 4) * G::KB + kb0) * 2048; };
-    float *part = (EPI == 0 ? a.gp : a.dp) + (size_t)split * a.tokens * kTopK * G::NOUT;
+    const uint8_t *wb = a.gu_wt + (size_t)e * 2 * kMI * kMH;
+    // weight scales of the block's gate rows (row block b) and up rows (row block 6 + b)
+    const cu32 *wsg = as_const_u32(a.gu_s + ((size_t)e * (2 * kMI / 128) + b) * G::KB);
+    const cu32 *wsu = as_const_u32(a.gu_s + ((size_t)e * (2 * kMI / 128) + G::BLOCKS + b) * G::KB);
+    const uint32_t tg = 8 * b + TPW * w;
     for (uint32_t m0 = 0; m0 < cnt; m0 += 16) {
         const bool valid = m0 + n < cnt;
         const uint32_t row = r0 + (valid ? m0 + n : 0);
-        const uint32_t xrow = EPI == 0 ? a.row_token[row] : row;
-        MoeTileA<KBW> cur;
-        cur.load(blk(f0(t0)), blk(f1(t0)), lane);
-        // the column tile's activation terms for this slice
-        const uint8_t *xr = xq + ((size_t)xrow * G::KB + kb0) * kTerms * 128 + 16 * g;
-        const float *sr = xs + ((size_t)xrow * G::KB + kb0) * 4;
-        i32x8 B[KBW][kTerms];
-        int sbe[KBW][kTerms];  // the terms' E8M0 scales
+        const uint32_t xrow = a.row_token[row];
+        const uint8_t *xr = a.xq + (size_t)xrow * G::KB * kTerms * 128 + 16 * g;
+        const float *sr = a.xs + (size_t)xrow * G::KB * 4;
+        // the expert's base taken afresh per column tile: the weight addresses are formed next to
+        // their loads (scalar base + lane offset) instead of all being held in registers
+        const uint8_t *wbt = wb;
+        asm volatile("" : "+s"(wbt));
+        f32x4 acc[TPW][2];
 #pragma unroll
-        for (int j = 0; j < KBW; ++j) {
+        for (uint32_t i = 0; i < TPW; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // two stages take turns over the fully unrolled k-blocks: a stage is reloaded with the
+        // k-block two ahead as soon as its products are issued, and no load reaches past the row
+        G::Stage st[2];
+        G::load(st[0], wbt, tg, 0, xr, sr, lane);
+        G::load(st[1], wbt, tg, 1, xr, sr, lane);
 #pragma unroll
-            for (uint32_t t = 0; t < kTerms; ++t) B[j][t] = ld32_cached(xr + (j * kTerms + t) * 128);
-            const f32x4 v = *as_global_f32x4(sr + 4 * j);
-            sbe[j][0] = e8m0_of(v.x);
-            sbe[j][1] = e8m0_of(v.y);
-            sbe[j][2] = e8m0_of(v.z);
-            sbe[j][3] = e8m0_of(v.w);
+        for (uint32_t kb = 0; kb < G::KB; ++kb) {
+            G::products(st[kb & 1], __uint_as_float(wsg[kb]), __uint_as_float(wsu[kb]), acc);
+            // the products issued here (not sunk below later loads), and no load hoisted above them
+#pragma unroll
+            for (uint32_t i = 0; i < TPW; ++i) asm volatile("" : "+v"(acc[i][0]), "+v"(acc[i][1]));
+            if (kb + 2 < G::KB) G::load(st[kb & 1], wbt, tg, kb + 2, xr, sr, lane);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // lanes past the segment's rows store to the sink: every store is unconditional, so no
-        // branch joins the loop's vector-memory waits
-        float *prow = (valid ? part + (size_t)row * G::NOUT : a.sink) + 4 * g;
-        // tile i's products with the slice's terms; its weight scales come from scalar loads
-        auto tile_out = [&](const MoeTileA<KBW> &T, uint32_t tile) {
-            const cu32 *ws0 = as_const_u32(sb + (size_t)(f0(tile) >> 7) * G::KB + kb0);
-            const cu32 *ws1 = as_const_u32(sb + (size_t)(f1(tile) >> 7) * G::KB + kb0);
-            f32x4 tot[2];
-            tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // lane (g, n): row n's features 128 b + 16 (TPW w + i) + 4 g + q of gate and up
+        float v[TPW][4];
 #pragma unroll
-            for (int j = 0; j < KBW; ++j) {
-                const float w0 = __uint_as_float(ws0[j]), w1 = __uint_as_float(ws1[j]);
-                f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t i = 0; i < TPW; ++i)
 #pragma unroll
-                for (uint32_t t = 0; t < kTerms; ++t) {
-                    c0 = mfma_fp8_sb(T.A[0][j], B[j][t], c0, sbe[j][t]);
-                    c1 = mfma_fp8_sb(T.A[1][j], B[j][t], c1, sbe[j][t]);
+            for (int q = 0; q < 4; ++q) {
+                float gg = acc[i][0][q], uu = acc[i][1][q];
+                if (a.mutant == 5) {
+                    const float t = gg;
+                    gg = uu;
+                    uu = t;
                 }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    tot[0][q] = fmaf(c0[q], w0, tot[0][q]);
-                    tot[1][q] = fmaf(c1[q], w1, tot[1][q]);
-                }
+                v[i][q] = gg / (1.0f + expf(-gg)) * uu;
             }
-            *reinterpret_cast<f32x4 *>(prow + f0(tile)) = tot[0];
-            *reinterpret_cast<f32x4 *>(prow + f1(tile)) = tot[1];
-        };
-        // Two tile sets take turns (nt is even): while one tile's products run, the other set's
-        // tile is in flight, and a set is reloaded as soon as its tile is consumed. The loop body
-        // is one straight path with every load unconditional, so waiting for one set never waits
-        // for the other; the last two tiles are peeled off so no load reaches past the run.
-        MoeTileA<KBW> nx;
-        nx.load(blk(f0(t0 + 1)), blk(f1(t0 + 1)), lane);
-#pragma unroll 1
-        for (uint32_t i = 0; i + 2 < nt; i += 2) {
-            tile_out(cur, t0 + i);
-            cur.load(blk(f0(t0 + i + 2)), blk(f1(t0 + i + 2)), lane);
-            tile_out(nx, t0 + i + 1);
-            nx.load(blk(f0(t0 + i + 3)), blk(f1(t0 + i + 3)), lane);
+        // the 4-term split of the row's block (the steps of split8: each term's power-of-two
+        // scale from the block maximum of what the previous terms left)
+        uint32_t tq[kTerms][TPW];
+        float ts[kTerms];
+#pragma unroll
+        for (uint32_t t = 0; t < kTerms; ++t) {
+            float am = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < TPW; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) am = fmaxf(am, fabsf(v[i][q]));
+            am = xor_max<32>(xor_max<16>(am));  // over the four lanes of row n
+            if (g == 0) bmax[t & 1][w][n] = am;
+            __syncthreads();
+#pragma unroll
+            for (uint32_t u = 0; u < G::WAVES; ++u) am = fmaxf(am, bmax[t & 1][u][n]);
+            float inv;
+            const float sc = pow2_scale(am, inv);
+#pragma unroll
+            for (uint32_t i = 0; i < TPW; ++i) {
+                int p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][0] * inv, v[i][1] * inv, 0, false);
+                p = __builtin_amdgcn_cvt_pk_fp8_f32(v[i][2] * inv, v[i][3] * inv, p, true);
+                tq[t][i] = (uint32_t)p;
+                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(p, false);
+                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(p, true);
+                v[i][0] -= lo.x * sc;
+                v[i][1] -= lo.y * sc;
+                v[i][2] -= hi.x * sc;
+                v[i][3] -= hi.y * sc;
+            }
+            ts[t] = (a.mutant == 7 && t > 0) ? 0.f : sc;
         }
-        tile_out(cur, t0 + nt - 2);
-        tile_out(nx, t0 + nt - 1);
+        if (valid) {
+            uint8_t *qb = a.aq + ((size_t)row * G::BLOCKS + b) * kTerms * 128 + 16 * TPW * w + 4 * g;
+#pragma unroll
+            for (uint32_t t = 0; t < kTerms; ++t)
+#pragma unroll
+                for (uint32_t i = 0; i < TPW; ++i) *reinterpret_cast<uint32_t *>(qb + t * 128 + 16 * i) = tq[t][i];
+            if (w == 0 && g == 0)
+                *reinterpret_cast<f32x4 *>(a.as + ((size_t)row * G::BLOCKS + b) * 4) = f32x4{ts[0], ts[1], ts[2], ts[3]};
+        }
     }
 }
 
-// the gate|up k-slices summed in slice order, SwiGLU, then the split terms of the row (one
-// 16-lane row per 128-value block)
-__global__ __launch_bounds__(256) void k_moe_split_act(const MoeArgs a) {
-    using G = MoeGemm<0>;
-    const uint32_t blk = blockIdx.x * 16 + (threadIdx.x >> 4), j = threadIdx.x & 15;
-    const uint32_t rows = a.tokens * kTopK;
-    const uint32_t row = blk / (kMI / 128), b = blk % (kMI / 128);
-    const bool live = row < rows;
-    const size_t slice = (size_t)rows * G::NOUT;
-    const float *src = a.gp + (size_t)(live ? row : 0) * G::NOUT + 128 * b + 8 * j;
-    float gv[8], uv[8];
+// down over the whole k (6 k-blocks of the SwiGLU row's split terms): a workgroup is (expert
+// segment, 256 output features), each of its four wavefronts owns TPW 16-row tiles, and the
+// finished rows go to dp [row][2048] for the combine.
+struct MoeDn {
+    static constexpr uint32_t KB = kMI / 128;  // 6 k-blocks
+    static constexpr uint32_t TPW = 4;         // 16-feature tiles per wavefront
+    static constexpr uint32_t WAVES = 4;
+    static constexpr uint32_t GROUPS = kMH / (16 * TPW * WAVES);  // workgroups per segment
+    struct Stage {
+        i32x8 A[TPW];
+        i32x8 B[kTerms];
+        f32x4 bs;
+    };
+    __device__ static void load(Stage &st, const uint8_t *wb, uint32_t t0, uint32_t kb, const uint8_t *xr,
+                                const float *sr, uint32_t lane) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) gv[i] = uv[i] = 0.f;
+        for (uint32_t i = 0; i < TPW; ++i) st.A[i] = ld_tile(wb + ((size_t)(t0 + i) * KB + kb) * 2048, lane);
 #pragma unroll
-    for (uint32_t s = 0; s < G::SPLITS; ++s) {
-        const float *p = src + s * slice;
-        const f32x4 g0 = *as_global_f32x4(p), g1 = *as_global_f32x4(p + 4);
-        const f32x4 u0 = *as_global_f32x4(p + kMI), u1 = *as_global_f32x4(p + kMI + 4);
-        const float gs[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float us[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        for (uint32_t t = 0; t < kTerms; ++t) st.B[t] = ld32_cached(xr + (kb * kTerms + t) * 128);
+        st.bs = *as_global_f32x4(sr + 4 * kb);
+    }
+    __device__ static void products(const Stage &st, float ws, f32x4 (&acc)[TPW]) {
+        const int sbe[kTerms] = {e8m0_of(st.bs.x), e8m0_of(st.bs.y), e8m0_of(st.bs.z), e8m0_of(st.bs.w)};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            gv[i] += gs[i];
-            uv[i] += us[i];
+        for (uint32_t i = 0; i < TPW; ++i) {
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t t = 0; t < kTerms; ++t) c = mfma_fp8_sb(st.A[i], st.B[t], c, sbe[t]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[i][q] = fmaf(c[q], ws, acc[i][q]);
         }
     }
-    float v[8];
+};
+
+__global__ __launch_bounds__(64 * MoeDn::WAVES) void k_moe_dn(const MoeArgs a) {
+    using D = MoeDn;
+    constexpr uint32_t TPW = D::TPW;
+    const uint32_t lane = lane_id(), w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+    const uint32_t grp = blockIdx.x % D::GROUPS, seg = blockIdx.x / D::GROUPS;
+    if (seg >= *as_const_u32(a.plan)) return;  // the whole workgroup: its waves share seg
+    const uint32_t e = as_const_u32(a.seg_expert)[seg], r0 = as_const_u32(a.seg_start)[seg];
+    const uint32_t cnt = as_const_u32(a.seg_count)[seg];
+    const uint8_t *wb = a.dn_wt + (size_t)e * kMH * kMI;
+    const uint32_t t0 = (grp * D::WAVES + w) * TPW, f0 = 16 * t0;
+    // the wavefront's 16 TPW features lie in one 128-row scale block
+    const cu32 *ws = as_const_u32(a.dn_s + ((size_t)e * (kMH / 128) + (f0 >> 7)) * D::KB);
+    for (uint32_t m0 = 0; m0 < cnt; m0 += 16) {
+        const bool valid = m0 + n < cnt;
+        const uint32_t row = r0 + (valid ? m0 + n : 0);
+        const uint8_t *xr = a.aq + (size_t)row * D::KB * kTerms * 128 + 16 * g;
+        const float *sr = a.as + (size_t)row * D::KB * 4;
+        const uint8_t *wbt = wb;  // addresses formed next to their loads, as in k_moe_gu
+        asm volatile("" : "+s"(wbt));
+        f32x4 acc[TPW];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float gg = gv[i], uu = uv[i];
-        if (a.mutant == 5) {
-            const float t = gg;
-            gg = uu;
-            uu = t;
+        for (uint32_t i = 0; i < TPW; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        D::Stage st[2];
+        D::load(st[0], wbt, t0, 0, xr, sr, lane);
+        D::load(st[1], wbt, t0, 1, xr, sr, lane);
+#pragma unroll
+        for (uint32_t kb = 0; kb < D::KB; ++kb) {
+            D::products(st[kb & 1], __uint_as_float(ws[kb]), acc);
+#pragma unroll
+            for (uint32_t i = 0; i < TPW; ++i) asm volatile("" : "+v"(acc[i]));  // as in k_moe_gu
+            if (kb + 2 < D::KB) D::load(st[kb & 1], wbt, t0, kb + 2, xr, sr, lane);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        v[i] = gg / (1.0f + expf(-gg)) * uu;
+        // lane (g, n): row n's features f0 + 16 i + 4 g + q
+        if (valid) {
+            float *o = a.dp + (size_t)row * kMH + f0 + 4 * g;
+#pragma unroll
+            for (uint32_t i = 0; i < TPW; ++i) *reinterpret_cast<f32x4 *>(o + 16 * i) = acc[i];
+        }
     }
-    u32x2 q[kTerms];
-    float sc[kTerms];
-    split8(v, q, sc, a.mutant == 7);  // every lane of the 16-lane row takes part (the block maximum)
-    if (live) store_split(a.aq, a.as, row, kMI / 128, b, j, q, sc);
 }
 
 // ------------------------------------------------------------------ 4/6 below kMoeGemvMax tokens: grouped GEMVs
@@ -506,20 +582,15 @@ __global__ __launch_bounds__(256) void k_moe_dn_rows(const MoeArgs a) {
 }
 
 // ------------------------------------------------------------------ 7. combine (slot order from zero) [+ residual]
-// each slot's down row is its SPLITS k-slices summed in slice order
-template <uint32_t SPLITS>
+// each token's moe row: its slots' down rows weighted, summed in slot order from zero
 __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
     const uint32_t t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
-    const size_t slice = (size_t)a.tokens * kTopK * kMH;
     float moe = 0.f;
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
         const uint32_t row = a.pair_row[t * kTopK + s];
         const float w = (a.mutant == 6 && s == kTopK - 1) ? 0.f : a.weights[t * kTopK + s];
-        float y = 0.f;
-#pragma unroll
-        for (uint32_t k = 0; k < SPLITS; ++k) y += a.dp[k * slice + (size_t)row * kMH + c];
-        moe += w * y;
+        moe += w * a.dp[(size_t)row * kMH + c];
     }
     const size_t o = (size_t)t * kMH + c;
     a.out[o] = a.resid ? a.resid[o] + moe : moe;
@@ -535,15 +606,12 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
         // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
         OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);
         OMEGA_LAUNCH(k_moe_dn_rows, dim3(segs_max * (kMH / 8) / 4), dim3(256), 0, st, a);
-        OMEGA_LAUNCH(k_moe_combine<1>, dim3(T, kMH / 256), dim3(256), 0, st, a);
+        OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
         return hipGetLastError();
     }
-    const uint32_t w0 = segs_max * (MoeGemm<0>::TILES / a.nt[0]) * MoeGemm<0>::SPLITS;
-    const uint32_t w1 = segs_max * (MoeGemm<1>::TILES / a.nt[1]) * MoeGemm<1>::SPLITS;
-    OMEGA_LAUNCH(k_moe_gemm<0>, dim3((w0 + 3) / 4), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_split_act, dim3((P * (kMI / 128) + 15) / 16), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_gemm<1>, dim3((w1 + 3) / 4), dim3(256), 0, st, a);
-    OMEGA_LAUNCH(k_moe_combine<MoeGemm<1>::SPLITS>, dim3(T, kMH / 256), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_moe_gu, dim3(segs_max * MoeGu::BLOCKS), dim3(64 * MoeGu::WAVES), 0, st, a);
+    OMEGA_LAUNCH(k_moe_dn, dim3(segs_max * MoeDn::GROUPS), dim3(64 * MoeDn::WAVES), 0, st, a);
+    OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -571,14 +639,10 @@ size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens) {
     a.seg_count = reinterpret_cast<uint32_t *>(take(kME * 4));
     a.pair_row = reinterpret_cast<uint32_t *>(take(P * 4));
     a.row_token = reinterpret_cast<uint32_t *>(take(P * 4));
-    a.gp = reinterpret_cast<float *>(take(MoeGemm<0>::SPLITS * P * MoeGemm<0>::NOUT * 4));
+    a.gp = reinterpret_cast<float *>(take(P * kMI * 4));  // the SwiGLU rows of the GEMV path
     a.aq = take(P * (kMI / 128) * kTerms * 128);
     a.as = reinterpret_cast<float *>(take(P * (kMI / 128) * 16));
-    a.dp = reinterpret_cast<float *>(take(MoeGemm<1>::SPLITS * P * MoeGemm<1>::NOUT * 4));
-    a.sink = reinterpret_cast<float *>(take(kMH * 4));
-    // tiles per wavefront: long runs once there are segments enough to fill the chip
-    a.nt[0] = tokens >= 8 ? 16 : 2;
-    a.nt[1] = tokens >= 8 ? 8 : 2;
+    a.dp = reinterpret_cast<float *>(take(P * kMH * 4));
     return o;
 }
 
