@@ -126,10 +126,60 @@ __global__ __launch_bounds__(64) void k_moe_router(const MoeArgs a) {
 // prefix sums and every pair's row. The epoch lives in device memory: each launch reads the word
 // the previous launch's grouping workgroup left and flags with one more; the grouping workgroup
 // writes it back as it finishes, so consecutive launches (one stream, kernel boundaries between
-// them) never mistake an old flag for a new one.
+// them) never mistake an old flag for a new one. Up to kPlanSolo tokens the launch is one
+// workgroup whose wavefronts rank the tokens side by side straight into LDS (no handoff).
 constexpr uint32_t kPlanSpins = 1u << 22;  // bounded wait (seconds)
+constexpr uint32_t kPlanSolo = 4;           // up to this many tokens: one workgroup, no handoff
 // [0] the last launch's epoch, [32 + t] token t's flag; zero at load, one array per device
 static __device__ __align__(256) uint32_t g_plan_sync[32 + kMoeMaxTokens];
+
+// The grouping from the pairs' expert ids (sid) and expert masks in LDS: per-expert counts, the
+// row and segment prefix sums, the segment tables and every pair's grouped row.
+__device__ __forceinline__ void moe_group(const MoeArgs &a, const uint32_t *sid,
+                                          uint32_t (&mask)[kME][kMoeMaxTokens * kTopK / 32],
+                                          uint32_t (&scan)[2][kME], uint32_t tid, uint32_t pairs) {
+    constexpr uint32_t kWords = kMoeMaxTokens * kTopK / 32;
+    // counts and the two prefix sums (rows, segments) over the experts: a log-step scan
+    if (tid < kME) {
+        uint32_t c = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kWords; ++w) c += __popc(mask[tid][w]);
+        scan[0][tid] = c | (c ? 1u << 16 : 0u);
+    }
+    __syncthreads();
+    uint32_t src = 0;
+#pragma unroll
+    for (uint32_t d = 1; d < kME; d <<= 1) {
+        if (tid < kME) scan[src ^ 1][tid] = scan[src][tid] + (tid >= d ? scan[src][tid - d] : 0u);
+        src ^= 1;
+        __syncthreads();
+    }
+    if (tid < kME) {  // inclusive sums -> this expert's row offset and segment index
+        const uint32_t incl = scan[src][tid];
+        const uint32_t own = scan[src][tid] - (tid ? scan[src][tid - 1] : 0u);
+        const uint32_t c = own & 0xffffu, off = (incl & 0xffffu) - c, sg = (incl >> 16) - (c ? 1u : 0u);
+        if (tid == kME - 1) {
+            a.plan[0] = incl >> 16;  // segments
+            a.plan[1] = 0u;          // the wait ended in time
+        }
+        if (c) {
+            a.seg_expert[sg] = tid;
+            a.seg_start[sg] = off;
+            a.seg_count[sg] = c;
+        }
+    }
+    // every pair's row: its expert's offset plus the pairs before it on that expert
+    for (uint32_t p = tid; p < pairs; p += 256) {
+        const uint32_t e = sid[p];
+        uint32_t rank = __popc(mask[e][p >> 5] & ((1u << (p & 31)) - 1u));
+        for (uint32_t w = 0; w < (p >> 5); ++w) rank += __popc(mask[e][w]);
+        const uint32_t incl = scan[src][e] & 0xffffu;
+        const uint32_t own = incl - (e ? (scan[src][e - 1] & 0xffffu) : 0u);
+        const uint32_t row = incl - own + rank;
+        a.pair_row[p] = row;
+        a.row_token[row] = p / kTopK;
+    }
+}
 
 __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     constexpr uint32_t kWords = kMoeMaxTokens * kTopK / 32;
@@ -138,12 +188,36 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     __shared__ uint32_t scan[2][kME];       // count | (count > 0) << 16, prefix-summed
     const uint32_t tid = threadIdx.x, lane = lane_id();
     const uint32_t T = a.tokens, pairs = T * kTopK;
+    // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
+    const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
+    if (gridDim.x == 1) {
+        // up to kPlanSolo tokens: this workgroup's wavefront t ranks token t straight into LDS,
+        // with no handoff between workgroups
+        for (uint32_t i = tid; i < kME * kWords; i += 256) (&mask[0][0])[i] = 0u;
+        __syncthreads();  // masks cleared before any wavefront marks its pairs
+        const uint32_t t = tid >> 6;
+        if (t < T) {
+            Route r;
+            route_topk<kME / 64>(a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
+#pragma unroll
+            for (int sl = 0; sl < kTopK; ++sl) {
+                if (lane == (uint32_t)sl) {
+                    const uint32_t p = t * kTopK + sl;
+                    sid[p] = r.id[sl];
+                    a.ids[p] = r.id[sl];
+                    a.weights[p] = r.w[sl];
+                    atomicOr(&mask[r.id[sl]][p >> 5], 1u << (p & 31));
+                }
+            }
+        }
+        __syncthreads();
+        moe_group(a, sid, mask, scan, tid, pairs);
+        return;
+    }
     const uint32_t epoch = __hip_atomic_load(&g_plan_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     if (blockIdx.x < T) {
         if (tid >= 64) return;
         const uint32_t t = blockIdx.x;
-        // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
-        const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
         Route r;
         route_topk<kME / 64>(a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
 #pragma unroll
@@ -193,46 +267,7 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
         atomicOr(&mask[e][p >> 5], 1u << (p & 31));
     }
     __syncthreads();
-    // counts and the two prefix sums (rows, segments) over the experts: a log-step scan
-    if (tid < kME) {
-        uint32_t c = 0;
-#pragma unroll
-        for (uint32_t w = 0; w < kWords; ++w) c += __popc(mask[tid][w]);
-        scan[0][tid] = c | (c ? 1u << 16 : 0u);
-    }
-    __syncthreads();
-    uint32_t src = 0;
-#pragma unroll
-    for (uint32_t d = 1; d < kME; d <<= 1) {
-        if (tid < kME) scan[src ^ 1][tid] = scan[src][tid] + (tid >= d ? scan[src][tid - d] : 0u);
-        src ^= 1;
-        __syncthreads();
-    }
-    if (tid < kME) {  // inclusive sums -> this expert's row offset and segment index
-        const uint32_t incl = scan[src][tid];
-        const uint32_t own = scan[src][tid] - (tid ? scan[src][tid - 1] : 0u);
-        const uint32_t c = own & 0xffffu, off = (incl & 0xffffu) - c, sg = (incl >> 16) - (c ? 1u : 0u);
-        if (tid == kME - 1) {
-            a.plan[0] = incl >> 16;  // segments
-            a.plan[1] = 0u;          // the wait ended in time
-        }
-        if (c) {
-            a.seg_expert[sg] = tid;
-            a.seg_start[sg] = off;
-            a.seg_count[sg] = c;
-        }
-    }
-    // every pair's row: its expert's offset plus the pairs before it on that expert
-    for (uint32_t p = tid; p < pairs; p += 256) {
-        const uint32_t e = sid[p];
-        uint32_t rank = __popc(mask[e][p >> 5] & ((1u << (p & 31)) - 1u));
-        for (uint32_t w = 0; w < (p >> 5); ++w) rank += __popc(mask[e][w]);
-        const uint32_t incl = scan[src][e] & 0xffffu;
-        const uint32_t own = incl - (e ? (scan[src][e - 1] & 0xffffu) : 0u);
-        const uint32_t row = incl - own + rank;
-        a.pair_row[p] = row;
-        a.row_token[row] = p / kTopK;
-    }
+    moe_group(a, sid, mask, scan, tid, pairs);
     // the epoch this launch used, for the next launch (every wavefront here is past its reads of
     // the flags; the ranking workgroups are done)
     if (tid == 0) __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -601,7 +636,7 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
     const uint32_t segs_max = P < kME ? P : kME;
     OMEGA_LAUNCH(k_moe_prep, dim3(T), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_router, dim3(kME, (T + 3) / 4), dim3(64), 0, st, a);
-    OMEGA_LAUNCH(k_moe_plan, dim3(T + 1), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_moe_plan, dim3(T <= kPlanSolo ? 1 : T + 1), dim3(256), 0, st, a);
     if (T < kMoeGemvMax) {
         // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
         OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);

@@ -57,7 +57,7 @@ def bf16_rows(oracle, rng, T):
     return oracle.bf16_to_f32(oracle.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32)))
 
 
-@pytest.mark.parametrize("T", [1, 4, 15, 16, 17, 32, 64])
+@pytest.mark.parametrize("T", [1, 3, 4, 5, 15, 16, 17, 32, 64])
 def test_moe_block_matches_the_oracle(omega, oracle, model, T):
     h = bf16_rows(oracle, np.random.default_rng(100 + T), T)
     out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
@@ -110,7 +110,7 @@ def test_device_entry_adds_the_residual(omega, oracle, model):
 
 
 @pytest.mark.parametrize("T,mutant", [(32, 1), (32, 2), (32, 5), (32, 6), (32, 7),
-                                       (8, 1), (8, 2), (8, 5), (8, 6)])
+                                       (8, 1), (8, 2), (8, 5), (8, 6), (3, 1), (3, 2)])
 def test_moe_mutants_are_caught(omega, oracle, model, T, mutant):
     h = bf16_rows(oracle, np.random.default_rng(11), T)
     want, want_ids, want_w = oracle_block(oracle, model, h)
