@@ -208,25 +208,36 @@ def bench_gemv(om, args):
     om.sync()
     stream = lib.omega_gpu_stream()
     graph, exe = C.c_void_p(), C.c_void_p()
-    assert h.hipStreamBeginCapture(C.c_void_p(stream), 1) == 0   # hipStreamCaptureModeThreadLocal
-    for t in ts:
-        assert lib.omega_gpu_fp8_gemv_dev(t.as_raw(), 0, x.ptr, y.ptr) == 0
-    assert h.hipStreamEndCapture(C.c_void_p(stream), C.byref(graph)) == 0
-    assert h.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)) == 0
+
+    def direct():
+        for t in ts:
+            assert lib.omega_gpu_fp8_gemv_dev(t.as_raw(), 0, x.ptr, y.ptr) == 0
+
+    if args.eager:  # the same launches made directly (a kernel trace cannot follow a graph replay)
+        run = direct
+    else:
+        assert h.hipStreamBeginCapture(C.c_void_p(stream), 1) == 0   # hipStreamCaptureModeThreadLocal
+        direct()
+        assert h.hipStreamEndCapture(C.c_void_p(stream), C.byref(graph)) == 0
+        assert h.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)) == 0
+
+        def run():
+            assert h.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
     timer = om.StreamTimer()
     reps = args.gemv_reps
     for _ in range(2):
-        assert h.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
+        run()
     timer.start()
     for _ in range(reps):
-        assert h.hipGraphLaunch(exe, C.c_void_p(stream)) == 0
+        run()
     timer.stop()
     ms = timer.ms()
     us = ms * 1e3 / (reps * GEMV_COPIES)
     b = gemv_bytes()
     gbs = b / (us * 1e3)
-    h.hipGraphExecDestroy(exe)
-    h.hipGraphDestroy(graph)
+    if not args.eager:
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
     cpu = None if args.no_cpu else gemv_cpu_baseline()
     print(json.dumps({
         "metric": "FP8 block-scaled GEMV 5120 x 2048 (configuration 1), achieved HBM GB/s vs peak",
@@ -234,7 +245,8 @@ def bench_gemv(om, args):
         "us_per_gemv": round(us, 3), "gemvs": reps * GEMV_COPIES,
         "dtype": "fp8 (e4m3 weights, f32 activations, fp32 accumulate)",
         "data": "synthetic N(0, 0.02) weights block-quantised to e4m3, bf16 N(0,1) row",
-        "config": {"workload": "q|k|v GEMV 5120 x 2048, 48 weight copies, hipGraph of 48 launches"},
+        "config": {"workload": "q|k|v GEMV 5120 x 2048, 48 weight copies, "
+                               + ("48 direct launches" if args.eager else "hipGraph of 48 launches")},
         "roofline": {"bound": "hbm", "kernel": "k_fp8_rows", "achieved": round(gbs, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu}), flush=True)
