@@ -118,12 +118,14 @@ __global__ __launch_bounds__(256) void k_bd_rows(const BdArgs a) {
 }
 
 // ------------------------------------------------------------------ dense FP8 GEMM (the batch's rows)
-// A wavefront = (32-row tile, k-slice of 2 blocks), all T <= 16 MT rows: the tile's weights
-// (8 KiB from the tiled twin, 1 KiB contiguous per load instruction) and the slice's activation
-// terms of every row go out together, one round trip, then the products and the partial sums
-// of the k-slice. One tile per wavefront puts the whole weight stream in flight at once (q|k|v:
-// 160 tiles x 8 slices = 1280 wavefronts). Scales come through scalar loads and every store is
-// unconditional (rows past T write the sink), so no wait merges over a branch.
+// A workgroup = (4 tiles of 32 weight rows, k-slice of 2 blocks), all T <= 16 MT rows. The
+// slice's activation terms of every row (16 MT rows x 1 KiB) are staged once per workgroup in
+// LDS, so each of the four wavefronts reads them there instead of from L2 (the terms are four
+// times the weights' bytes per wavefront); each wavefront's tile weights (8 KiB from the tiled
+// twin, 1 KiB contiguous per load instruction) go out first, then the products and the partial
+// sums of the k-slice. One tile per wavefront puts the whole weight stream in flight at once
+// (q|k|v: 160 tiles x 8 slices = 1280 wavefronts). Scales come through scalar loads and every
+// store is unconditional (rows past T write the sink), so no wait merges over a branch.
 struct DenseArgs {
     const uint8_t *wt = nullptr;  // tiled twin of a [1][n][k] FP8 tensor
     const float *s = nullptr;     // [n/128][k/128]
@@ -135,28 +137,38 @@ struct DenseArgs {
     float *sink = nullptr;        // [64]: where the lanes of rows past T store
 };
 
-template <int MT>
+// k-blocks per slice: q|k|v (k = 2048) 2, o_proj (k = 4096) 4, so both write 8 k-slices
+constexpr uint32_t dense_kbw(uint32_t k) { return k >= 4096 ? 4 : 2; }
+constexpr uint32_t kDenseSlices = 8;
+
+template <int MT, int KBW>
 __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
-    constexpr int KBW = 2;
-    const uint32_t lane = lane_id(), g = lane >> 4, n = lane & 15;
-    const uint32_t KB = a.k / 128, splits = KB / KBW, tiles = a.n / 32;
-    const uint32_t item = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    const uint32_t split = item % splits, tile = item / splits;
-    if (tile >= tiles) return;
+    constexpr uint32_t kDenseRowBytes = KBW * kTerms * 128;  // a row's terms of one slice
+    constexpr uint32_t kDensePitch = kDenseRowBytes + 16;     // LDS row pitch (rows 4 banks apart)
+    __shared__ __align__(16) uint8_t bl[MT * 16 * kDensePitch];
+    const uint32_t lane = lane_id(), g = lane >> 4, n = lane & 15, wid = threadIdx.x >> 6;
+    const uint32_t KB = a.k / 128, splits = KB / KBW;
+    const uint32_t split = blockIdx.x % splits, tile = (blockIdx.x / splits) * 4 + wid;
     const uint32_t kb0 = split * KBW;
     MoeTileA<KBW> A;
     A.load(a.wt + ((size_t)(2 * tile) * KB + kb0) * 2048, a.wt + ((size_t)(2 * tile + 1) * KB + kb0) * 2048, lane);
-    i32x8 B[MT][KBW][kTerms];
+    // the slice's terms of all 16 MT rows (rows past T repeat row T - 1): 1 KiB contiguous per row
+    constexpr uint32_t kChunks = MT * 16 * kDenseRowBytes / 16;
+    u32x4 st[kChunks / 256];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks / 256; ++c) {
+        const uint32_t ch = threadIdx.x + 256 * c, row = ch / (kDenseRowBytes / 16), off = 16 * (ch % (kDenseRowBytes / 16));
+        const uint32_t tok = min(row, a.T - 1);
+        st[c] = *as_global(a.xq + ((size_t)tok * KB + kb0) * kTerms * 128 + off);
+    }
+    // the terms' scales of the lane's rows
     int sbe[MT][KBW][kTerms];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const uint32_t tok = min(16 * m + n, a.T - 1);
-        const uint8_t *xr = a.xq + ((size_t)tok * KB + kb0) * kTerms * 128 + 16 * g;
         const float *sr = a.xs + ((size_t)tok * KB + kb0) * 4;
 #pragma unroll
         for (int j = 0; j < KBW; ++j) {
-#pragma unroll
-            for (uint32_t t = 0; t < kTerms; ++t) B[m][j][t] = ld32_cached(xr + (j * kTerms + t) * 128);
             const f32x4 v = *as_global_f32x4(sr + 4 * j);
             sbe[m][j][0] = e8m0_of(v.x);
             sbe[m][j][1] = e8m0_of(v.y);
@@ -164,10 +176,27 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
             sbe[m][j][3] = e8m0_of(v.w);
         }
     }
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks / 256; ++c) {
+        const uint32_t ch = threadIdx.x + 256 * c, row = ch / (kDenseRowBytes / 16), off = 16 * (ch % (kDenseRowBytes / 16));
+        *reinterpret_cast<u32x4 *>(bl + row * kDensePitch + off) = st[c];
+    }
+    __syncthreads();  // n is a multiple of 128, so every wavefront has a tile
     const cu32 *ws = as_const_u32(a.s + (size_t)((32 * tile) >> 7) * KB + kb0);
     float *part = a.part + (size_t)split * a.T * a.n;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
+        // lane (g, n): row 16 m + n, bytes 16 g and 64 + 16 g of each 128-byte term
+        const uint8_t *br = bl + (16 * m + n) * kDensePitch + 16 * g;
+        i32x8 B[KBW][kTerms];
+#pragma unroll
+        for (int j = 0; j < KBW; ++j)
+#pragma unroll
+            for (uint32_t t = 0; t < kTerms; ++t) {
+                const u32x4 lo = *reinterpret_cast<const u32x4 *>(br + (j * kTerms + t) * 128);
+                const u32x4 hi = *reinterpret_cast<const u32x4 *>(br + (j * kTerms + t) * 128 + 64);
+                B[j][t] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
         f32x4 tot[2];
         tot[0] = tot[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -176,8 +205,8 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
             f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (uint32_t t = 0; t < kTerms; ++t) {
-                c0 = mfma_fp8_sb(A.A[0][j], B[m][j][t], c0, sbe[m][j][t]);
-                c1 = mfma_fp8_sb(A.A[1][j], B[m][j][t], c1, sbe[m][j][t]);
+                c0 = mfma_fp8_sb(A.A[0][j], B[j][t], c0, sbe[m][j][t]);
+                c1 = mfma_fp8_sb(A.A[1][j], B[j][t], c1, sbe[m][j][t]);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -193,9 +222,17 @@ __global__ __launch_bounds__(256) void k_dense_gemm(const DenseArgs a) {
 }
 
 hipError_t launch_dense_gemm(const DenseArgs &a, hipStream_t st) {
-    const uint32_t waves = (a.k / 256) * (a.n / 32);
-    if (a.T <= 16) OMEGA_LAUNCH(k_dense_gemm<1>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
-    else OMEGA_LAUNCH(k_dense_gemm<2>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    // workgroups of 4 tiles of 32 rows, one per (tile group, k-slice)
+    const uint32_t kbw = dense_kbw(a.k);
+    if (a.n % 128 || a.k != kDenseSlices * 128 * kbw || a.T == 0 || a.T > 32) return hipErrorInvalidValue;
+    const uint32_t wgs = kDenseSlices * (a.n / 128);
+    if (kbw == 2) {
+        if (a.T <= 16) OMEGA_LAUNCH((k_dense_gemm<1, 2>), dim3(wgs), dim3(256), 0, st, a);
+        else OMEGA_LAUNCH((k_dense_gemm<2, 2>), dim3(wgs), dim3(256), 0, st, a);
+    } else {
+        if (a.T <= 16) OMEGA_LAUNCH((k_dense_gemm<1, 4>), dim3(wgs), dim3(256), 0, st, a);
+        else OMEGA_LAUNCH((k_dense_gemm<2, 4>), dim3(wgs), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
@@ -510,7 +547,7 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         m.dn_w = L.dn->w;
         m.h = b->x;
         m.opart = b->o_part;
-        m.oslices = kBdAttn / 256;
+        m.oslices = kDenseSlices;
         m.hout = b->x;
         m.resid = b->x;
         m.out = b->x;
@@ -610,12 +647,12 @@ int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpu
     M((void **)&b->x, (size_t)T * kBdH * 4);
     M((void **)&b->xq, (size_t)T * (kBdH / 128) * kTerms * 128);
     M((void **)&b->xs, (size_t)T * (kBdH / 128) * 16);
-    M((void **)&b->qkv_part, (size_t)(kBdH / 256) * T * kBdQkv * 4);
+    M((void **)&b->qkv_part, (size_t)kDenseSlices * T * kBdQkv * 4);
     M((void **)&b->q, (size_t)T * 32 * 128 * 4);
     M((void **)&b->apart, (size_t)kItemMax * 32 * kPartStride * 4);
     M((void **)&b->oq, (size_t)T * 32 * kTerms * 128);
     M((void **)&b->os, (size_t)T * 32 * 16);
-    M((void **)&b->o_part, (size_t)(kBdAttn / 256) * T * kBdH * 4);
+    M((void **)&b->o_part, (size_t)kDenseSlices * T * kBdH * 4);
     M((void **)&b->sink, 256);
     M((void **)&b->hidden, (size_t)T * kBdH * 4);
     M((void **)&b->hid_hi, (size_t)T * kBdH * 2);
