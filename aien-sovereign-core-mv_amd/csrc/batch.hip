@@ -14,9 +14,11 @@
 // GEMM with the argmax folded in. Only the MoE planner exchanges data between the workgroups of
 // one launch (its rankings, then the grouping).
 //
-// Per layer: rows (norm + split) | q|k|v GEMM (k-slice partials) | q/k norm, RoPE, K/V append |
-// paged attention items | combine + split | o GEMM (k-slice partials) | MoE block (7 launches,
-// its first adds the o partials into the residual). Then final norm | lm_head + argmax.
+// Per layer: rows (the previous layer's MoE combine into the residual, norm + split) | q|k|v GEMM
+// (k-slice partials) | q/k norm, RoPE, K/V append | paged attention items | combine + split |
+// o GEMM (k-slice partials) | MoE block (5 launches, its first adds the o partials into the
+// residual; its combine is left to the next rows launch). Then final norm (with the last
+// layer's combine) | lm_head + argmax.
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
@@ -27,6 +29,7 @@
 #include "device.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
+#include "route.hpp"
 #include "runtime.hpp"
 
 namespace omega {
@@ -77,7 +80,32 @@ struct BdArgs {
     float *q = nullptr;               // [T][32][128]
     float *hidden = nullptr;          // [T][2048] final-normed rows
     uint16_t *hid_hi = nullptr, *hid_lo = nullptr;  // their bf16 hi / lo halves
+    // the previous layer's MoE combine, done by this launch (null: none pending)
+    const float *moe_dp = nullptr;         // [T * 8][2048] down rows
+    const uint32_t *moe_row = nullptr;     // [T * 8] grouped row of pair t * 8 + s
+    const float *moe_w = nullptr;          // [T * 8] slot weights
+    int moe_mutant = 0;                    // 6: slot 7 dropped
 };
+
+// x[t][8 tid .. +8] += the token's MoE row: its slots' down rows weighted, summed in slot order
+// from zero (the arithmetic of the MoE block's combine), written back as the residual row
+__device__ __forceinline__ void bd_moe_combine(const BdArgs &a, uint32_t t, uint32_t tid, float *xr, float (&v)[8]) {
+    float moe[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kTopK; ++s) {
+        const uint32_t row = as_const_u32(a.moe_row)[t * kTopK + s];
+        const float w = (a.moe_mutant == 6 && s == kTopK - 1) ? 0.f : __uint_as_float(as_const_u32(a.moe_w)[t * kTopK + s]);
+        const float *y = a.moe_dp + (size_t)row * kBdH + 8 * tid;
+        const f32x4 y0 = *as_global_f32x4(y), y1 = *as_global_f32x4(y + 4);
+        const float yv[8] = {y0.x, y0.y, y0.z, y0.w, y1.x, y1.y, y1.z, y1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) moe[i] += w * yv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = v[i] + moe[i];
+    *reinterpret_cast<f32x4 *>(xr) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4 *>(xr + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
 
 // ------------------------------------------------------------------ rows: (embedding) + RMSNorm + split
 __global__ __launch_bounds__(256) void k_bd_rows(const BdArgs a) {
@@ -99,6 +127,7 @@ __global__ __launch_bounds__(256) void k_bd_rows(const BdArgs a) {
         const f32x4 h0 = *as_global_f32x4(xr), h1 = *as_global_f32x4(xr + 4);
         v[0] = h0.x; v[1] = h0.y; v[2] = h0.z; v[3] = h0.w;
         v[4] = h1.x; v[5] = h1.y; v[6] = h1.z; v[7] = h1.w;
+        if (a.moe_dp) bd_moe_combine(a, t, tid, xr, v);
     }
     const f32x4 w0 = *as_global_f32x4(a.norm_w + 8 * tid), w1 = *as_global_f32x4(a.norm_w + 8 * tid + 4);
     const float nw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -289,9 +318,10 @@ __global__ __launch_bounds__(64) void k_bd_qkv(const BdArgs a) {
 __global__ __launch_bounds__(256) void k_bd_final(const BdArgs a) {
     __shared__ double red[4];
     const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wid = tid >> 6;
-    const float *xr = a.x + (size_t)t * kBdH + 8 * tid;
+    float *xr = a.x + (size_t)t * kBdH + 8 * tid;
     const f32x4 h0 = *as_global_f32x4(xr), h1 = *as_global_f32x4(xr + 4);
     float v[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    if (a.moe_dp) bd_moe_combine(a, t, tid, xr, v);
     const f32x4 w0 = *as_global_f32x4(a.norm_w + 8 * tid), w1 = *as_global_f32x4(a.norm_w + 8 * tid + 4);
     const float nw[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     double ss = 0.0;
@@ -555,7 +585,12 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         m.weights = b->route_w + (size_t)l * kBdMaxSeqs * 8;
         m.mutant = knobs().moe_mutant;
         m.errc = &b->io->moe_late[0];
+        m.defer_combine = 1;  // the next layer's rows launch (or the final norm) adds the MoE rows
         OMEGA_HIP(F_SESSION, launch_moe_batch(m, st));
+        a.moe_dp = m.dp;
+        a.moe_row = m.pair_row;
+        a.moe_w = m.weights;
+        a.moe_mutant = m.mutant;
     }
     a.norm_w = b->final_norm;
     OMEGA_LAUNCH(k_bd_final, dim3(T), dim3(256), 0, st, a);

@@ -230,6 +230,7 @@ struct MoeArgs {
     float *logits = nullptr;           // [T][128]
     uint32_t *plan = nullptr;          // [0]: segments, [1]: 1 when the planner's wait ran out
     uint32_t *errc = nullptr;          // optional: counts the planner's waits that ran out
+    int defer_combine = 0;             // 1: no combine launch; the caller adds the dp rows
     uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
     uint32_t *row_token = nullptr;     // [T * 8]: token of grouped row

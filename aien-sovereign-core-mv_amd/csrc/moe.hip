@@ -641,12 +641,12 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
         // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
         OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);
         OMEGA_LAUNCH(k_moe_dn_rows, dim3(segs_max * (kMH / 8) / 4), dim3(256), 0, st, a);
-        OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
+        if (!a.defer_combine) OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
         return hipGetLastError();
     }
     OMEGA_LAUNCH(k_moe_gu, dim3(segs_max * MoeGu::BLOCKS), dim3(64 * MoeGu::WAVES), 0, st, a);
     OMEGA_LAUNCH(k_moe_dn, dim3(segs_max * MoeDn::GROUPS), dim3(64 * MoeDn::WAVES), 0, st, a);
-    OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
+    if (!a.defer_combine) OMEGA_LAUNCH(k_moe_combine, dim3(T, kMH / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
