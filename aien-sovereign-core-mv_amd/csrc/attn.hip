@@ -1076,8 +1076,8 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 // and dims in order for the matrix-core kernels; either way partial dim d sits at 4 + d, so one
 // combine serves all. One wavefront per (seq, q head, quarter of the dims): lane l covers dim
 // 32 q + l % 32 of the slots of parity l / 32, so a workgroup reads 8 KiB of partials per 64
-// slots (a CU's loads share one queue). CH chunks of 64 slots: 1 for up to 64 splits, 4 for up
-// to 256.
+// slots (a CU's loads share one queue). CH chunks of 64 slots (1: up to 16 splits here; more
+// splits take k_attn_combine_wide).
 template <int CH>
 __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
     __shared__ float wsh[64 * CH];
@@ -1130,9 +1130,77 @@ __global__ __launch_bounds__(64) void k_attn_combine(const CombineArgs a) {
     if (lane < 32) a.out[((size_t)b * a.qh + head) * 128 + d] = O * (a.out_scale / L);
 }
 
+// More than 16 splits (up to kCombineWideMax): workgroup (head, quarter of the dims, sequence) of 256
+// threads. Thread t holds the (m, l) of split t and the f32x4 pieces (split
+// 32 k + t / 8, dims 4 (t % 8) ..) of its quarter, all loaded in one round trip (8 vector loads
+// per 256 splits instead of 128 scalar loads per lane); the maximum and the sum of the weighted l
+// are workgroup reductions, and the 32 split groups' sums meet in LDS, added in group order.
+constexpr uint32_t kCombineWideMax = 256;
+
+template <uint32_t KMAX>  // split rows per thread: up to 32 KMAX splits
+__global__ __launch_bounds__(256) void k_attn_combine_wide(const CombineArgs a) {
+    __shared__ float red[8];
+    __shared__ f32x4 osum[32][8];
+    const uint32_t head = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y, tid = threadIdx.x;
+    const uint32_t lane = lane_id(), w = tid >> 6;
+    const float *pp = a.part + ((size_t)b * a.qh + head) * a.splits * kPartStride;
+    const uint32_t sg = tid >> 3, dc = 4 * (tid & 7);  // split group, dims (within the quarter)
+    const uint32_t jm = min(tid, a.splits - 1);
+    const float mr = *as_global_f32(pp + (size_t)jm * kPartStride);
+    const float lr = *as_global_f32(pp + (size_t)jm * kPartStride + 1);
+    f32x4 f[KMAX];
+#pragma unroll
+    for (uint32_t k = 0; k < KMAX; ++k) {
+        const uint32_t j = min(32 * k + sg, a.splits - 1);
+        f[k] = *as_global_f32x4(pp + (size_t)j * kPartStride + 4 + 32 * quarter + dc);
+    }
+    uint32_t tiles;
+    if (a.context_lens) tiles = ((uint32_t)a.context_lens[b] + a.tile_tokens - 1) / a.tile_tokens;
+    else tiles = ((a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host) + a.tile_tokens - 1) / a.tile_tokens;
+    uint32_t active, tps;
+    attn_split_plan(tiles, a.splits, a.tiles_per_split, active, tps);  // active <= splits <= 256
+    // M: the maximum over the active splits
+    float M = tid < active ? mr : -INFINITY;
+    M = row16_max(M);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    if (lane == 0) red[w] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // split t's weight, and L = sum of w l (waves, then in wave order)
+    const float w0 = tid < active ? (a.mutant == 4 ? 1.0f : expf(mr - M)) : 0.f;
+    const float lw = wave_sum(w0 * (tid < active ? lr : 0.f));
+    __shared__ float wsh[kCombineWideMax];
+    wsh[tid] = w0;
+    if (lane == 0) red[4 + w] = lw;
+    __syncthreads();
+    const float L = (red[4] + red[5]) + (red[6] + red[7]);
+    // this thread's splits 32 k + sg in order; slots past `active` are selected out (their
+    // contents may not be finite)
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t k = 0; k < KMAX; ++k) {
+        const uint32_t j = 32 * k + sg;
+        if (j < active) {
+            const float wj = wsh[j];
+            o = f32x4{fmaf(f[k].x, wj, o.x), fmaf(f[k].y, wj, o.y), fmaf(f[k].z, wj, o.z), fmaf(f[k].w, wj, o.w)};
+        }
+    }
+    osum[sg][tid & 7] = o;
+    __syncthreads();
+    if (tid < 32) {
+        float v = 0.f;
+        for (uint32_t g = 0; g < 32; ++g) v += osum[g][tid >> 2][tid & 3];
+        a.out[((size_t)b * a.qh + head) * 128 + 32 * quarter + tid] = v * (a.out_scale / L);
+    }
+}
+
 hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
-    if (a.splits > 64) OMEGA_LAUNCH(k_attn_combine<4>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
-    else OMEGA_LAUNCH(k_attn_combine<1>, dim3(a.qh * 4, a.seqs), dim3(64), 0, st, a);
+    if (a.splits > kCombineWideMax) return hipErrorInvalidValue;
+    const dim3 grid(a.qh * 4, a.seqs);
+    if (a.splits > 128) OMEGA_LAUNCH(k_attn_combine_wide<8>, grid, dim3(256), 0, st, a);
+    else if (a.splits > 64) OMEGA_LAUNCH(k_attn_combine_wide<4>, grid, dim3(256), 0, st, a);
+    else if (a.splits > 16) OMEGA_LAUNCH(k_attn_combine_wide<2>, grid, dim3(256), 0, st, a);
+    else OMEGA_LAUNCH(k_attn_combine<1>, grid, dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
