@@ -124,18 +124,11 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     __shared__ float sp_sh[8];       // split 0: this token's score per head
     const uint32_t lane = threadIdx.x, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
     const uint32_t g = lane >> 4, n = lane & 15;
-    const uint32_t pos = a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host;
-    const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
-    uint32_t active, pps;
-    attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
-    // splits 0..7 of every kv head stay to merge one q head each, with or without pages
-    if (s >= active && s >= 8) return;
-    const bool holds = s < active;
-    const uint32_t p_begin = holds ? s * pps : 0, p_end = holds ? min(pages, p_begin + pps) : 0;
-
     // Every load below is issued unconditionally, the page stream last: vector-memory waits
     // complete in issue order and merge conservatively at branch joins, so a conditional load
-    // here would make the preparation math wait on the page stream.
+    // here would make the preparation math wait on the page stream. The q|k|v row and the norm
+    // weights do not depend on the position, so they go out before the position is read (they
+    // travel while it arrives) rather than after the split plan that needs it.
     const float *qraw = a.qkv + h * 8 * 128;
     float q0[8], q1[8];
 #pragma unroll
@@ -144,14 +137,22 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         q1[r] = *as_global_f32(qraw + r * 128 + 64 + lane);
     }
     const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
-    const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
-    const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
     float k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
     float k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
     const float v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
     const float v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
     const float kw0 = *as_global_f32(a.k_norm + lane);
     const float kw1 = *as_global_f32(a.k_norm + 64 + lane);
+    const uint32_t pos = a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host;
+    const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
+    uint32_t active, pps;
+    attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
+    // splits 0..7 of every kv head stay to merge one q head each, with or without pages
+    if (s >= active && s >= 8) return;
+    const bool holds = s < active;
+    const uint32_t p_begin = holds ? s * pps : 0, p_end = holds ? min(pages, p_begin + pps) : 0;
+    const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
+    const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
     // the first page's K/V stream starts before the preparation math (page 0 stands in when the
     // split has no page: pos == 0)
     DattnPage T;
