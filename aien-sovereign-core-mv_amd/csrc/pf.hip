@@ -13,10 +13,14 @@
 // Every entry is synchronous: it returns after the chip finished, with the chip nanoseconds of
 // its launches (HIP events on the library stream) in *ns, also added to the module's counters.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "device.hpp"
@@ -372,6 +376,89 @@ __global__ __launch_bounds__(256) void k_pf_resid_norm(const PfNormArgs a) {
     for (uint32_t c = t; c < a.k; c += 256) orow[c] = xr[c] * scale * a.w[c];
 }
 
+// ------------------------------------------------------------------ host threads for per-token host work
+// The MoE plan of a long prompt ranks every token on the host (MoeBatchPlan::from_logits). A few
+// threads, started on first use and kept for the process, split such a loop into contiguous
+// ranges; the caller takes a range too. One job at a time (the entry points hold the library
+// lock).
+class HostPool {
+  public:
+    static HostPool &get() {
+        static HostPool p;
+        return p;
+    }
+    uint32_t width() const { return (uint32_t)th_.size() + 1; }
+    // fn(part) for part in 0 .. parts - 1, over the pool and the calling thread. The job lives on
+    // this frame: a thread takes it under the lock and counts itself in `users`, and run() returns
+    // only when every part has finished and no thread still holds the job.
+    void run(uint32_t parts, const std::function<void(uint32_t)> &fn) {
+        Job job{&fn, parts};
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            cur_ = &job;
+            ++gen_;
+        }
+        cv_.notify_all();
+        work(job);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return job.finished.load() == parts && job.users == 0; });
+        cur_ = nullptr;
+    }
+    ~HostPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (std::thread &t : th_) t.join();
+    }
+
+  private:
+    struct Job {
+        const std::function<void(uint32_t)> *fn;
+        uint32_t parts;
+        std::atomic<uint32_t> next{0}, finished{0};
+        uint32_t users = 0;  // guarded by mu_
+    };
+    HostPool() {
+        const unsigned hc = std::thread::hardware_concurrency();
+        const unsigned n = std::min(hc ? hc : 1u, 16u);  // a one-GPU share of the host
+        for (unsigned i = 1; i < n; ++i) th_.emplace_back([this] { loop(); });
+    }
+    static void work(Job &j) {
+        for (uint32_t p; (p = j.next.fetch_add(1)) < j.parts;) {
+            (*j.fn)(p);
+            j.finished.fetch_add(1);
+        }
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            Job *j;
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                cv_.wait(lk, [&] { return stop_ || (cur_ && gen_ != seen); });
+                if (stop_) return;
+                seen = gen_;
+                j = cur_;
+                ++j->users;
+            }
+            work(*j);
+            {
+                std::lock_guard<std::mutex> lk(mu_);
+                --j->users;
+            }
+            done_.notify_all();
+        }
+    }
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    std::vector<std::thread> th_;
+    Job *cur_ = nullptr;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
 // ------------------------------------------------------------------ session memory and counters
 struct PfState {
     std::mutex mu;
@@ -559,41 +646,64 @@ int omega_gpu_pf_moe_plan(uint32_t tokens, uint32_t experts, uint32_t top_k, con
         const int32_t b = (int32_t)__builtin_bit_cast(uint32_t, v);
         return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
     };
-    for (uint32_t e = 0; e < experts; ++e) counts[e] = 0;
-    for (uint32_t t = 0; t < tokens; ++t) {
-        const float *row = logits + (size_t)t * experts;
-        // top_k by (key descending, id ascending): insertion into a sorted list of top_k
-        uint32_t sel[64];
-        int32_t sk[64];
-        uint32_t n = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            if (!std::isfinite(row[e])) {
-                set_error(F_SESSION, "pf moe plan: logit of token %u, expert %u is not finite", t, e);
-                return OMEGA_GPU_BAD_ARGS;
+    // tokens t0 .. t1 - 1: top_k by (key descending, id ascending), insertion into a sorted list
+    // of top_k; returns the first non-finite logit's index (token * experts + expert) or ~0
+    auto rank = [&](uint32_t t0, uint32_t t1) -> uint64_t {
+        for (uint32_t t = t0; t < t1; ++t) {
+            const float *row = logits + (size_t)t * experts;
+            uint32_t sel[64];
+            int32_t sk[64];
+            uint32_t n = 0;
+            for (uint32_t e = 0; e < experts; ++e) {
+                if (!std::isfinite(row[e])) return (uint64_t)t * experts + e;
+                const int32_t k = key(row[e]);
+                if (n == top_k && k <= sk[n - 1]) continue;  // a tie goes to the lower id, already held
+                uint32_t i = n < top_k ? n++ : n - 1;
+                while (i > 0 && sk[i - 1] < k) {
+                    sk[i] = sk[i - 1];
+                    sel[i] = sel[i - 1];
+                    --i;
+                }
+                sk[i] = k;
+                sel[i] = e;
             }
-            const int32_t k = key(row[e]);
-            if (n == top_k && k <= sk[n - 1]) continue;  // a tie goes to the lower id, already held
-            uint32_t i = n < top_k ? n++ : n - 1;
-            while (i > 0 && sk[i - 1] < k) {
-                sk[i] = sk[i - 1];
-                sel[i] = sel[i - 1];
-                --i;
+            const float mx = row[sel[0]];
+            float prob[64], sum = 0.0f;
+            for (uint32_t j = 0; j < top_k; ++j) {
+                prob[j] = std::exp(row[sel[j]] - mx);
+                sum += prob[j];
             }
-            sk[i] = k;
-            sel[i] = e;
+            for (uint32_t j = 0; j < top_k; ++j) {
+                topk_ids[(size_t)t * top_k + j] = sel[j];
+                topk_weights[(size_t)t * top_k + j] = prob[j] / sum;
+            }
         }
-        const float mx = row[sel[0]];
-        float prob[64], sum = 0.0f;
-        for (uint32_t j = 0; j < top_k; ++j) {
-            prob[j] = std::exp(row[sel[j]] - mx);
-            sum += prob[j];
-        }
-        for (uint32_t j = 0; j < top_k; ++j) {
-            topk_ids[(size_t)t * top_k + j] = sel[j];
-            topk_weights[(size_t)t * top_k + j] = prob[j] / sum;
-            ++counts[sel[j]];
-        }
+        return ~0ull;
+    };
+    // long prompts: contiguous token ranges over the host threads (the results do not depend on
+    // the split); the first non-finite logit in row order is the one reported
+    constexpr uint32_t kTokensPerPart = 64;
+    uint64_t bad = ~0ull;
+    HostPool &pool = HostPool::get();
+    if (tokens >= 4 * kTokensPerPart && pool.width() > 1) {
+        const uint32_t parts = std::min(pool.width() * 4, (tokens + kTokensPerPart - 1) / kTokensPerPart);
+        const uint32_t per = (tokens + parts - 1) / parts;
+        std::vector<uint64_t> first(parts, ~0ull);
+        pool.run(parts, [&](uint32_t p) {
+            const uint32_t t0 = std::min(tokens, p * per), t1 = std::min(tokens, t0 + per);
+            first[p] = rank(t0, t1);
+        });
+        for (uint64_t f : first) bad = std::min(bad, f);
+    } else {
+        bad = rank(0, tokens);
     }
+    if (bad != ~0ull) {
+        set_error(F_SESSION, "pf moe plan: logit of token %u, expert %u is not finite", (uint32_t)(bad / experts),
+                  (uint32_t)(bad % experts));
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    for (uint32_t e = 0; e < experts; ++e) counts[e] = 0;
+    for (uint64_t a = 0; a < (uint64_t)tokens * top_k; ++a) ++counts[topk_ids[a]];
     // stable counting sort of the assignments by expert
     std::vector<uint32_t> cursor(experts);
     uint32_t acc = 0;

@@ -81,6 +81,21 @@ def test_routing_plan_refusals(pf):
         pf.moe_plan(bad, 4, 16, 4)
     with pytest.raises(OmegaGpuError):
         pf.moe_plan(np.zeros((4, 16), np.float32), 4, 16, 17)   # top_k > experts
+    # a long prompt is ranked over several host threads: the first bad logit in row order is named
+    bad = np.random.default_rng(5).standard_normal((1500, 128)).astype(np.float32)
+    bad[1400, 9] = np.inf
+    bad[700, 100] = np.nan
+    bad[700, 101] = -np.inf
+    with pytest.raises(OmegaGpuError, match="token 700, expert 100"):
+        pf.moe_plan(bad, 1500, 128, 8)
+    bad[700, 100:102] = 0.0
+    with pytest.raises(OmegaGpuError, match="token 1400, expert 9"):
+        pf.moe_plan(bad, 1500, 128, 8)
+    bad[1400, 9] = 0.0
+    ref = pf.moe_plan(bad, 1500, 128, 8)
+    for _ in range(3):   # the split over threads does not change the result
+        for got, want in zip(pf.moe_plan(bad, 1500, 128, 8), ref):
+            np.testing.assert_array_equal(got, want)
 
 
 def test_host_rmsnorm_matches_the_oracle(pf, oracle):
