@@ -333,8 +333,10 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         if (c * 16 >= active) break;
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i) {
+            // lanes past `active` hold weight 0, so a split past it adds nothing (its o values are
+            // the last split's, finite)
             const uint32_t si = c * 16 + i;
-            const float wi = si < active ? readlane_f32(wj, (int)si) : 0.f;
+            const float wi = readlane_f32(wj, (int)si);
             o0 = fmaf(wi, __uint_as_float((uint32_t)xo[si]), o0);
             o1 = fmaf(wi, __uint_as_float((uint32_t)(xo[si] >> 32)), o1);
         }
