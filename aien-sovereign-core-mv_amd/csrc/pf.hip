@@ -23,6 +23,8 @@
 #include <thread>
 #include <vector>
 
+#include <pthread.h>
+
 #include "device.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
@@ -380,14 +382,17 @@ __global__ __launch_bounds__(256) void k_pf_resid_norm(const PfNormArgs a) {
 // The MoE plan of a long prompt ranks every token on the host (MoeBatchPlan::from_logits). A few
 // threads, started on first use and kept for the process, split such a loop into contiguous
 // ranges; the caller takes a range too. One job at a time (the entry points hold the library
-// lock).
+// lock). The pool is never destroyed (its threads end with the process, nothing joins them at
+// exit), and a child forked from the process has none of its threads: there width() is 1 and
+// the caller runs the loop alone. The fork handlers hold the pool's lock across the fork so the
+// child does not inherit it taken by a worker.
 class HostPool {
   public:
     static HostPool &get() {
-        static HostPool p;
-        return p;
+        static HostPool *p = new HostPool();
+        return *p;
     }
-    uint32_t width() const { return (uint32_t)th_.size() + 1; }
+    uint32_t width() const { return forked_ ? 1u : (uint32_t)th_.size() + 1; }
     // fn(part) for part in 0 .. parts - 1, over the pool and the calling thread. The job lives on
     // this frame: a thread takes it under the lock and counts itself in `users`, and run() returns
     // only when every part has finished and no thread still holds the job.
@@ -404,14 +409,6 @@ class HostPool {
         done_.wait(lk, [&] { return job.finished.load() == parts && job.users == 0; });
         cur_ = nullptr;
     }
-    ~HostPool() {
-        {
-            std::lock_guard<std::mutex> lk(mu_);
-            stop_ = true;
-        }
-        cv_.notify_all();
-        for (std::thread &t : th_) t.join();
-    }
 
   private:
     struct Job {
@@ -423,6 +420,11 @@ class HostPool {
     HostPool() {
         const unsigned hc = std::thread::hardware_concurrency();
         const unsigned n = std::min(hc ? hc : 1u, 16u);  // a one-GPU share of the host
+        pthread_atfork([] { get().mu_.lock(); }, [] { get().mu_.unlock(); },
+                       [] {
+                           get().forked_ = true;
+                           get().mu_.unlock();
+                       });
         for (unsigned i = 1; i < n; ++i) th_.emplace_back([this] { loop(); });
     }
     static void work(Job &j) {
@@ -437,8 +439,7 @@ class HostPool {
             Job *j;
             {
                 std::unique_lock<std::mutex> lk(mu_);
-                cv_.wait(lk, [&] { return stop_ || (cur_ && gen_ != seen); });
-                if (stop_) return;
+                cv_.wait(lk, [&] { return cur_ && gen_ != seen; });
                 seen = gen_;
                 j = cur_;
                 ++j->users;
@@ -456,7 +457,7 @@ class HostPool {
     std::vector<std::thread> th_;
     Job *cur_ = nullptr;
     uint64_t gen_ = 0;
-    bool stop_ = false;
+    bool forked_ = false;
 };
 
 // ------------------------------------------------------------------ session memory and counters

@@ -3,6 +3,7 @@ host mirror of build_tiles (aien-omega-pf/src/lib.rs:122-160), the C router pack
 packed layout (lib.rs:460-478), the routing plan of the driver against the oracle's
 MoeBatchPlan::from_logits, the host RMSNorm against the oracle's, and the struct layouts."""
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -96,6 +97,23 @@ def test_routing_plan_refusals(pf):
     for _ in range(3):   # the split over threads does not change the result
         for got, want in zip(pf.moe_plan(bad, 1500, 128, 8), ref):
             np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.skipif(not hasattr(os, "fork") or os.path.exists("/dev/kfd"),
+                    reason="forks the test process: only where no GPU runtime can be live in it")
+def test_routing_plan_in_a_forked_child(pf):
+    """The plan's host threads do not follow a fork: a child ranks a long prompt alone, with the
+    parent's results."""
+    lg = np.random.default_rng(6).standard_normal((1024, 128)).astype(np.float32)
+    ref = pf.moe_plan(lg, 1024, 128, 8)  # starts the host threads in this process
+    pid = os.fork()
+    if pid == 0:
+        ok = all(np.array_equal(a, b) for a, b in zip(pf.moe_plan(lg, 1024, 128, 8), ref))
+        os._exit(0 if ok else 1)
+    _, status = os.waitpid(pid, 0)
+    assert os.WIFEXITED(status) and os.WEXITSTATUS(status) == 0
+    for a, b in zip(pf.moe_plan(lg, 1024, 128, 8), ref):  # and the parent's threads still serve
+        np.testing.assert_array_equal(a, b)
 
 
 def test_host_rmsnorm_matches_the_oracle(pf, oracle):
