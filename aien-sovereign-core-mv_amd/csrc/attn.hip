@@ -759,11 +759,68 @@ __global__ __launch_bounds__(64) void k_pattn_prep(const PattnArgs a) {
 // pos0 + t0 + j + 1 (a token can see none of a chunk's pages: its state stays empty, m -inf and
 // l 0, and the combine gives it no weight). Item words: t0, c, the group's first partial slot
 // base and its chunk count nch; token j's partial of chunk c is slot base * TQ + j * nch + c, so
-// each token's partials are contiguous for the combine. The work per (page, token) is the same
-// either way (the matrix-core products and the softmax), so tiles pay only where the prefix is
-// long enough for the saved page reads to matter: TQ 4 for contexts of 1024 and more, else 1
-// (which keeps a wavefront per token for the parallelism of short prompts).
+// each token's partials are contiguous for the combine. A tile of TQ > 1 runs its tokens in pairs
+// that share every matrix-core product (pattn_page2: the 16 columns are 2 tokens x 8 heads, so
+// the softmax work per (page, token) halves against TQ = 1, whose 16 columns are one token's 8
+// heads in hi and lo halves), and each page is loaded once for all TQ tokens: TQ 4 for contexts
+// of 1024 and more, 2 from 256, else 1 (a wavefront per token for the parallelism of short
+// prompts).
 constexpr uint32_t kPattnTqLong = 4, kPattnLongCtx = 1024;
+constexpr uint32_t kPattnMidCtx = 256;  // from here one pair of tokens per wavefront
+
+// One page for a pair of query tokens (TQ > 1): the 16 B-columns of S^T = K q^T are the 16
+// queries (token 2 p + n / 8, head n % 8) of the pair, the q operand's hi and lo halves in two
+// product chains into one accumulator, so every lane's four scores are distinct (token, query)
+// entries and the softmax runs once per query; the 16 A-rows of O = P V are the same 16 queries,
+// the probability's hi and lo halves again in two chains. Lane (g, n) holds query n's state (m, l)
+// and rows 4 g + i of O (query 4 g + i, dim 16 nb + n); a query that sees none of the page keeps
+// an empty state (a maximum of -inf is replaced by 0 as the exponent's reference).
+__device__ __forceinline__ void pattn_page2(const DattnPage &T, const bf16x8 (&qh)[4], const bf16x8 (&ql)[4],
+                                            uint32_t tok0, uint32_t ctx_n, uint32_t g, uint32_t n, float &m_l,
+                                            float &l_l, f32x4 (&O)[8]) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), qh[ks], acc, 0, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), ql[ks], acc, 0, 0, 0);
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = tok0 + 4 * g + i < ctx_n ? acc[i] * kInvSqrt128 : -INFINITY;
+    const float mx = xor_max<32>(xor_max<16>(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))));
+    const float m_new = fmaxf(m_l, mx);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pr[i] = expf(sc[i] - m_ref);
+        psum += pr[i];
+    }
+    psum = xor_sum<32>(xor_sum<16>(psum));
+    const float alpha = expf(m_l - m_ref);
+    l_l = l_l * alpha + psum;
+    m_l = m_new;
+    // row 4 g + i is query 4 g + i, whose state lane 4 g + i (lane group 0) holds
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float ai = __shfl(alpha, (int)(4 * g + i));
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
+    }
+    s16x4 ph, pl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        ph[i] = (short)bf16_split_hi(pr[i]);
+        pl[i] = (short)bf16_split_lo(pr[i]);
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, __builtin_bit_cast(s16x4, T.v[nb]), O[nb], 0, 0, 0);
+        O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, __builtin_bit_cast(s16x4, T.v[nb]), O[nb], 0, 0, 0);
+    }
+}
 
 template <uint32_t TQ>
 __global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
@@ -775,45 +832,110 @@ __global__ __launch_bounds__(64) void k_pattn(const PattnArgs a) {
     const uint32_t valid = a.m - t0 < TQ ? a.m - t0 : TQ;  // tokens of this group
     const uint32_t pages = (a.pos0 + t0 + valid + 15) / 16;
     const uint32_t p_begin = c * kPattnChunk, p_end = min(pages, p_begin + kPattnChunk), last = p_end - 1;
-    bf16x8 qop[TQ][4];
     uint32_t ctx[TQ];
 #pragma unroll
-    for (uint32_t j = 0; j < TQ; ++j) {
-        const uint32_t tj = j < valid ? t0 + j : t0;  // a missing token repeats the first (never stored)
-        paged_q(a.qn + ((size_t)tj * 32 + h * 8) * 128, lane, qhl[j], qop[j]);
-        ctx[j] = j < valid ? a.pos0 + t0 + j + 1 : 0u;
-    }
+    for (uint32_t j = 0; j < TQ; ++j) ctx[j] = j < valid ? a.pos0 + t0 + j + 1 : 0u;
     DattnArgs d;
     d.pool = a.pool;
     d.g = a.g;
     d.layer = a.layer;
     DattnPage A, B;
-    dattn_load(d, h, p_begin, lane, A);
-    dattn_load(d, h, min(p_begin + 1, last), lane, B);
-    float m_l[TQ], l_l[TQ];
-    f32x4 O[TQ][8];
+    if constexpr (TQ == 1) {
+        bf16x8 qop[4];
+        paged_q(a.qn + ((size_t)t0 * 32 + h * 8) * 128, lane, qhl[0], qop);
+        dattn_load(d, h, p_begin, lane, A);
+        dattn_load(d, h, min(p_begin + 1, last), lane, B);
+        float m_l = -INFINITY, l_l = 0.f;
+        f32x4 O[8];
 #pragma unroll
-    for (uint32_t j = 0; j < TQ; ++j) {
-        m_l[j] = -INFINITY;
-        l_l[j] = 0.f;
+        for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t p = p_begin; p < p_end; p += 2) {
+            const bool has_b = p + 1 < p_end;  // else B is the null page (every score -inf)
+            dattn_page<false, true>(A, qop, p * 16, ctx[0], g, n, m_l, l_l, O);
+            dattn_load(d, h, min(p + 2, last), lane, A);
+            dattn_page<false, true>(B, qop, (p + 1) * 16, has_b ? ctx[0] : 0u, g, n, m_l, l_l, O);
+            dattn_load(d, h, min(p + 3, last), lane, B);
+        }
+        paged_store(a.part + (((size_t)base * TQ + c) * 32 + h * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
+    } else {
+        // pairs of tokens share every product (pattn_page2); the 8 q heads of each token are
+        // staged as bf16 hi / lo halves (a missing token repeats the first, never stored)
+        static_assert(TQ % 2 == 0, "query tiles of whole pairs");
+        constexpr uint32_t NP = TQ / 2;
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) O[j][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t j = 0; j < TQ; ++j) {
+            const float *q = a.qn + ((size_t)(j < valid ? t0 + j : t0) * 32 + h * 8) * 128;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const float q0 = *as_global_f32(q + r * 128 + lane), q1 = *as_global_f32(q + r * 128 + 64 + lane);
+                qhl[j][0][r][lane] = bf16_split_hi(q0);
+                qhl[j][1][r][lane] = bf16_split_lo(q0);
+                qhl[j][0][r][lane + 64] = bf16_split_hi(q1);
+                qhl[j][1][r][lane + 64] = bf16_split_lo(q1);
+            }
+        }
+        dattn_load(d, h, p_begin, lane, A);
+        dattn_load(d, h, min(p_begin + 1, last), lane, B);
+        __syncthreads();
+        // B operands: column n of pair p is query (token 2 p + n / 8, head n % 8); k-step ks of
+        // lane group g covers dims 32 ks + 8 g .. +8
+        bf16x8 qh[NP][4], ql[NP][4];
+        uint32_t cn[NP];
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const uint32_t j = 2 * p + (n >> 3);
+            cn[p] = ctx[0];
+#pragma unroll
+            for (uint32_t jj = 1; jj < TQ; ++jj)
+                if (jj == j) cn[p] = ctx[jj];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qh[p][ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[j][0][n & 7][32 * ks + 8 * g]));
+                ql[p][ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[j][1][n & 7][32 * ks + 8 * g]));
+            }
+        }
+        float m_l[NP], l_l[NP];
+        f32x4 O[NP][8];
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            m_l[p] = -INFINITY;
+            l_l[p] = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) O[p][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (uint32_t pg = p_begin; pg < p_end; pg += 2) {
+            const bool has_b = pg + 1 < p_end;  // else B is the null page (every score -inf)
+#pragma unroll
+            for (uint32_t p = 0; p < NP; ++p) pattn_page2(A, qh[p], ql[p], pg * 16, cn[p], g, n, m_l[p], l_l[p], O[p]);
+            dattn_load(d, h, min(pg + 2, last), lane, A);
+#pragma unroll
+            for (uint32_t p = 0; p < NP; ++p)
+                pattn_page2(B, qh[p], ql[p], (pg + 1) * 16, has_b ? cn[p] : 0u, g, n, m_l[p], l_l[p], O[p]);
+            dattn_load(d, h, min(pg + 3, last), lane, B);
+        }
+        // partials: row 4 g + i of pair p is query 4 g + i (token 2 p + g / 2, head 4 (g % 2) + i);
+        // lanes 0..15 hold query n's (m, l). Token j's partial of chunk c is slot base * TQ + j *
+        // nch + c, its head r at r * kPartStride (m, l, -, -, o[128]).
+#pragma unroll
+        for (uint32_t p = 0; p < NP; ++p) {
+            const uint32_t jo = 2 * p + (g >> 1);
+            if (jo < valid) {
+                float *pt = a.part + (((size_t)base * TQ + jo * nch + c) * 32 + h * 8) * kPartStride;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float *pp = pt + (size_t)(4 * (g & 1) + i) * kPartStride + 4;
+#pragma unroll
+                    for (int nb = 0; nb < 8; ++nb) pp[16 * nb + n] = O[p][nb][i];
+                }
+            }
+            const uint32_t jm = 2 * p + (n >> 3);
+            if (lane < 16 && jm < valid) {
+                float *pp = a.part + (((size_t)base * TQ + jm * nch + c) * 32 + h * 8 + (n & 7)) * kPartStride;
+                pp[0] = m_l[p];
+                pp[1] = l_l[p];
+            }
+        }
     }
-    for (uint32_t p = p_begin; p < p_end; p += 2) {
-        const bool has_b = p + 1 < p_end;  // else B is the null page (every score -inf)
-#pragma unroll
-        for (uint32_t j = 0; j < TQ; ++j) dattn_page<false, true>(A, qop[j], p * 16, ctx[j], g, n, m_l[j], l_l[j], O[j]);
-        dattn_load(d, h, min(p + 2, last), lane, A);
-#pragma unroll
-        for (uint32_t j = 0; j < TQ; ++j)
-            dattn_page<false, true>(B, qop[j], (p + 1) * 16, has_b ? ctx[j] : 0u, g, n, m_l[j], l_l[j], O[j]);
-        dattn_load(d, h, min(p + 3, last), lane, B);
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < TQ; ++j)
-        if (j < valid)
-            paged_store(a.part + (((size_t)base * TQ + j * nch + c) * 32 + h * 8) * kPartStride, kPartStride, lane,
-                        m_l[j], l_l[j], O[j]);
 }
 
 // ---------------------------------------------------------------- KV park / restore (extension)
@@ -1818,7 +1940,8 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
         // groups of tq tokens share their page loads; each group's chunks follow its last token's
         // context, and token j of a group owns the partial slots base * tq + j * nch + chunk (kSub
         // is a multiple of tq, so a group never spans sub-batches)
-        const uint32_t tq = pos0 + t0 + mm >= kPattnLongCtx ? kPattnTqLong : 1;
+        const uint32_t ctx_end = pos0 + t0 + mm;
+        const uint32_t tq = ctx_end >= kPattnLongCtx ? kPattnTqLong : ctx_end >= kPattnMidCtx ? 2u : 1u;
         uint32_t base = 0;
         for (uint32_t g0 = 0; g0 < mm; g0 += tq) {
             const uint32_t valid = std::min(tq, mm - g0);
@@ -1845,6 +1968,8 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
         OMEGA_HIP(F_DATTN, hipGetLastError());
         if (tq == 1)
             OMEGA_LAUNCH(k_pattn<1>, dim3(4 * n), dim3(64), 0, cx->stream, a);
+        else if (tq == 2)
+            OMEGA_LAUNCH(k_pattn<2>, dim3(4 * n), dim3(64), 0, cx->stream, a);
         else
             OMEGA_LAUNCH(k_pattn<kPattnTqLong>, dim3(4 * n), dim3(64), 0, cx->stream, a);
         OMEGA_HIP(F_DATTN, hipGetLastError());
