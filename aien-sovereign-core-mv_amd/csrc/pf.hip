@@ -242,8 +242,10 @@ __global__ __launch_bounds__(256) void k_pf_qgemm(const PfGemmArgs a) {
 // wavefront of 64 experts one contiguous KiB per group of 4 columns; the R rows of x are staged
 // through LDS in passes of kPfRouterKc columns and read as broadcasts, and the weight groups are
 // loaded kPfRouterNg at a time in two register sets so the next set is in flight while one is
-// summed. Rows come in tiles of kPfRouterRows (the buffers hold whole tiles).
-constexpr uint32_t kPfRouterRows = 4;
+// summed. Rows come in tiles of kPfRouterRows (the buffers hold whole tiles): 16, the reference
+// engine's rows per CTA that the reference's own tests expect of router_rows()
+// (aien-omega-pf/src/lib.rs:1300); a launch takes 4, 2 or 1 rows per lane of such tiles.
+constexpr uint32_t kPfRouterRows = 16;
 constexpr uint32_t kPfRouterKc = 1024;
 constexpr uint32_t kPfRouterNg = 4;
 

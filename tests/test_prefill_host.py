@@ -34,6 +34,12 @@ def test_tile_builder_matches_the_host_mirror(pf):
     assert n == 0
 
 
+def test_router_tile_is_the_reference_engines(pf):
+    # the reference's own test of the linked library expects 16 rows per router tile
+    # (aien-omega-pf/src/lib.rs:1300); buffers hold whole tiles
+    assert pf.router_rows() == 16
+
+
 def test_router_pack_layout(pf):
     rng = np.random.default_rng(2)
     e, k = 6, 16
