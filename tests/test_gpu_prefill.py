@@ -101,9 +101,10 @@ def dequant_weights(oracle, w, s):
     return t[w].astype(np.float64) * sc
 
 
-def test_qgemm_plain_dense(omega, oracle, pf):
+@pytest.mark.parametrize("n", [384, 512])
+def test_qgemm_plain_dense(omega, oracle, pf, n):
     rng = np.random.default_rng(4)
-    n, k, m = 384, 1024, 70
+    k, m = 1024, 70
     w, s = oracle.synth_fp8(11, 1, 1, n, k)
     T = omega.Fp8Tensor.upload(1, n, k, w, s)
     bm = pf.qgemm_bm()
