@@ -1334,6 +1334,36 @@ hipError_t launch_attn_combine(const CombineArgs &a, hipStream_t st) {
 // the items' (m, l) are read by thread j % 256 of item j, their weights exp(m - M) staged in LDS;
 // thread t then sums dims 4 (t % 32) .. +3 over the items j = t / 32 (mod 8) and the 8 groups
 // meet in LDS in a fixed order; 16 lanes split the head's row.
+// The f32 rows of sequences (prefill tokens) that have at most 64 partials each: one wavefront per
+// (sequence, q head), lane j holding partial j's (m, l), lane l dims l and l + 64; the partials
+// merge in item order (out = sum w_j o_j / sum w_j l_j with w_j = exp(m_j - max m), times
+// out_scale). A token always has a partial that sees its own position, so the maximum is finite.
+__global__ __launch_bounds__(256) void k_attn_combine_rows(const CombineItemsArgs a, uint32_t seqs) {
+    const uint32_t lane = lane_id(), wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wv >= seqs * 32) return;  // uniform per wavefront
+    const uint32_t s = wv >> 5, head = wv & 31;
+    const uint32_t off = a.item_off[s], n = a.item_off[s + 1] - off;  // 1 ..= 64
+    constexpr size_t kItem = 32 * (size_t)kPartStride;                // floats from one item to the next
+    const float *base = a.part + ((size_t)off * 32 + head) * kPartStride;
+    const u32x2 ml = *as_global_u32x2(base + min(lane, n - 1) * kItem);
+    const float mj = lane < n ? __uint_as_float(ml.x) : -INFINITY;
+    float M = row16_max(mj);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    const float wj = lane < n ? expf(mj - M) : 0.f;
+    const float L = wave_sum(wj * (lane < n ? __uint_as_float(ml.y) : 0.f));
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll 4
+    for (uint32_t i = 0; i < n; ++i) {
+        const float wi = readlane_f32(wj, (int)i);
+        const float *p = base + i * kItem + 4;
+        o0 = fmaf(wi, *as_global_f32(p + lane), o0);
+        o1 = fmaf(wi, *as_global_f32(p + 64 + lane), o1);
+    }
+    float *out = a.out + ((size_t)s * 32 + head) * 128;
+    out[lane] = o0 / L * a.out_scale;
+    out[64 + lane] = o1 / L * a.out_scale;
+}
+
 __global__ __launch_bounds__(256) void k_attn_combine_items(const CombineItemsArgs a) {
     constexpr uint32_t kRounds = (kCombineMaxItems + 255) / 256;
     __shared__ float wsh[kRounds * 256];
@@ -1978,7 +2008,12 @@ static int prefill_attn_run(OmegaGpuDecodeAttnCache *c, uint32_t layer, uint32_t
         cb.item_off = doff;
         cb.out = out_dev + (size_t)t0 * 4096;
         cb.out_scale = out_scale;
-        OMEGA_HIP(F_DATTN, launch_attn_combine_items(cb, mm, cx->stream));
+        if (widest <= 64) {  // a wavefront per (token, q head)
+            OMEGA_LAUNCH(k_attn_combine_rows, dim3((mm * 32 + 3) / 4), dim3(256), 0, cx->stream, cb, mm);
+            OMEGA_HIP(F_DATTN, hipGetLastError());
+        } else {
+            OMEGA_HIP(F_DATTN, launch_attn_combine_items(cb, mm, cx->stream));
+        }
         // the host plan is read by the copies above before the next sub-batch rewrites it
         OMEGA_HIP(F_DATTN, hipStreamSynchronize(cx->stream));
     }
