@@ -1352,7 +1352,6 @@ __global__ __launch_bounds__(256) void k_attn_combine_rows(const CombineItemsArg
     const float wj = lane < n ? expf(mj - M) : 0.f;
     const float L = wave_sum(wj * (lane < n ? __uint_as_float(ml.y) : 0.f));
     float o0 = 0.f, o1 = 0.f;
-#pragma unroll 4
     for (uint32_t i = 0; i < n; ++i) {
         const float wi = readlane_f32(wj, (int)i);
         const float *p = base + i * kItem + 4;
