@@ -113,16 +113,18 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     if (blockIdx.x == 0 && wid == 0 && lane < (uint32_t)kTopK) {
         const uint32_t id = sh_id[lane];
         const float wt = sh_w[lane];
-        const uint64_t gu0 = a.dir_gu[2 * id], gu1 = a.dir_gu[2 * id + 1];
-        const uint64_t dn0 = a.dir_dn[2 * id], dn1 = a.dir_dn[2 * id + 1];
         a.ids[lane] = id;
         a.weights[lane] = wt;
         if (a.log_ids) a.log_ids[lane] = id;
         if (a.log_w) a.log_w[lane] = wt;
-        a.tab_gu[2 * lane] = gu0;
-        a.tab_gu[2 * lane + 1] = gu1;
-        a.tab_dn[2 * lane] = dn0;
-        a.tab_dn[2 * lane + 1] = dn1;
+        if (a.tab_gu) {  // the group tables (the MoE block's one-token form has none)
+            const uint64_t gu0 = a.dir_gu[2 * id], gu1 = a.dir_gu[2 * id + 1];
+            const uint64_t dn0 = a.dir_dn[2 * id], dn1 = a.dir_dn[2 * id + 1];
+            a.tab_gu[2 * lane] = gu0;
+            a.tab_gu[2 * lane + 1] = gu1;
+            a.tab_dn[2 * lane] = dn0;
+            a.tab_dn[2 * lane + 1] = dn1;
+        }
     }
     float ag[kGuPairs], au[kGuPairs];
 #pragma unroll
@@ -146,7 +148,8 @@ struct DownArgs {
     const uint32_t *ids = nullptr;
     const float *weights = nullptr;
     const float *act = nullptr;  // [8][768]
-    float *x = nullptr;          // residual [2048]
+    const float *xin = nullptr;  // residual read [2048] (null: the combine alone is written)
+    float *x = nullptr;          // out [2048]: xin + the combine (the decode step: xin == x)
     int graph_mutant = 0;        // 2: slot 7 dropped from the combine
 };
 
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
     float xr[P][16];
     S::load_x(a.act + slot * kInter, lane, xr);
     const float wraw = *as_global_f32(a.weights + (lane & (kTopK - 1)));  // lane s: slot s's weight
-    const float xres = *as_global_f32(a.x + row0 + (lane & (kDnRows - 1)));
+    const float xres = a.xin ? *as_global_f32(a.xin + row0 + (lane & (kDnRows - 1))) : 0.f;
     float sc[P];
     S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f, 0, sc);
     S slab;
@@ -190,6 +193,37 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
         }
         a.x[row0 + threadIdx.x] = xres + moe;
     }
+}
+
+// The MoE block of one token as the decode step runs it: router logits and x' (ra), then gate|up
+// with the top-8 ranking in its prologue and SwiGLU, then down with the slot-order combine into
+// out (plus resid when given). ra.ids / ra.weights receive the route; act holds [8][768].
+hipError_t launch_moe_one_token(const RouterArgs &ra, const uint8_t *gu_w, const float *gu_s,
+                                const uint8_t *dn_w, const float *dn_s, float *act, const float *resid,
+                                float *out, hipStream_t st) {
+    hipError_t e = launch_router_logits(ra, st);
+    if (e != hipSuccess) return e;
+    GateUpArgs gu;
+    gu.w = gu_w;
+    gu.s = gu_s;
+    gu.logits = ra.logits;
+    gu.norm_topk = ra.norm_topk;
+    gu.route_mutant = ra.mutant;
+    gu.xn = ra.xout;
+    gu.act = act;
+    gu.ids = ra.ids;
+    gu.weights = ra.weights;
+    OMEGA_LAUNCH(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
+    DownArgs dn;
+    dn.w = dn_w;
+    dn.s = dn_s;
+    dn.ids = ra.ids;
+    dn.weights = ra.weights;
+    dn.act = act;
+    dn.xin = resid;
+    dn.x = out;
+    OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
+    return hipGetLastError();
 }
 
 }  // namespace omega
@@ -375,6 +409,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         dn.ids = ra.ids;
         dn.weights = ra.weights;
         dn.act = g->act;
+        dn.xin = g->x;
         dn.x = g->x;
         dn.graph_mutant = g->mutant;
         arm();

@@ -106,6 +106,11 @@ struct RouterArgs {
 // logits (and x'); then the ranking of the logits (ids, weights, group tables)
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st);
 hipError_t launch_router_topk(const RouterArgs &a, hipStream_t st);
+// one token's MoE block through the decode step's kernels (router logits, gate|up with the
+// ranking in its prologue, down with the combine): three launches
+hipError_t launch_moe_one_token(const RouterArgs &ra, const uint8_t *gu_w, const float *gu_s,
+                                const uint8_t *dn_w, const float *dn_s, float *act, const float *resid,
+                                float *out, hipStream_t st);
 
 // ---------------------------------------------------------------- attention
 constexpr uint32_t kAttnTile = 64;       // tokens per tile of the paged kernel (one wavefront)

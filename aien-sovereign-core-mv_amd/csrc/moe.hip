@@ -736,6 +736,25 @@ MoeArgs moe_args(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tenso
     return a;
 }
 
+// One token runs the decode step's three launches (router logits, gate|up with the ranking in its
+// prologue, down with the slot-order combine) instead of the batched form's six: no grouping is
+// needed for 8 rows of 8 distinct experts. The mutant knobs keep the batched form.
+bool moe_one_token(uint32_t tokens) { return tokens == 1 && knobs().moe_mutant == 0; }
+
+hipError_t launch_moe_one(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tensor *gu,
+                          const OmegaGpuFp8Tensor *dn, const MoeArgs &a, float eps, int norm_topk,
+                          hipStream_t st) {
+    RouterArgs ra = router_args(r, layer, a.h, eps, norm_topk, 1.0f);
+    ra.logits = a.logits;
+    ra.xout = a.xn;
+    ra.ids = a.ids;
+    ra.weights = a.weights;
+    ra.tab_gu = ra.tab_dn = nullptr;
+    ra.route_log = nullptr;
+    ra.route_log_w = nullptr;
+    return launch_moe_one_token(ra, gu->w, gu->s, dn->w, dn->s, a.gp, a.resid, a.out, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -764,7 +783,8 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
     a.ids = ids_dev;
     a.weights = weights_dev;
     a.out = out_dev;
-    OMEGA_HIP(F_GEMM, launch_moe_batch(a, c->stream));
+    if (moe_one_token(tokens)) OMEGA_HIP(F_GEMM, launch_moe_one(router, layer, gate_up, down, a, eps, norm_topk, c->stream));
+    else OMEGA_HIP(F_GEMM, launch_moe_batch(a, c->stream));
     return OMEGA_GPU_OK;
 }
 
@@ -800,13 +820,16 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     a.weights = reinterpret_cast<float *>(d + o_w);
     memcpy(pin, h, hb);
     OMEGA_HIP(F_GEMM, hipMemcpyAsync(d + o_h, pin, hb, hipMemcpyHostToDevice, c->stream));
-    OMEGA_HIP(F_GEMM, launch_moe_batch(a, c->stream));
+    const bool one = moe_one_token(tokens);
+    if (one) OMEGA_HIP(F_GEMM, launch_moe_one(router, layer, gate_up, down, a, eps, norm_topk, c->stream));
+    else OMEGA_HIP(F_GEMM, launch_moe_batch(a, c->stream));
     OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin, d + o_out, hb, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin + hb, d + o_ids, 2 * ib, hipMemcpyDeviceToHost, c->stream));
-    OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin + hb + 2 * ib, a.plan + 1, 4, hipMemcpyDeviceToHost, c->stream));
+    // the planner's timed-out flag (the one-token form has no planner)
+    if (!one) OMEGA_HIP(F_GEMM, hipMemcpyAsync(pin + hb + 2 * ib, a.plan + 1, 4, hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_GEMM, hipStreamSynchronize(c->stream));
     uint32_t late = 0;
-    memcpy(&late, pin + hb + 2 * ib, 4);
+    if (!one) memcpy(&late, pin + hb + 2 * ib, 4);
     if (late) {
         set_error(F_GEMM, "moe batch: the plan timed out waiting for the token rankings");
         return OMEGA_GPU_CHIP_FAIL;

@@ -623,7 +623,9 @@ def bench_moe(om, args):
         line = {"workload": "moe_block", "tokens": T, "us_per_block": round(us, 2),
                 "distinct_experts": d, "algorithmic_bytes": int(b), "GBs": round(b / (us * 1e3), 1),
                 "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times),
-                "launches": 6, "expert_path": "grouped GEMV" if T < 16 else "FP8 MFMA"}
+                "launches": 3 if T == 1 else 6,
+                "expert_path": ("decode-step GEMVs (router logits, gate|up with the ranking, down with the combine)"
+                                if T == 1 else "grouped GEMV" if T < 16 else "FP8 MFMA")}
         print(json.dumps(line), flush=True)
         lines.append(line)
         for buf in hs + [od, idd, wd]:

@@ -7,7 +7,9 @@ Bars: expert ids bit-exact, weights within 1e-6 relative, moe_out within 2e-3 re
 (max abs error over max abs value, per token). From 16 tokens on the GEMMs run on the FP8 matrix
 cores with the activations split into four e4m3 terms; the one-term mutant (a plain fp8 cast of
 the activations) must fail the 2e-3 bar, which shows the bar resolves the split's precision.
-Below 16 tokens the projections are grouped GEMVs on the f32 rows, held to 1e-4.
+Below 16 tokens the projections are grouped GEMVs on the f32 rows, held to 1e-4; one token runs
+the decode step's own three launches (router logits, gate|up with the top-8 ranking in its
+prologue, down with the slot-order combine), also GEMVs on the f32 rows under the same bar.
 """
 import numpy as np
 import pytest
@@ -90,8 +92,8 @@ def test_crowded_experts_use_several_row_tiles(omega, oracle, model):
     assert max(rel_err(out[t], want[t]) for t in range(64)) <= TOL
 
 
-def test_device_entry_adds_the_residual(omega, oracle, model):
-    T = 32
+@pytest.mark.parametrize("T", [1, 32])
+def test_device_entry_adds_the_residual(omega, oracle, model, T):
     h = bf16_rows(oracle, np.random.default_rng(9), T)
     out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
     lib = omega.lib()
@@ -107,6 +109,13 @@ def test_device_entry_adds_the_residual(omega, oracle, model):
     np.testing.assert_array_equal(idd.download(np.uint32, T * 8).reshape(T, 8), ids)
     # the same moe rows, then one f32 add of the residual
     np.testing.assert_array_equal(got, (h + out).astype(np.float32))
+    # without the residual the device entry writes the moe rows alone
+    rc = lib.omega_gpu_moe_batch_dev(model["router"].as_raw(), 0, model["gu"].as_raw(),
+                                     model["dn"].as_raw(), T, hd.ptr, 1e-6, 1, None, idd.ptr,
+                                     wd.ptr, od.ptr)
+    assert rc == 0
+    np.testing.assert_array_equal(od.download(np.float32, T * H).reshape(T, H), out)
+    np.testing.assert_array_equal(wd.download(np.float32, T * 8).reshape(T, 8), w)
 
 
 @pytest.mark.parametrize("T,mutant", [(32, 1), (32, 2), (32, 5), (32, 6), (32, 7),
