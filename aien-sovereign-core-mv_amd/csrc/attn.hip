@@ -20,14 +20,19 @@
 // about 2^-16 relative error per operand instead of bf16's 2^-8. The cache stores each page's V
 // plane transposed ([head][dim][16 tokens]) so that a lane's 4 tokens of one dim are 8
 // contiguous bytes. The 8 heads' RMSNorm scales come from one transposed f64 reduction. Split 0
-// appends this token's K/V and folds it in as one more online-softmax step. A second small
-// launch combines the splits (k_attn_combine); nothing is exchanged between workgroups inside a
-// launch.
+// appends this token's K/V and folds it in as one more online-softmax step. The splits are
+// merged in the same launch: each split stores its partial with agent-scope stores and, once
+// they are acknowledged, sets its flag to the launch's epoch; splits 0..7 of every kv head then
+// wait (a bounded number of polls; a wait that runs out is counted in errc and reported by the
+// entry point) for all of the head's flags and merge one q head each. Every split workgroup is
+// resident at once (at most 4 x 64 one-wavefront workgroups). The building blocks live in
+// dattn.hpp, shared with the persistent token kernel.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <vector>
 
+#include "dattn.hpp"
 #include "device.hpp"
 #include "kernels.hpp"
 #include "mfma.hpp"
@@ -35,95 +40,10 @@
 
 namespace omega {
 
-constexpr float kInvSqrt128 = 0.08838834764831845f;
-constexpr uint32_t kVtHead = 4096;  // bytes per kv head of a transposed V plane (128 dims x 32 B)
-
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));  // a 16x16x16 bf16 operand
-
-// one 16-token page: lane (g = lane / 16, n = lane % 16) holds token n's K dims 32 ks + 8 g .. +8
-// for k-step ks (the four lane groups of a k-step read 64 contiguous bytes of each K row), and
-// V^T[dim 16 nb + n][tokens 4 g .. +4] for n-block nb
-struct DattnPage {
-    u32x4 k[4];
-    u32x2 v[8];
-};
-
-__device__ __forceinline__ void dattn_load(const DattnArgs &a, uint32_t h, uint32_t page, uint32_t lane,
-                                           DattnPage &T) {
-    const uint32_t g = lane >> 4, n = lane & 15;
-    const uint8_t *pg = a.pool + (uint64_t)a.layer * a.g.layer_stride + (uint64_t)page * a.g.block_stride;
-    const gu32x4 *kp = as_global(pg + (uint64_t)n * a.g.token_stride + (uint64_t)h * a.g.head_stride + 16 * g);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) T.k[ks] = __builtin_nontemporal_load(kp + 4 * ks);
-    const uint8_t *vp = pg + a.g.plane_stride + (uint64_t)h * kVtHead + n * 32 + 8 * g;
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) T.v[nb] = __builtin_nontemporal_load(as_global_u32x2(vp + nb * 16 * 32));
-}
-
-
-// One online-softmax step over a page whose first token is tok0 (< pos). The online state of
-// head n % 8 (m, l) sits in every lane of column n; O[nb][i] is row 4 g + i (head (4 g + i) % 8,
-// hi half for g < 2, lo half otherwise), dim 16 nb + n.
-// GUARD: the page may hold no valid token for a running state that has seen none either (the
-// prefill's query tiles), so a maximum of -inf is replaced by 0 as the exponent's reference.
-template <bool FIRST, bool GUARD = false>  // FIRST: no earlier page (the running state starts here)
-__device__ __forceinline__ void dattn_page(const DattnPage &T, const bf16x8 (&qop)[4], uint32_t tok0,
-                                           uint32_t pos, uint32_t g, uint32_t n, float &m_l, float &l_l,
-                                           f32x4 (&O)[8]) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), qop[ks], acc, 0, 0, 0);
-    float sc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float full = acc[i] + dpp_f32<DPP_ROR8>(acc[i]);  // hi + lo columns
-        sc[i] = tok0 + 4 * g + i < pos ? full * kInvSqrt128 : -INFINITY;
-    }
-    // max and sum over the four lane groups (rows) of a column: row swaps, no LDS
-    const float mx = xor_max<32>(xor_max<16>(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))));
-    const float m_new = FIRST ? mx : fmaxf(m_l, mx);  // finite unless GUARD: token tok0 is valid
-    const float m_ref = GUARD && m_new == -INFINITY ? 0.f : m_new;
-    float pr[4];
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        pr[i] = expf(sc[i] - m_ref);
-        psum += pr[i];
-    }
-    psum = xor_sum<32>(xor_sum<16>(psum));
-    if (FIRST) {
-        l_l = psum;
-    } else {
-        const float alpha = expf(m_l - m_ref);
-        l_l = l_l * alpha + psum;
-        // accumulator row 4 g + i belongs to head (4 g + i) % 8: head i for even g, 4 + i for
-        // odd g, whose alpha every row's lane (head) holds
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float a_lo = readlane_f32(alpha, i), a_hi = readlane_f32(alpha, 4 + i);
-            const float ai = (g & 1) ? a_hi : a_lo;
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb) O[nb][i] *= ai;
-        }
-    }
-    m_l = m_new;
-    // A operand of O = P V: row n = head n % 8 (hi or lo half), k = tokens 4 g .. +4
-    s16x4 pop;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pop[i] = (short)(n < 8 ? bf16_split_hi(pr[i]) : bf16_split_lo(pr[i]));
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-        O[nb] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pop, __builtin_bit_cast(s16x4, T.v[nb]), O[nb], 0, 0, 0);
-}
 
 __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
-    __shared__ __align__(16) uint16_t qhl[2][8][128];  // the prepared q heads: bf16 hi, lo halves
-    __shared__ float vs[128];        // split 0: this token's V as stored (bf16 values)
-    __shared__ float sp_sh[8];       // split 0: this token's score per head
+    __shared__ __align__(16) DattnLds lds;
     const uint32_t lane = threadIdx.x, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
-    const uint32_t g = lane >> 4, n = lane & 15;
     // Every load below is issued unconditionally, the page stream last: vector-memory waits
     // complete in issue order and merge conservatively at branch joins, so a conditional load
     // here would make the preparation math wait on the page stream. The q|k|v row and the norm
@@ -137,8 +57,8 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         q1[r] = *as_global_f32(qraw + r * 128 + 64 + lane);
     }
     const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
-    float k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
-    float k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
+    const float k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
+    const float k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
     const float v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
     const float v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
     const float kw0 = *as_global_f32(a.k_norm + lane);
@@ -158,135 +78,13 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     DattnPage T;
     dattn_load(a, h, p_begin < p_end ? p_begin : 0, lane, T);
     __builtin_amdgcn_sched_barrier(0);  // all of the above is issued before any arithmetic
-
-    // the 8 heads' f64 sums of squares in one reduction; lane l then holds head l / 8's scale
-    const bool rope = a.mutant != 1;
-    double ss[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) ss[r] = (double)q0[r] * (double)q0[r] + (double)q1[r] * (double)q1[r];
-    const float scale_l = rms_scale(head_sums8(ss, lane), 128, a.eps);
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        head_scale_rope(q0[r], q1[r], readlane_f32(scale_l, 8 * r), qw0, qw1, rc, rs, rope);
-        qhl[0][r][lane] = bf16_split_hi(q0[r]);
-        qhl[1][r][lane] = bf16_split_lo(q0[r]);
-        qhl[0][r][lane + 64] = bf16_split_hi(q1[r]);
-        qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
-    }
-    if (s == 0) {
-        const float kscale = rms_scale(wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1), 128, a.eps);
-        head_scale_rope(k0, k1, kscale, kw0, kw1, rc, rs, rope);
-        const uint16_t kb0 = bf16_rne(k0), kb1 = bf16_rne(k1);
-        const uint16_t vb0 = bf16_rne(v0), vb1 = bf16_rne(v1);
-        if (a.mutant != 3) {
-            uint16_t *krow = reinterpret_cast<uint16_t *>(
-                a.pool + kv_row_offset(a.g, pos >> 4, a.layer, 0, pos & 15, h));
-            krow[lane] = kb0;
-            krow[lane + 64] = kb1;
-            const uint32_t vpos = a.mutant == 2 ? min(pos + 1, a.max_pos - 1) : pos;
-            uint8_t *vplane = a.pool + (uint64_t)(vpos >> 4) * a.g.block_stride +
-                              (uint64_t)a.layer * a.g.layer_stride + a.g.plane_stride +
-                              (uint64_t)h * kVtHead + (vpos & 15) * 2;
-            *reinterpret_cast<uint16_t *>(vplane + lane * 32) = vb0;
-            *reinterpret_cast<uint16_t *>(vplane + (lane + 64) * 32) = vb1;
-        }
-        const float kf0 = bf16_to_f32(kb0), kf1 = bf16_to_f32(kb1);
-        vs[lane] = bf16_to_f32(vb0);
-        vs[lane + 64] = bf16_to_f32(vb1);
-        float d[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) d[r] = fmaf(q0[r], kf0, q1[r] * kf1);
-        const float sp = head_sums8(d, lane) * kInvSqrt128;
-        if ((lane & 7) == 0) sp_sh[lane >> 3] = sp;
-    }
-    __syncthreads();  // qhl / vs / sp_sh complete (waits on LDS only: the page stream stays in flight)
-
-    // B operand of S^T = K q^T: head column n is head n % 8, its hi (n < 8) or lo (n >= 8) half;
-    // k-step ks of lane group g covers dims 32 ks + 8 g .. +8 (16 bytes of LDS)
-    bf16x8 qop[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-        qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[n >> 3][n & 7][32 * ks + 8 * g]));
-
-    float m_l = -INFINITY, l_l = 0.f;
-    f32x4 O[8];
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) O[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (p_begin + 1 == p_end) {
-        dattn_page<true>(T, qop, p_begin * kDattnPage, pos, g, n, m_l, l_l, O);
-    } else if (p_begin < p_end) {
-        // each page computed with the next page's loads in flight
-        DattnPage nx;
-        dattn_load(a, h, p_begin + 1, lane, nx);
-        dattn_page<true>(T, qop, p_begin * kDattnPage, pos, g, n, m_l, l_l, O);
-        T = nx;
-        uint32_t p = p_begin + 1;
-        for (; p + 1 < p_end; ++p) {
-            dattn_load(a, h, p + 1, lane, nx);
-            dattn_page<false>(T, qop, p * kDattnPage, pos, g, n, m_l, l_l, O);
-            T = nx;
-        }
-        dattn_page<false>(T, qop, p * kDattnPage, pos, g, n, m_l, l_l, O);
-    }
-    // Output. Row 4 g + i holds the hi half of head 4 g + i for g < 2 and the lo half for g >= 2,
-    // so a pair sum over lanes {l, l ^ 32} gives the full value; one swap serves two accumulators:
-    // lanes 0-31 get O[nb] (head 4 g + i, dims 16 nb + n), lanes 32-63 get O[nb + 4] (head
-    // 4 (g - 2) + i, dims 16 (nb + 4) + n), so every lane stores 16 values.
-    const uint32_t hg = g & 1, nb_off = (g >> 1) * 4;
-    float ov[4][4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ov[nb][i] = pair_sum<32>(O[nb][i], O[nb + 4][i]);
-    if (s == 0) {
-        // this token: one more online-softmax step with score sp and value vs; lane n of every
-        // row holds head n % 8's state, so the head of row i is gathered by readlane
-        const float sp = sp_sh[n & 7];
-        const float m_new = fmaxf(m_l, sp);
-        const float aold = expf(m_l - m_new);
-        const float pnow = expf(sp - m_new);
-        l_l = l_l * aold + pnow;
-        m_l = m_new;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float a_lo = readlane_f32(aold, i), a_hi = readlane_f32(aold, 4 + i);
-            const float p_lo = readlane_f32(pnow, i), p_hi = readlane_f32(pnow, 4 + i);
-            const float ai = hg ? a_hi : a_lo;
-            const float pi = hg ? p_hi : p_lo;
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb) ov[nb][i] = fmaf(pi, vs[16 * (nb + nb_off) + n], ov[nb][i] * ai);
-        }
-    }
     const uint32_t epoch = a.epoch_dev ? *as_global_u32(a.epoch_dev) * 64u + a.layer : a.epoch_host;
-    float *part = a.part + ((size_t)h * 8 * kDattnSplits + s) * kPartStride;
-    if (holds) {
-        // the partial goes where every CU reads it (agent-scope stores write through the XCD's
-        // L2); once the stores are acknowledged the split's flag carries this launch's epoch.
-        // Dims d and d + 64 sit side by side (o at 4 + 2 (d % 64) + d / 64), so the merge's lane l
-        // reads its two dims with one 8-byte load.
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float *pp = part + (size_t)(4 * hg + i) * kDattnSplits * kPartStride;
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb) {
-                const uint32_t d = 16 * (nb + nb_off) + n;
-                __hip_atomic_store(pp + 4 + 2 * (d & 63) + (d >> 6), ov[nb][i], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        if (lane < 8) {  // lane r holds head r's running max and sum
-            float *pp = part + (size_t)lane * kDattnSplits * kPartStride;
-            __hip_atomic_store(pp, m_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(pp + 1, l_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (lane == 0) __hip_atomic_store(a.flags + h * kDattnSplits + s, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    dattn_split(a, h, s, pos, holds, p_begin, p_end, q0, q1, k0, k1, v0, v1, qw0, qw1, kw0, kw1, rc, rs, T, lds,
+                epoch, lane);
     if (s >= 8) return;
     // Merge of q head 8 h + s: wait until every split of kv head h has flagged this epoch (every
     // split is resident: at most 4 x 64 one-wavefront workgroups), with a bounded number of polls
-    // (a wait that runs out is counted and the merge goes on), then the split-order merge
-    // out = sum w_i o_i / sum w_i l_i with w_i = exp(m_i - max m); lane l holds dims l, l + 64.
+    // (a wait that runs out is counted and the merge goes on).
     {
         const uint32_t *fl = a.flags + h * kDattnSplits;
         uint32_t spins = 0;
@@ -302,51 +100,14 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
         }
     }
     const uint32_t hq = h * 8 + s;
-    const float *base = a.part + (size_t)hq * kDattnSplits * kPartStride;
-    // Every load of the merge goes out at once (one round trip): lane j's (m, l) of split j, and
-    // per split i the (o[l], o[l + 64]) pair of lane l, in chunks of 16 splits up to `active`
-    // (indices past it clamp to the last split and get weight 0).
-    const uint32_t j = min(lane, active - 1);
-    const uint64_t mlj = __hip_atomic_load(reinterpret_cast<const uint64_t *>(base + (size_t)j * kPartStride),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint64_t xo[kDattnSplits];
-#pragma unroll
-    for (uint32_t c = 0; c < kDattnSplits / 16; ++c) {
-        if (c * 16 >= active) break;
-#pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-            const uint32_t si = min(c * 16 + i, active - 1);
-            xo[c * 16 + i] = __hip_atomic_load(
-                reinterpret_cast<const uint64_t *>(base + (size_t)si * kPartStride + 4 + 2 * lane),
-                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    const float mj = __uint_as_float((uint32_t)mlj), lj = __uint_as_float((uint32_t)(mlj >> 32));
-    const float mv = lane < active ? mj : -INFINITY;
-    float M = row16_max(mv);
-    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
-    const float wj = lane < active ? (a.mutant == 4 ? 1.f : expf(mj - M)) : 0.f;
-    const float L = wave_sum(wj * (lane < active ? lj : 0.f));
-    float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-    for (uint32_t c = 0; c < kDattnSplits / 16; ++c) {
-        if (c * 16 >= active) break;
-#pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-            // lanes past `active` hold weight 0, so a split past it adds nothing (its o values are
-            // the last split's, finite)
-            const uint32_t si = c * 16 + i;
-            const float wi = readlane_f32(wj, (int)si);
-            o0 = fmaf(wi, __uint_as_float((uint32_t)xo[si]), o0);
-            o1 = fmaf(wi, __uint_as_float((uint32_t)(xo[si] >> 32)), o1);
-        }
-    }
-    a.out[hq * 128 + lane] = o0 * (a.out_scale / L);
-    a.out[hq * 128 + 64 + lane] = o1 * (a.out_scale / L);
+    float o0, o1;
+    dattn_merge<kDattnSplits>(a.part, hq, active, a.mutant, a.out_scale, o0, o1, lane);
+    a.out[hq * 128 + lane] = o0;
+    a.out[hq * 128 + 64 + lane] = o1;
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_dattn, dim3(4, kDattnSplits), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_dattn, dim3(4, a.splits), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 

@@ -276,11 +276,28 @@ struct OmegaGpuDecodeGraph {
     GraphIo *pin = nullptr;         // pinned host twin of io
     const OmegaGpuBf16Tensor *embed = nullptr;  // optional: device embedding (token-id entry)
     // graphs: [0] x from the host, [1] x gathered from the embedding by token id; [2], [3] the
-    // same with an event-record node before the first kernel and after every kernel (stamps)
-    hipGraph_t graph_v[4] = {nullptr, nullptr, nullptr, nullptr};
-    hipGraphExec_t exec_v[4] = {nullptr, nullptr, nullptr, nullptr};
-    bool dirty_v[4] = {true, true, true, true};
-    void mark_dirty() { dirty_v[0] = dirty_v[1] = dirty_v[2] = dirty_v[3] = true; }
+    // same with an event-record node before the first kernel and after every kernel (stamps);
+    // [4], [5] the persistent form (one launch of every layer, then the lm_head) of [0], [1]
+    static constexpr int kVariants = 6;
+    hipGraph_t graph_v[kVariants] = {};
+    hipGraphExec_t exec_v[kVariants] = {};
+    bool dirty_v[kVariants] = {true, true, true, true, true, true};
+    void mark_dirty() {
+        for (bool &d : dirty_v) d = true;
+        players_dirty = true;
+    }
+    // the persistent form: per-layer descriptors, words (f32 | epoch) per (layer, stage), the
+    // attention's split flags per layer, stage stamps
+    bool persistent = false;        // chosen at create when the device holds the whole launch
+    bool players_dirty = true;
+    PLayer *players = nullptr;      // [layers]
+    uint64_t *words = nullptr;
+    size_t words_bytes = 0;
+    uint32_t *pflags = nullptr;     // [layers][4][kDattnSplits]
+    unsigned long long *pstamps = nullptr;  // [1 + layers * kTokStampsPerLayer]
+    bool stage_stamps = false;
+    bool stage_valid = false;
+    std::vector<unsigned long long> stage_host;
     bool stamps_graph = false;  // the last stamped token ran as the stamped graph
     int mutant = 0;
     bool stamps = false;
@@ -353,6 +370,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_QKV));
         // 2. attention (q/k norm + RoPE, K/V append) with the split merge in the same launch
         DattnArgs da = cache_dattn(g->cache, l, eps, g->qkv, g->part);
+        da.splits = kGraphSplits;
         da.pos_dev = pos_dev;
         da.flags = g->flags;
         da.errc = &g->io->merge_err;
@@ -434,6 +452,139 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
     return OMEGA_GPU_OK;
 }
 
+// words of one (layer, stage) buffer set, carved from g->words in this order
+struct WordLayout {
+    size_t x, qkv, att, xn, log, xp, act, total;
+};
+WordLayout word_layout(uint32_t layers) {
+    WordLayout w{};
+    size_t o = 0;
+    w.x = o;
+    o += (size_t)(layers + 1) * kHidden;
+    w.qkv = o;
+    o += (size_t)layers * 5120;
+    w.att = o;
+    o += (size_t)layers * 4096;
+    w.xn = o;
+    o += (size_t)layers * kHidden;
+    w.log = o;
+    o += (size_t)layers * kExperts;
+    w.xp = o;
+    o += (size_t)layers * kHidden;
+    w.act = o;
+    o += (size_t)layers * kTopK * kInter;
+    w.total = o;
+    return w;
+}
+
+// the per-layer descriptors of the persistent form, rebuilt after set_layer / force_routes
+int upload_players(OmegaGpuDecodeGraph *g) {
+    std::vector<PLayer> h(g->cfg.layers);
+    for (uint32_t l = 0; l < g->cfg.layers; ++l) {
+        const GLayer &L = g->layers[l];
+        RouterArgs ra = router_args(g->router, l, g->x, g->cfg.eps, g->cfg.norm_topk, 1.0f);
+        DattnArgs da = cache_dattn(g->cache, l, g->cfg.eps, g->qkv, g->part);
+        PLayer &p = h[l];
+        p.qkv_w = L.qkv->w;
+        p.qkv_s = L.qkv->s;
+        p.o_w = L.o->w;
+        p.o_s = L.o->s;
+        p.gu_w = L.gu->w;
+        p.gu_s = L.gu->s;
+        p.dn_w = L.dn->w;
+        p.dn_s = L.dn->s;
+        p.in_norm = L.input_norm;
+        p.rgate = ra.gate;
+        p.rnorm = ra.norm_w;
+        p.dir_gu = ra.dir_gu;
+        p.dir_dn = ra.dir_dn;
+        p.q_norm = da.q_norm;
+        p.k_norm = da.k_norm;
+        p.forced = g->force_on ? g->forced + (size_t)l * 8 : nullptr;
+        p.log_ids = g->route_log + (size_t)l * 8;
+        p.log_w = g->route_log_w + (size_t)l * 8;
+    }
+    OMEGA_HIP(F_SESSION, hipMemcpy(g->players, h.data(), h.size() * sizeof(PLayer), hipMemcpyHostToDevice));
+    g->players_dirty = false;
+    return OMEGA_GPU_OK;
+}
+
+// One token in the persistent form: every layer in one launch, then the final norm, lm_head and
+// argmax as in the chain.
+int enqueue_token_persistent(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &kinds, bool gather,
+                             std::vector<hipEvent_t> *kev = nullptr) {
+    kinds.clear();
+    size_t k_i = 0;
+    // direct launches in stamp mode: each launch records its own start / stop
+    auto arm = [&]() {
+        if (kev && k_i + 1 < kev->size()) {
+            launch_stamp().start = (*kev)[k_i];
+            launch_stamp().stop = (*kev)[k_i + 1];
+            k_i += 2;
+        }
+    };
+    const WordLayout wl = word_layout(g->cfg.layers);
+    RouterArgs ra = router_args(g->router, 0, g->x, g->cfg.eps, g->cfg.norm_topk, 1.0f);
+    DattnArgs da = cache_dattn(g->cache, 0, g->cfg.eps, g->qkv, g->part);
+    PTokenArgs a;
+    a.layers = g->players;
+    a.nlayers = g->cfg.layers;
+    a.io = &g->io->pos;
+    a.errc = &g->io->merge_err;
+    a.abort = &g->io->pad[0];
+    a.embed = gather ? g->embed->w : nullptr;
+    a.embed_rows = gather ? g->embed->n : 0;
+    a.x = g->x;
+    a.pool = da.pool;
+    a.g = da.g;
+    a.max_pos = da.max_pos;
+    a.rope_cos = da.rope_cos;
+    a.rope_sin = da.rope_sin;
+    a.eps = g->cfg.eps;
+    a.norm_topk = g->cfg.norm_topk;
+    a.w_x = g->words + wl.x;
+    a.w_qkv = g->words + wl.qkv;
+    a.w_att = g->words + wl.att;
+    a.w_xn = g->words + wl.xn;
+    a.w_log = g->words + wl.log;
+    a.w_xp = g->words + wl.xp;
+    a.w_act = g->words + wl.act;
+    a.part = g->part;
+    a.aflags = g->pflags;
+    a.r_xout = ra.xout;
+    a.r_logits = ra.logits;
+    a.r_weights = ra.weights;
+    a.r_ids = ra.ids;
+    a.r_tab_gu = ra.tab_gu;
+    a.r_tab_dn = ra.tab_dn;
+    a.graph_mutant = g->mutant;
+    // a wait runs out after 10 ms of the 100 MHz clock; test mutant 9: at once (every wait that
+    // is not already satisfied gives up, the token is reported failed, every kernel exits)
+    a.wait_ticks = g->mutant == 9 ? 0 : 1000000;
+    a.dattn_mutant = da.mutant;
+    a.router_mutant = ra.mutant;
+    a.tiles_per_split = da.tiles_per_split;
+    a.attn_out_scale = g->mutant == 3 ? 2.0f : 1.0f;
+    a.stamps = g->stage_stamps ? g->pstamps : nullptr;
+    arm();
+    OMEGA_HIP(F_SESSION, launch_token(a, st));
+    kinds.push_back(OMEGA_GPU_DGRAPH_K_QKV);
+    Bf16RowsArgs b;
+    b.w = g->lm->w;
+    b.n = g->lm->n;
+    b.k = g->lm->k;
+    b.x = g->x;
+    b.norm_w = g->final_norm;
+    b.eps = g->cfg.eps;
+    b.hidden_out = g->hidden;
+    b.y = g->logits;
+    b.argmax = g->io->argmax;
+    arm();
+    OMEGA_HIP(F_SESSION, launch_bf16_rows(b, st));
+    kinds.push_back(OMEGA_GPU_DGRAPH_K_LM_HEAD);
+    return OMEGA_GPU_OK;
+}
+
 int ensure_events(std::vector<hipEvent_t> &v, size_t n) {
     while (v.size() < n) {
         hipEvent_t e;
@@ -460,7 +611,12 @@ int rebuild(OmegaGpuDecodeGraph *g, Ctx *c, int v) {
         if (rc) return rc;
         ev = &g->events;
     }
+    if (v >= 4 && g->players_dirty) {
+        const int rc = upload_players(g);
+        if (rc) return rc;
+    }
     const int rc = build_graph(F_SESSION, "decode graph", &g->graph_v[v], &g->exec_v[v], [&]() {
+        if (v >= 4) return enqueue_token_persistent(g, c->stream, g->kinds, (v & 1) == 1);
         return enqueue_token(g, c->stream, g->kinds, ev, nullptr, false, (v & 1) == 1);
     });
     if (rc) return rc;
@@ -541,6 +697,12 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     M((void **)&g->forced, (size_t)cfg->layers * 8 * 4);
     M((void **)&g->flags, 4 * kDattnSplits * 4);
     for (auto &L : g->layers) M((void **)&L.input_norm, kHidden * 4);
+    // the persistent form's state (words start at epoch 0, which no token uses)
+    g->words_bytes = word_layout(cfg->layers).total * 8;
+    M((void **)&g->players, (size_t)cfg->layers * sizeof(PLayer));
+    M((void **)&g->words, g->words_bytes);
+    M((void **)&g->pflags, (size_t)cfg->layers * 4 * kDattnSplits * 4);
+    M((void **)&g->pstamps, (size_t)(1 + cfg->layers * kTokStampsPerLayer) * 8);
     if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -549,6 +711,9 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
         return OMEGA_GPU_CHIP_FAIL;
     }
     memset(g->pin, 0, sizeof(GraphIo));
+    // the chain is the default form: on the MI355X it measured faster (1.65 against 1.86 ms a
+    // token); omega_gpu_decode_graph_set_persistent switches
+    g->persistent = false;
     *out = g;
     return OMEGA_GPU_OK;
 }
@@ -558,14 +723,15 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *c = ctx(F_SESSION);
     if (c) (void)hipStreamSynchronize(c->stream);
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < OmegaGpuDecodeGraph::kVariants; ++v) {
         if (g->exec_v[v]) (void)hipGraphExecDestroy(g->exec_v[v]);
         if (g->graph_v[v]) (void)hipGraphDestroy(g->graph_v[v]);
     }
     for (hipEvent_t e : g->events) (void)hipEventDestroy(e);
     for (hipEvent_t e : g->kevents) (void)hipEventDestroy(e);
     void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
-                  g->final_norm, g->route_log, g->route_log_w, g->forced, g->flags};
+                  g->final_norm, g->route_log, g->route_log_w, g->forced, g->flags,
+                  g->players, g->words, g->pflags, g->pstamps};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     for (auto &L : g->layers)
@@ -640,9 +806,12 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     }
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
-    // graph variant: x from the host or by token id; stamped (event nodes between kernels) or not
-    const int v = (x_embed ? 0 : 1) + (g->stamps ? 2 : 0);
+    // graph variant: x from the host or by token id; stamped (event nodes between kernels) or not;
+    // the persistent form unless stamps or direct launches ask for the chain
+    const bool pers = g->persistent && ((!g->stamps && g->flush_each == 0) || g->flush_each == 3);
+    const int v = pers ? 4 + (x_embed ? 0 : 1) : (x_embed ? 0 : 1) + (g->stamps ? 2 : 0);
     g->stamps_valid = false;
+    g->stage_valid = false;
     uint64_t record_ns = 0;
     // flush_each runs the same kernels as direct launches (with stamps: events between them and
     // each launch timed by its dispatch); otherwise the graph is replayed
@@ -660,8 +829,12 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     pin->tok = token_in;
     // The attention's split flags hold epoch * 64 + layer. Before the epoch wraps, or after a token
     // that failed once its epoch was taken, the flags are cleared and the epochs start again from 1.
+    // The persistent form's words and split flags hold the epoch itself, so they are cleared
+    // whenever the epochs start again.
     if (++g->epoch >= (1u << 26) || g->sync_stale) {
         OMEGA_HIP(F_SESSION, hipMemsetAsync(g->flags, 0, 4 * kDattnSplits * 4, c->stream));
+        OMEGA_HIP(F_SESSION, hipMemsetAsync(g->words, 0, g->words_bytes, c->stream));
+        OMEGA_HIP(F_SESSION, hipMemsetAsync(g->pflags, 0, (size_t)g->cfg.layers * 4 * kDattnSplits * 4, c->stream));
         g->epoch = 1;
     }
     g->sync_stale = true;  // until this token has completed
@@ -673,7 +846,23 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
         OMEGA_HIP(F_SESSION, hipMemcpyAsync(g->x, xin, kHidden * 4, hipMemcpyHostToDevice, c->stream));
     }
     OMEGA_HIP(F_SESSION, hipEventRecord(c->ev0, c->stream));
-    if (eager) {
+    if (eager && pers) {
+        // the persistent form as direct launches (flush_each 3), each timed by its dispatch in
+        // stamp mode
+        std::vector<hipEvent_t> *kev = nullptr;
+        if (g->stamps) {
+            int rc = ensure_events(g->kevents, 4);
+            if (!rc) rc = ensure_events(g->events, 3);
+            if (rc) return rc;
+            kev = &g->kevents;
+        }
+        if (g->players_dirty) {
+            const int rc = upload_players(g);
+            if (rc) return rc;
+        }
+        int rc = enqueue_token_persistent(g, c->stream, g->kinds, (v & 1) == 1, kev);
+        if (rc) return rc;
+    } else if (eager) {
         std::vector<hipEvent_t> *ev = nullptr, *kev = nullptr;
         if (g->stamps) {
             const size_t launches = (size_t)kLaunchesPerLayer * g->cfg.layers + 1;
@@ -695,10 +884,17 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
                                         c->stream));
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
     if (pin->merge_err) {
-        set_error(F_SESSION, "decode graph: the attention's split merge ran out of waits (%u)", pin->merge_err);
+        set_error(F_SESSION, "decode graph: %u in-launch waits ran out (%s form)", pin->merge_err,
+                  pers ? "persistent" : "chain");
         return OMEGA_GPU_CHIP_FAIL;
     }
     g->sync_stale = false;
+    if (pers && g->stage_stamps) {
+        g->stage_host.resize(1 + (size_t)g->cfg.layers * kTokStampsPerLayer);
+        OMEGA_HIP(F_SESSION, hipMemcpy(g->stage_host.data(), g->pstamps, g->stage_host.size() * 8,
+                                       hipMemcpyDeviceToHost));
+        g->stage_valid = true;
+    }
     *token = argmax_from_slots(pin->argmax);
     g->stamps_valid = g->stamps;
     g->stamps_graph = g->stamps && !eager;
@@ -779,7 +975,9 @@ void omega_gpu_decode_graph_set_flush_each(OmegaGpuDecodeGraph *g, int on) {
     // 1 (any non-zero but 2): submit and wait after every launch (the batching comparison);
     // 2: direct launches without the graph and without waits (profilers that cannot follow
     // graph capture)
-    g->flush_each = on == 2 ? 2 : (on != 0 ? 1 : 0);
+    // 3: the persistent form as direct launches (each dispatch timed in stamp mode); the chain
+    // where the persistent form is off
+    g->flush_each = on == 2 ? 2 : on == 3 ? (g->persistent ? 3 : 2) : (on != 0 ? 1 : 0);
 }
 
 void omega_gpu_decode_graph_test_set_mutant(OmegaGpuDecodeGraph *g, int mutant) {
@@ -892,6 +1090,43 @@ int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint3
 
 const char *omega_gpu_decode_graph_kind_name(uint8_t kind) {
     return kind < 12 ? kKindNames[kind] : "?";
+}
+
+int omega_gpu_decode_graph_set_persistent(OmegaGpuDecodeGraph *g, int on) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g) return OMEGA_GPU_BAD_ARGS;
+    int dev = 0;
+    const bool want = on != 0 && hipGetDevice(&dev) == hipSuccess && token_fits(dev);
+    g->persistent = want;
+    return want ? 1 : 0;
+}
+
+void omega_gpu_decode_graph_set_stage_stamps(OmegaGpuDecodeGraph *g, int on) {
+    if (!g) return;
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    if (g->stage_stamps != (on != 0)) g->dirty_v[4] = g->dirty_v[5] = true;
+    g->stage_stamps = on != 0;
+    g->stage_valid = false;
+}
+
+int omega_gpu_decode_graph_stage_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g || !ns) return OMEGA_GPU_BAD_ARGS;
+    if (!g->stage_valid) {
+        set_error(F_SESSION, "decode graph stage_ns: stage stamps off, or the last token ran as the chain");
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    const uint32_t n = g->cfg.layers * kTokStampsPerLayer;
+    if (cap < n) {
+        set_error(F_SESSION, "decode graph stage_ns: capacity %u < %u", cap, n);
+        return OMEGA_GPU_TOO_LARGE;
+    }
+    // the constant clock runs at 100 MHz: 10 ns a tick
+    const unsigned long long t0 = g->stage_host[0];
+    for (uint32_t i = 0; i < n; ++i) ns[i] = (uint64_t)(g->stage_host[1 + i] - t0) * 10u;
+    return (int)n;
 }
 
 }  // extern "C"

@@ -160,7 +160,12 @@ struct DattnArgs {
     float *out = nullptr;            // [32][128]
     float out_scale = 1.0f;
     int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written; 4: maxima ignored
+    uint32_t splits = kDattnSplits;  // split workgroups per kv head (the launch's grid y, <= kDattnSplits)
 };
+// The decode graph cuts a kv head's pages into at most this many splits in both of its forms (the
+// persistent launch holds two splits per attention workgroup), so the two forms give the same bits
+// at every position.
+constexpr uint32_t kGraphSplits = 64;
 constexpr uint32_t kDattnMergeSpins = 1u << 22;  // bounded wait of the split merge (seconds)
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st);
 
@@ -301,5 +306,71 @@ hipError_t launch_attn_combine_items(const CombineItemsArgs &a, uint32_t seqs, h
 
 // RoPE table of one position range (host twin of the oracle's rope_cos_sin)
 void rope_table(double theta, uint32_t positions, float *cos_out, float *sin_out);
+
+// ---------------------------------------------------------------- persistent decode token
+// The decode graph's layers as one persistent launch (ptoken.hip). One descriptor per layer, in
+// device memory.
+struct PLayer {
+    const uint8_t *qkv_w;  // [5120][2048] e4m3, scales [40][16]
+    const float *qkv_s;
+    const uint8_t *o_w;    // [2048][4096], scales [16][32]
+    const float *o_s;
+    const uint8_t *gu_w;   // [128][1536][2048], scales [128][12][16]
+    const float *gu_s;
+    const uint8_t *dn_w;   // [128][2048][768], scales [128][16][6]
+    const float *dn_s;
+    const float *in_norm;  // [2048]
+    const uint16_t *rgate; // router [128][2048] bf16
+    const float *rnorm;    // [2048]
+    const uint64_t *dir_gu, *dir_dn;  // [128][2]: expert weight / scale addresses
+    const float *q_norm, *k_norm;     // [128]
+    const uint32_t *forced;           // parity tests: 8 expert ids instead of the ranking, or null
+    uint32_t *log_ids;                // [8] routed ids of the last token
+    float *log_w;                     // [8]
+};
+constexpr uint32_t kTokGroups = 256;   // one workgroup per CU, all resident
+constexpr uint32_t kTokThreads = 512;  // eight wavefronts
+constexpr uint32_t kTokStampsPerLayer = 5;
+struct PTokenArgs {
+    const PLayer *layers = nullptr;
+    uint32_t nlayers = 0;
+    const uint32_t *io = nullptr;  // pos, token id, epoch (written by the host before the launch)
+    uint32_t *errc = nullptr;      // waits that ran out
+    uint32_t *abort = nullptr;     // set by the first wait that runs out: every later wait ends
+    const uint16_t *embed = nullptr;  // layer 0's row from the embedding by token id, or null: from x
+    uint32_t embed_rows = 0;
+    float *x = nullptr;            // residual row: layer 0's input without embed; the last layer's output
+    uint8_t *pool = nullptr;       // the fused decode cache
+    KvGeom g{};
+    uint32_t max_pos = 0;
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    float eps = 1e-6f;
+    int norm_topk = 1;
+    // words (f32 value | epoch), one buffer per (layer, stage)
+    uint64_t *w_x = nullptr;    // [layers + 1][2048] layer inputs (index 0 unused)
+    uint64_t *w_qkv = nullptr;  // [layers][5120]
+    uint64_t *w_att = nullptr;  // [layers][4096]
+    uint64_t *w_xn = nullptr;   // [layers][2048] residual after the attention
+    uint64_t *w_log = nullptr;  // [layers][128]
+    uint64_t *w_xp = nullptr;   // [layers][2048] the post-attention normed row x'
+    uint64_t *w_act = nullptr;  // [layers][8][768]
+    float *part = nullptr;      // attention partials [32][kDattnSplits][kPartStride]
+    uint32_t *aflags = nullptr; // [layers][4][kDattnSplits] split flags (epochs)
+    // the router's device state after the token (the last layer's)
+    float *r_xout = nullptr, *r_logits = nullptr, *r_weights = nullptr;
+    uint32_t *r_ids = nullptr;
+    uint64_t *r_tab_gu = nullptr, *r_tab_dn = nullptr;
+    int graph_mutant = 0;       // 1: gate and up swapped; 2: slot 7 dropped from the combine
+    uint64_t wait_ticks = 0;    // a wait runs out after this many 100 MHz ticks (0 runs out at once)
+    int dattn_mutant = 0;
+    int router_mutant = 0;
+    uint32_t tiles_per_split = 0;
+    float attn_out_scale = 1.0f;
+    unsigned long long *stamps = nullptr;  // [1 + layers * kTokStampsPerLayer] or null
+};
+constexpr uint32_t kTokLds = 96 * 1024;  // dynamic LDS: one workgroup per CU
+hipError_t launch_token(const PTokenArgs &a, hipStream_t st);
+// whether this device can hold every workgroup of the persistent token kernel at once
+bool token_fits(int device);
 
 }  // namespace omega

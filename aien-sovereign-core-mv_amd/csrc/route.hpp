@@ -57,12 +57,12 @@ __device__ __forceinline__ void route_keys(const float *logits, uint32_t (&k)[Q]
     for (int q = 0; q < Q; ++q) k[q] = ord_key(*as_global_f32(logits + lane + 64 * q));
 }
 
-// logits: Q * 64 expert values (+1 shared) in global memory, their keys already loaded (the
-// keys are consumed).
+// logits: Q * 64 expert values (+1 shared), read through `logit(id)` (global memory or an LDS
+// copy), their keys already loaded (the keys are consumed).
 // mutant 2: the mask after a pick hits id ^ 1; mutant 4: weights not normalised.
-template <int Q>
-__device__ __forceinline__ void route_topk_keys(uint32_t (&k)[Q], const float *logits, uint32_t shared,
-                                                int norm_topk, int mutant, Route &r) {
+template <int Q, typename Logit>
+__device__ __forceinline__ void route_topk_keys_r(uint32_t (&k)[Q], Logit logit, uint32_t shared,
+                                                  int norm_topk, int mutant, Route &r) {
     constexpr uint32_t experts = 64 * Q;
     const uint32_t lane = lane_id();
     float v[kTopK];
@@ -96,25 +96,32 @@ __device__ __forceinline__ void route_topk_keys(uint32_t (&k)[Q], const float *l
     }
     if (!norm_topk) {
         sum = 0.f;
-        for (uint32_t id = 0; id < experts; ++id) sum += expf(*as_global_f32(logits + id) - mx);
+        for (uint32_t id = 0; id < experts; ++id) sum += expf(logit(id) - mx);
     }
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) r.w[s] = mutant == 4 ? p[s] : p[s] / sum;
     if (shared) {
         r.id[kTopK] = experts;
-        r.w[kTopK] = 1.0f / (1.0f + expf(-*as_global_f32(logits + experts)));
+        r.w[kTopK] = 1.0f / (1.0f + expf(-logit(experts)));
     }
+}
+template <int Q>
+__device__ __forceinline__ void route_topk_keys(uint32_t (&k)[Q], const float *logits, uint32_t shared,
+                                                int norm_topk, int mutant, Route &r) {
+    route_topk_keys_r<Q>(k, [&](uint32_t id) { return *as_global_f32(logits + id); }, shared, norm_topk,
+                         mutant, r);
 }
 
 // Teacher forcing for parity tests: the 8 expert ids come from `forced` (slot order), the weights
 // are the softmax of this launch's own logits over that set (exp(l - max) / sum, as the ranking
 // computes them for its own set). Every lane ends with the same result.
-__device__ __forceinline__ void route_forced(const float *logits, const uint32_t *forced, Route &r) {
+template <typename Logit>
+__device__ __forceinline__ void route_forced_r(Logit logit, const uint32_t *forced, Route &r) {
     float v[kTopK];
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
         r.id[s] = *as_global_u32(forced + s);
-        v[s] = *as_global_f32(logits + r.id[s]);
+        v[s] = logit(r.id[s]);
     }
     float mx = v[0];
 #pragma unroll
@@ -127,6 +134,9 @@ __device__ __forceinline__ void route_forced(const float *logits, const uint32_t
     }
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) r.w[s] = p[s] / sum;
+}
+__device__ __forceinline__ void route_forced(const float *logits, const uint32_t *forced, Route &r) {
+    route_forced_r([&](uint32_t id) { return *as_global_f32(logits + id); }, forced, r);
 }
 
 template <int Q>

@@ -30,11 +30,14 @@ struct Slab {
     __device__ static uint32_t col_bytes(int ph, uint32_t lane) { return (ph * 1024u + 16u * lane) % KB; }
 
     u32x4 v[CH];
-    __device__ __forceinline__ void load(const void *rows, uint32_t lane) {
+    // The chunk array may also live outside a Slab (a persistent kernel's prefetch registers):
+    // the static forms take it as `w` and are what the members call.
+    __device__ __forceinline__ static void load_v(u32x4 *w, const void *rows, uint32_t lane) {
         const gu32x4 *p = as_global(rows) + lane;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) v[c] = __builtin_nontemporal_load(p + c * 64);
+        for (int c = 0; c < CH; ++c) w[c] = __builtin_nontemporal_load(p + c * 64);
     }
+    __device__ __forceinline__ void load(const void *rows, uint32_t lane) { load_v(v, rows, lane); }
     __device__ __forceinline__ void zero() {
 #pragma unroll
         for (int c = 0; c < CH; ++c) v[c] = u32x4{0u, 0u, 0u, 0u};
@@ -43,10 +46,15 @@ struct Slab {
     template <typename Dot>
     __device__ __forceinline__ void accumulate(const float (&sc)[P], float (&acc)[RPW], uint32_t lane,
                                                Dot dot) const {
+        accumulate_v(v, sc, acc, lane, dot);
+    }
+    template <typename Dot>
+    __device__ __forceinline__ static void accumulate_v(const u32x4 *w, const float (&sc)[P], float (&acc)[RPW],
+                                                        uint32_t lane, Dot dot) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int ph = c % P;
-            const float p = dot(v[c], ph);
+            const float p = dot(w[c], ph);
             const int r0 = row_lo(c), sl = split_lane(c);
             if (sl >= 64) {
                 acc[r0] = fmaf(p, sc[ph], acc[r0]);
@@ -124,7 +132,11 @@ struct Fp8Slab : Slab<K, RPW> {
     }
     __device__ __forceinline__ void dot(const float (&xr)[P][16], const float (&sc)[P],
                                         float (&acc)[RPW], uint32_t lane) const {
-        this->accumulate(sc, acc, lane, [&](const u32x4 w, int ph) { return fp8_dot16(w, xr[ph]); });
+        dot_v(this->v, xr, sc, acc, lane);
+    }
+    __device__ __forceinline__ static void dot_v(const u32x4 *w, const float (&xr)[P][16], const float (&sc)[P],
+                                                 float (&acc)[RPW], uint32_t lane) {
+        B::accumulate_v(w, sc, acc, lane, [&](const u32x4 q, int ph) { return fp8_dot16(q, xr[ph]); });
     }
     // RPW rows starting at row0 may reach into the next 128-row scale block when RPW does not
     // divide 128: sc[0] holds the scales of row0's block, sc[1] those of the last row's block, and
@@ -132,13 +144,51 @@ struct Fp8Slab : Slab<K, RPW> {
     static constexpr bool kOneBlock = 128 % RPW == 0;
     __device__ __forceinline__ void dot2(const float (&xr)[P][16], const float (&sc)[2][P], uint32_t row0,
                                          float (&acc)[RPW]) const {
+        dot2_v(this->v, xr, sc, row0, acc);
+    }
+    // dot_v / dot2_v with the activation read from a row staged in LDS chunk by chunk instead of
+    // held as phases in registers: the same values, products and order
+    __device__ __forceinline__ static void xphase_lds(const float *xs, int ph, uint32_t lane, float (&xx)[16]) {
+        const f32x4 *q = reinterpret_cast<const f32x4 *>(xs + B::col_bytes(ph, lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 t = q[i];
+            xx[4 * i] = t.x;
+            xx[4 * i + 1] = t.y;
+            xx[4 * i + 2] = t.z;
+            xx[4 * i + 3] = t.w;
+        }
+    }
+    __device__ __forceinline__ static void dot_lds(const u32x4 *w, const float *xs, const float (&sc)[P],
+                                                   float (&acc)[RPW], uint32_t lane) {
+        B::accumulate_v(w, sc, acc, lane, [&](const u32x4 q, int ph) {
+            float xx[16];
+            xphase_lds(xs, ph, lane, xx);
+            return fp8_dot16(q, xx);
+        });
+    }
+    __device__ __forceinline__ static void dot2_lds(const u32x4 *w, const float *xs, const float (&sc)[2][P],
+                                                    uint32_t row0, float (&acc)[RPW], uint32_t lane) {
         static_assert(K >= 1024, "one row per chunk");
 #pragma unroll
         for (int c = 0; c < B::CH; ++c) {
             const int ph = c % P;
             const int r = B::row_lo(c);
             const bool upper = ((row0 + r) >> 7) != (row0 >> 7);
-            acc[r] = fmaf(fp8_dot16(this->v[c], xr[ph]), upper ? sc[1][ph] : sc[0][ph], acc[r]);
+            float xx[16];
+            xphase_lds(xs, ph, lane, xx);
+            acc[r] = fmaf(fp8_dot16(w[c], xx), upper ? sc[1][ph] : sc[0][ph], acc[r]);
+        }
+    }
+    __device__ __forceinline__ static void dot2_v(const u32x4 *w, const float (&xr)[P][16], const float (&sc)[2][P],
+                                                  uint32_t row0, float (&acc)[RPW]) {
+        static_assert(K >= 1024, "one row per chunk");
+#pragma unroll
+        for (int c = 0; c < B::CH; ++c) {
+            const int ph = c % P;
+            const int r = B::row_lo(c);
+            const bool upper = ((row0 + r) >> 7) != (row0 >> 7);
+            acc[r] = fmaf(fp8_dot16(w[c], xr[ph]), upper ? sc[1][ph] : sc[0][ph], acc[r]);
         }
     }
 };

@@ -268,6 +268,9 @@ SIGNATURES = {
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
     "omega_gpu_decode_graph_test_force_routes": (i32, [P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
+    "omega_gpu_decode_graph_set_persistent": (i32, [P, i32]),
+    "omega_gpu_decode_graph_set_stage_stamps": (None, [P, i32]),
+    "omega_gpu_decode_graph_stage_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_embedding": (i32, [P, P]),
     "omega_gpu_decode_graph_token_id": (i32, [P, u32, u32, U32P, C.POINTER(GraphStats)]),
     "omega_gpu_stream": (P, []),
@@ -788,6 +791,28 @@ class DecodeGraph:
         if n < 0:
             self._rc(n, "stamps")
         return st[:n + 1], kinds[:n]
+
+    def set_persistent(self, on):
+        """The graph's form: True for one persistent launch of every layer (the default where
+        the device holds it), False for the chain of six launches per layer. Returns the form in
+        use afterwards."""
+        r = lib().omega_gpu_decode_graph_set_persistent(self.h, int(on))
+        if r < 0:
+            self._rc(r, "set_persistent")
+        return bool(r)
+
+    def set_stage_stamps(self, on):
+        lib().omega_gpu_decode_graph_set_stage_stamps(self.h, int(on))
+
+    def stage_ns(self):
+        """[layers][5] ns since the persistent launch started at which each layer's stages
+        ended (input row, attention row, residual, route inputs, down rows), last token."""
+        cap = self.layers * 5
+        ns = np.zeros(cap, np.uint64)
+        n = lib().omega_gpu_decode_graph_stage_ns(self.h, ns.ctypes.data_as(U64P), cap)
+        if n < 0:
+            self._rc(n, "stage_ns")
+        return ns[:n].reshape(self.layers, 5)
 
     def kernel_ns(self):
         """Per-launch durations (ns) of the last stamped token, as the dispatch recorded them."""

@@ -10,11 +10,18 @@ generates). A seeded 512-token prompt runs through the decode graph first (untim
 hipGraph replay (token id in, greedy token out). value = tokens / second.
 
 The JSON line also carries:
-  roofline: the dominant kernel's algorithmic bytes per launch over its average duration; the
-            durations come from a stamped pass of the same decode steps in which every launch's
-            start and end are recorded by its own dispatch (hipExtLaunchKernel events on the
-            library stream); peak 8 TB/s. traffic comes from the committed rocprofv3 PMC
-            summary for that kernel when one exists (profiles/), else null.
+  roofline: the dominant launch's algorithmic bytes over its average duration. The timed form
+            is the default chain of six launches per layer (or, with --persistent, every layer in
+            one persistent launch, "decode_layers", then the lm_head). The durations come from
+            further decode steps made as direct launches, each launch's start and end recorded by
+            its own dispatch (hipExtLaunchKernel events on the library stream); peak 8 TB/s.
+            traffic comes from the committed rocprofv3 PMC summary for that kernel when one exists
+            (profiles/), else null.
+  other_form: the same step in the other form (tok/s).
+  persistent_stage_us_per_layer: the persistent launch's own stage stamps (the GPU's constant
+            clock), the mean time per layer of each stage: input row handoff, q|k|v + attention,
+            o + residual, router and route, expert FFN (gate|up and down).
+  top2_margins: the top-2 logit margin of each untimed stamped token.
   cpu_baseline: the C oracle engine (the CPU restatement of the reference's host step) on the
             host cores at the GPU run's context: 4 of the 48 layers over a cache holding the
             same number of positions, plus the full-vocab lm_head, scaled to the 48-layer step;
@@ -52,7 +59,9 @@ def algorithmic_bytes(kind, ctx):
     scales, activations in and out; the KV rows the attention must read)."""
     if kind == "qkv":          # 5120 x 2048 e4m3 + scales + x + norm weights + q|k|v out
         return 5120 * 2048 + 40 * 16 * 4 + 2 * H * 4 + 5120 * 4
-    splits = min(64, max(1, -(-(ctx - 1) // 16)))
+    # the decode graph cuts a kv head's pages into at most 64 splits
+    pages = max(1, -(-(ctx - 1) // 16))
+    splits = -(-pages // -(-pages // 64))
     if kind == "attn":         # K and V of 4 heads over ctx positions + q|k|v in + the split
         # partials out and back in for the merge + the attention row out
         return 2 * KVH * ctx * HD * 2 + 5120 * 4 + 2 * QH * splits * 132 * 4 + 4096 * 4
@@ -127,6 +136,7 @@ def cpu_baseline(threads, ctx):
     many = timed(threads, 32, 4)
     return {"value": many["tok_s"], "unit": "tok/s", "cores": threads, "kind": "port",
             "nproc": nproc, "context": ctx,
+            "extrapolated": f"from {layers} of {L} layers (per-layer time x {L} + the full lm_head)",
             "single_thread": one, "all_cores": many,
             "sample": f"C oracle engine (oracle/oracle.c oref_engine_step + oref_engine_logits), "
                       f"{layers} of 48 layers with {ctx} cached positions, scaled to 48 layers; "
@@ -827,6 +837,12 @@ def main():
                     help="launch the step's kernels directly instead of replaying the hipGraph "
                          "(for profilers that cannot follow graph capture)")
     ap.add_argument("--cpu-threads", type=int, default=host_cores()[1])
+    ap.add_argument("--persistent", action="store_true",
+                    help="decode: time the persistent form (every layer in one launch) instead of the "
+                         "default six-launch chain")
+    ap.add_argument("--no-other", action="store_true",
+                    help="decode: skip timing the other form beside the headline")
+    ap.add_argument("--other-steps", type=int, default=32)
     ap.add_argument("--workload", choices=["decode", "gemv", "paged", "moe", "serve", "prefill", "kvio", "schedule"],
                     default="decode",
                     help="decode: the bs=1 decode step (configuration 4, the headline line); "
@@ -894,8 +910,9 @@ def main():
     max_pos = om.round_max_pos(total)
     model = build_model(om, max_pos)
     g = model["graph"]
+    persistent = g.set_persistent(args.persistent)
     if args.eager:
-        g.set_flush_each(2)
+        g.set_flush_each(3 if persistent else 2)
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, V, args.prompt).tolist()
     pos = 0
@@ -921,54 +938,107 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
 
-    # Per-kernel timing on further decode steps, two ways:
-    # (1) graph: the replayed graph with an event-record node before the first kernel and after
-    #     every kernel, so each kernel's span is its share of the replayed token (its launch gap
-    #     included); the event nodes' own cost is the stamped token time minus the plain one,
-    #     spread over the nodes, and is subtracted;
-    # (2) dispatch: direct launches, each timed by its own dispatch (the kernel's own start and
-    #     end, what a kernel-trace profiler reports), used for the per-kernel GB/s and roofline.
-    n_launch_tok = len(LAYER_KINDS) * L + 1
+    # Where the time goes, on further (untimed) decode steps:
+    # (1) dispatch durations of the timed form's launches, each timed by its own dispatch
+    #     (hipExtLaunchKernel events on the library stream; the same launches made directly):
+    #     the roofline of the dominant launch and per-kind GB/s;
+    # (2) the chain's graph spans per kind: its replayed graph with an event-record node before the
+    #     first kernel and after every kernel (each kernel's share of the replayed token, its launch
+    #     gap included; the event nodes' own cost is subtracted);
+    # (3) the other form of the same step: tok/s, and for the persistent form its own stage stamps
+    #     (the GPU's constant clock at the end of each stage of each layer).
     stamp_tokens = 8
+    ctx_mid = pos + stamp_tokens
+    margins = []
 
-    def kind_of(i):
-        return LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head"
+    def top2(lg):
+        t2 = np.sort(lg)[-2:]
+        margins.append(float(t2[1] - t2[0]))
 
-    ctx_mid = pos + stamp_tokens // 2
-    graph_ns, dispatch_ns, stamped_tok = {}, {}, []
+    def kind_names(n):
+        if persistent:
+            return ["decode_layers", "lm_head"]
+        return [LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head" for i in range(n)]
+
+    dispatch = {}
     g.set_stamps(True)
+    g.set_flush_each(3 if persistent else 2)
     for _ in range(stamp_tokens):
         tok, _ = g.token_id(tok, pos)
         pos += 1
-        st_, _ = g.stamps()
-        stamped_tok.append(float(st_[-1]))
+        top2(g.read(logits=True)[2])
         ns = g.kernel_ns()
-        assert len(ns) == n_launch_tok, len(ns)
-        for i, dt in enumerate(ns):
-            graph_ns.setdefault(kind_of(i), []).append(int(dt))
-    g.set_flush_each(2)
-    for _ in range(stamp_tokens):
+        for n_, dt in zip(kind_names(len(ns)), ns):
+            dispatch.setdefault(n_, []).append(int(dt))
+    g.set_flush_each(0)
+    layer_bytes = sum(algorithmic_bytes(k, ctx_mid) for k in LAYER_KINDS)
+    kernels = {}
+    for name, ds in dispatch.items():
+        n_launch = len(ds) // stamp_tokens
+        d_us = float(np.mean(ds)) / 1e3
+        b = L * layer_bytes if name == "decode_layers" else algorithmic_bytes(name, ctx_mid)
+        kernels[name] = dict(launches_per_token=n_launch, dispatch_us=round(d_us, 3),
+                             dispatch_us_per_token=round(d_us * n_launch, 2),
+                             algorithmic_bytes=b, dispatch_gbs=round(b / (d_us * 1e3), 1))
+    spans = {}
+    g.set_persistent(False)
+    for _ in range(4):
         tok, _ = g.token_id(tok, pos)
         pos += 1
+        top2(g.read(logits=True)[2])
+        st_, _ = g.stamps()
         for i, dt in enumerate(g.kernel_ns()):
-            dispatch_ns.setdefault(kind_of(i), []).append(int(dt))
-    g.set_flush_each(0)
+            k = LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head"
+            spans.setdefault(k, []).append(int(dt))
+        spans.setdefault("_token", []).append(int(st_[-1]))
     g.set_stamps(False)
-    event_node_ns = max(0.0, (float(np.mean(stamped_tok)) - ms_per_step * 1e6) / (n_launch_tok + 1))
-    kernels = {}
-    for name, ds in graph_ns.items():
-        n_launch = len(ds) // stamp_tokens
-        g_us = max(0.0, float(np.mean(ds)) - event_node_ns) / 1e3
-        d_us = float(np.mean(dispatch_ns[name])) / 1e3
-        b = algorithmic_bytes(name, ctx_mid)
-        kernels[name] = dict(launches_per_token=n_launch, graph_us=round(g_us, 3),
-                             graph_us_per_token=round(g_us * n_launch, 2), dispatch_us=round(d_us, 3),
-                             algorithmic_bytes=b, dispatch_gbs=round(b / (d_us * 1e3), 1))
-    dom = max(kernels, key=lambda k: kernels[k]["graph_us_per_token"])
+    dom = max(kernels, key=lambda k: kernels[k]["dispatch_us_per_token"])
     dk = kernels[dom]
     achieved = dk["algorithmic_bytes"] / (dk["dispatch_us"] * 1e3)
-    step_bytes = sum(algorithmic_bytes(k, ctx_mid) * v["launches_per_token"]
-                     for k, v in kernels.items())
+    step_bytes = L * layer_bytes + algorithmic_bytes("lm_head", ctx_mid)
+    # (3) the other form
+    other = None
+    if not args.no_other:
+        want_p = not persistent
+        got_p = g.set_persistent(want_p)
+        if got_p == want_p:
+            for _ in range(4):
+                tok, _ = g.token_id(tok, pos)
+                pos += 1
+            om.sync()
+            t1 = time.perf_counter()
+            for _ in range(args.other_steps):
+                tok, _ = g.token_id(tok, pos)
+                pos += 1
+            om.sync()
+            o_ms = (time.perf_counter() - t1) * 1e3 / args.other_steps
+            other = {"form": "persistent" if got_p else "chain", "tok_s": round(1e3 / o_ms, 2),
+                     "ms_per_step": round(o_ms, 4),
+                     "step_roofline_frac": round(step_bytes / (o_ms * 1e6) / PEAK_GBS, 4)}
+        g.set_persistent(persistent)
+    # the chain's spans less the event-record nodes' own cost (the stamped token's time beyond the
+    # plain chain token's, spread over its nodes)
+    chain_ms = ms_per_step if not persistent else (other["ms_per_step"] if other else None)
+    ev_ns = 0.0
+    if chain_ms:
+        ev_ns = max(0.0, float(np.mean(spans["_token"])) - chain_ms * 1e6) / (len(LAYER_KINDS) * L + 2)
+    chain_graph_us = {k: round(max(0.0, float(np.mean(v)) - ev_ns) / 1e3, 3)
+                      for k, v in spans.items() if k != "_token"}
+    stage_us = None
+    if g.set_persistent(True):
+        g.set_stage_stamps(True)
+        sts = []
+        for _ in range(4):
+            tok, _ = g.token_id(tok, pos)
+            pos += 1
+            ends = g.stage_ns().astype(np.int64).reshape(-1)
+            sts.append((ends - np.concatenate([[0], ends[:-1]])).reshape(L, 5))
+        g.set_stage_stamps(False)
+        st_all = np.stack(sts)
+        per = st_all[:, 1:, :].mean(axis=(0, 1)) / 1e3  # layer 0 also holds the launch's start
+        stage_us = {n: round(float(v), 3) for n, v in zip(["input", "qkv_attn", "o_proj", "route", "moe"], per)}
+        stage_us["layer"] = round(float(per.sum()), 3)
+    g.set_persistent(persistent)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_threads, ctx_mid)
     line = {
@@ -988,6 +1058,7 @@ def main():
         "config": {
             "workload": "Qwen3-30B-A3B FP8 decode step, bs=1, "
                         + ("direct kernel launches" if args.eager else "one hipGraph per token")
+                        + (" (every layer in one persistent launch)" if persistent else " (six launches per layer)")
                         + f", {args.prompt}-token prompt then greedy decode",
             "layers": L, "hidden": H, "q_heads": QH, "kv_heads": KVH, "head_dim": HD,
             "experts": E, "top_k": TOPK, "moe_intermediate": I, "vocab": V,
@@ -1008,11 +1079,17 @@ def main():
             "algorithmic_bytes_per_token": step_bytes,
             "achieved_GBs": round(step_bytes / (ms_per_step * 1e6), 1),
             "frac": round(step_bytes / (ms_per_step * 1e6) / PEAK_GBS, 4),
-            "graph_us_per_token": round(sum(v["graph_us_per_token"] for v in kernels.values()), 1),
-            "event_node_us": round(event_node_ns / 1e3, 3),
-            "launches_per_token": n_launch_tok,
+            "launches_per_token": 2 if persistent else len(LAYER_KINDS) * L + 1,
+            "form": "persistent (every layer in one launch) + lm_head" if persistent
+                    else "chain of six launches per layer + lm_head",
+            "chain_graph_span_us": chain_graph_us,
         },
         "kernels": kernels,
+        "other_form": other,
+        "persistent_stage_us_per_layer": stage_us,
+        "top2_margins": {"tokens": len(margins), "min": round(min(margins), 5),
+                         "median": round(float(np.median(margins)), 5),
+                         "values": [round(m_, 5) for m_ in margins]},
         "cpu_baseline": cpu,
         "extra": {"model_build_s": round(model["seconds"], 1),
                   "prompt_s": round(t_prompt, 2),

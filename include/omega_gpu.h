@@ -656,6 +656,20 @@ int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns,
  * oracle past a routing near-tie. */
 #define OMEGA_GPU_DGRAPH_RANK 0xFFFFFFFFu
 int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint32_t *ids);
+/* The decode graph's form (not in the reference ABI; the one-submission contract of
+ * crates/aien-omega-dgraph/src/lib.rs:16-30 holds either way). on = 0 (the default): the chain of
+ * six launches per layer; on = 1, where the device holds all 256 workgroups at once: each token's
+ * graph is one persistent launch of every layer plus the lm_head launch. Both compute every value
+ * the same way and give the same bits. Stamps run the chain; flush_each 3 runs the persistent
+ * form as direct launches. Returns the form in use after the call: 1 persistent, 0 chain. */
+int omega_gpu_decode_graph_set_persistent(OmegaGpuDecodeGraph *g, int on);
+/* Stage stamps of the persistent form (not in the reference ABI): with on, each token records
+ * on the GPU's constant clock, per layer, the end of its 5 stages — input row in every
+ * workgroup, attention row, residual after the attention, route inputs (logits and x'), down
+ * rows — as ns since the launch started. stage_ns copies the last token's layers * 5 values
+ * into ns; returns their count or rc < 0 (BAD_ARGS when the last token kept none). */
+void omega_gpu_decode_graph_set_stage_stamps(OmegaGpuDecodeGraph *g, int on);
+int omega_gpu_decode_graph_stage_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns, uint32_t cap);
 /* Batched MoE block (not in the reference ABI; the expert FFN of a decode step at token batch
  * T <= 64, the reference's per-token FP8 arm qwen3_moe_omega.rs:4287-4318 batched): for each of
  * `tokens` rows of h [T][2048] f32, RMSNorm with the router's layer weights, router logits, top-8
