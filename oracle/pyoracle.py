@@ -478,8 +478,16 @@ def fake_quant(x):
     return x
 
 
+def bf16_round(x):
+    """oref_bf16_round_row (fake_quant.rs bf16_round_row): each value rounded to bf16 (RNE), kept
+    as f32."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().oref_bf16_round_row(ptr(x), x.size)
+    return x
+
+
 def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, forced=None,
-                 forced_qkv=None, forced_att=None):
+                 forced_qkv=None, forced_att=None, w8a8: bool = True):
     """The whole-prompt prefill's arithmetic (qwen3_moe_omega_prefill.rs:483-760, W8A8: every
     GEMM input row fake-quantised per 128-block, the SwiGLU act rounded to bf16 first), layer by
     layer over the prompt: input RMSNorm, q|k|v, the decode attention of each token at its
@@ -493,9 +501,11 @@ def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, 
     flips one now and then), and `forced_att` (per layer [T][4096]) replaces the
     attention rows that enter the o projection (the W8A8 quantiser maps an f32 rounding difference
     of its input to a whole e4m3 step now and then), while the oracle's own attention rows are
-    still returned for comparison."""
+    still returned for comparison. With w8a8 False every quantiser is the identity (the OFF
+    path's f32 activations)."""
     c = model.cfg
     eps = c.eps
+    fq = fake_quant if w8a8 else (lambda v: np.asarray(v, dtype=np.float32))
     if cache is None:
         cache = Dattn(c.layers, max_pos, c.rope_theta)
         for l in range(c.layers):
@@ -514,14 +524,14 @@ def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, 
         gate, in_norm, post_norm = model.tensor(l, 4), model.tensor(l, 5), model.tensor(l, 6)
         qkvs, atts = [], []
         for t in range(T):
-            xn = fake_quant(rmsnorm(x[t], in_norm, eps))
+            xn = fq(rmsnorm(x[t], in_norm, eps))
             qkv = dequant_matvec(qw[0], qs[0], xn)
             q_in = qkv if forced_qkv is None else np.asarray(forced_qkv[l][t], dtype=np.float32)
             att = cache.attend(l, pos0 + t, q_in, eps)
             qkvs.append(qkv)
             atts.append(att)
             a_in = att if forced_att is None else np.asarray(forced_att[l][t], dtype=np.float32)
-            x[t] = x[t] + dequant_matvec(ow[0], os_[0], fake_quant(a_in))
+            x[t] = x[t] + dequant_matvec(ow[0], os_[0], fq(a_in))
         out["qkv"].append(np.stack(qkvs))
         out["att"].append(np.stack(atts))
         out["x_mid"].append(x.copy())
@@ -531,7 +541,7 @@ def prefill_w8a8(model, tokens, pos0: int = 0, cache=None, max_pos: int = 4096, 
         ids = plan["topk_experts"].reshape(T, c.top_k)
         wts = plan["topk_weights"].reshape(T, c.top_k)
         for t in range(T):
-            x[t] = x[t] + moe_block(gw, gs, dw, ds, ids[t], wts[t], posts[t], w8a8=True)
+            x[t] = x[t] + moe_block(gw, gs, dw, ds, ids[t], wts[t], posts[t], w8a8=w8a8)
         out["x_out"].append(x.copy())
         out["logits"].append(logits)
         out["ids"].append(ids.copy())
