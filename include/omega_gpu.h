@@ -739,7 +739,11 @@ int omega_gpu_sync(void);
 }
 #endif
 
-#ifdef __cplusplus
+/* layout checks for C++ and C11 consumers alike */
+#if defined(__cplusplus) || (defined(__STDC_VERSION__) && __STDC_VERSION__ >= 201112L)
+#ifndef __cplusplus
+#include <assert.h>
+#endif
 static_assert(sizeof(OmegaGpuMem) == 40, "OmegaGpuMem");
 static_assert(offsetof(OmegaGpuMem, va) == 24, "OmegaGpuMem.va");
 static_assert(sizeof(OmegaGpuPfTile) == 32, "OMEGA_QG_TILE_BYTES");

@@ -2,6 +2,8 @@
 declares (the shared library for dlopen / ctypes users and the static archive the reference's
 crates link with -lomega_gpu), the struct mirrors have the byte layouts the header asserts, and
 the checks that run before any device work refuse bad arguments with the reference's codes.
+A C program built by gcc against the header and linked to the static archive the way the
+crates link it (no hipcc) runs without a GPU: every hot entry answers CHIP_FAIL with a message.
 
 Reference: crates/*/build.rs detect the archive by `nm` lines ending " T <symbol>"
 (crates/aien-omega-fp8/build.rs:51-70, router/build.rs:45-52, dattn/build.rs:45-47,
@@ -52,6 +54,27 @@ def test_every_declared_symbol_is_exported(name):
     assert os.path.exists(path), "build first: python -c 'import __graft_entry__ as g; g.build()'"
     missing = [s for s in declared_symbols() if s not in exported(path)]
     assert not missing, missing
+
+
+ROCM_LIB = "/opt/rocm/lib"
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="this host has a GPU driver")
+def test_static_archive_links_from_c_and_answers_chip_fail_without_a_gpu(tmp_path):
+    archive = os.path.join(BUILD, "libomega_gpu.a")
+    assert os.path.exists(archive), "build first: python -c 'import __graft_entry__ as g; g.build()'"
+    exe = str(tmp_path / "static_link_driver")
+    # the reference's build.rs link line: -lomega_gpu, the HIP runtime, -lstdc++ -lpthread -lm
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-I", os.path.dirname(HEADER),
+                    os.path.join(REPO, "tests", "c", "static_link_driver.c"), archive,
+                    "-L" + ROCM_LIB, "-Wl,-rpath," + ROCM_LIB, "-lamdhip64", "-lstdc++",
+                    "-lpthread", "-lm", "-o", exe], check=True, capture_output=True, text=True)
+    run = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    lines = run.stdout.splitlines()
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert lines[-1] == "0 failed"
+    chip = [ln for ln in lines if "(CHIP_FAIL)" in ln]
+    assert len(chip) == 7 and all(ln.startswith("ok ") and "no HIP device" in ln for ln in chip), lines
 
 
 def test_library_loads_without_a_gpu_and_mirrors_match_the_header():
