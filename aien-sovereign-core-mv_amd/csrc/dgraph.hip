@@ -61,7 +61,8 @@ struct GateUpArgs {
     uint32_t *log_ids = nullptr;
     float *log_w = nullptr;
     const uint32_t *forced = nullptr;  // parity tests: the layer's 8 expert ids instead of the ranking
-    int graph_mutant = 0;        // 1: gate and up swapped
+    int graph_mutant = 0;        // 1: gate and up swapped; 4: every routed id e computed and
+                                 // reported as (e + 1) % 128; 5: expert block scales read as 1
 };
 
 constexpr uint32_t kGuPairs = 2;  // gate/up row pairs per wavefront
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
         if (lane == 0) {
 #pragma unroll
             for (int s = 0; s < kTopK; ++s) {
-                sh_id[s] = r.id[s];
+                sh_id[s] = a.graph_mutant == 4 ? (r.id[s] + 1) % kExperts : r.id[s];
                 sh_w[s] = r.w[s];
             }
         }
@@ -103,8 +104,9 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     const float *se = a.s + (size_t)e * (2 * kInter / 128) * (kHidden / 128);
     // block scales ahead of the weight stream: waits complete in issue order
     float scg[P], scu[P];
-    S::load_scales(se + (size_t)(j0 >> 7) * (kHidden / 128), lane, 1.0f, 0, scg);
-    S::load_scales(se + (size_t)((kInter + j0) >> 7) * (kHidden / 128), lane, 1.0f, 0, scu);
+    const int scale_mutant = a.graph_mutant == 5 ? 1 : 0;
+    S::load_scales(se + (size_t)(j0 >> 7) * (kHidden / 128), lane, 1.0f, scale_mutant, scg);
+    S::load_scales(se + (size_t)((kInter + j0) >> 7) * (kHidden / 128), lane, 1.0f, scale_mutant, scu);
     S gate, up;
     gate.load(we + (size_t)j0 * kHidden, lane);
     up.load(we + (size_t)(kInter + j0) * kHidden, lane);
@@ -150,7 +152,7 @@ struct DownArgs {
     const float *act = nullptr;  // [8][768]
     const float *xin = nullptr;  // residual read [2048] (null: the combine alone is written)
     float *x = nullptr;          // out [2048]: xin + the combine (the decode step: xin == x)
-    int graph_mutant = 0;        // 2: slot 7 dropped from the combine
+    int graph_mutant = 0;        // 2: slot 7 dropped from the combine; 5: block scales read as 1
 };
 
 constexpr uint32_t kDnRows = 8;  // output rows per workgroup (one wavefront per slot)
@@ -172,7 +174,8 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
     const float wraw = *as_global_f32(a.weights + (lane & (kTopK - 1)));  // lane s: slot s's weight
     const float xres = a.xin ? *as_global_f32(a.xin + row0 + (lane & (kDnRows - 1))) : 0.f;
     float sc[P];
-    S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f, 0, sc);
+    S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f,
+                   graph_mutant == 5 ? 1 : 0, sc);
     S slab;
     slab.load(a.w + ((size_t)e * kHidden + row0) * kInter, lane);
     __builtin_amdgcn_sched_barrier(0);
@@ -306,9 +309,27 @@ struct OmegaGpuDecodeGraph {
     std::vector<hipEvent_t> events;   // one before the first launch, one after each launch
     std::vector<hipEvent_t> kevents;  // start / stop pair per launch, recorded by the dispatch
     bool stamps_valid = false;
+    // test-only layer trace: the traced layers and one record of kTrWords floats per layer
+    std::vector<uint32_t> trace_layers;
+    float *trace = nullptr;
 };
 
 namespace {
+
+// one traced layer's record: the residual entering the layer, the o projection's output, the
+// residual after the attention (x'), the router's normed row, the MoE output (no residual), the
+// residual leaving the layer, then the routed ids (u32) and weights in slot order
+constexpr size_t kTrX = 0, kTrAttn = 2048, kTrMid = 4096, kTrPost = 6144, kTrMoe = 8192,
+                 kTrOut = 10240, kTrIds = 12288, kTrW = 12296, kTrWords = 12304;
+constexpr uint32_t kTrMaxLayers = 8;
+
+// the trace record of layer l, or null (not traced, or a graph is being recorded)
+float *trace_record(const OmegaGpuDecodeGraph *g, uint32_t l) {
+    if (!g->trace || graph_recorder()) return nullptr;
+    for (size_t i = 0; i < g->trace_layers.size(); ++i)
+        if (g->trace_layers[i] == l) return g->trace + i * kTrWords;
+    return nullptr;
+}
 
 // Enqueues one token's kernels on `st`. With `ev` (stamps), records an event before the first
 // launch and after each one.
@@ -365,9 +386,14 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
             a.embed_rows = g->embed->n;
             a.x_out = g->x;
         }
+        float *tr = trace_record(g, l);
+        auto trace_copy = [&](size_t at, const void *src, size_t bytes) -> hipError_t {
+            return hipMemcpyAsync(tr + at, src, bytes, hipMemcpyDeviceToDevice, st);
+        };
         arm();
         OMEGA_HIP(F_SESSION, launch_fp8_rows(a, EPI_STORE, xsrc, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_QKV));
+        if (tr) OMEGA_HIP(F_SESSION, trace_copy(kTrX, g->x, kHidden * 4));
         // 2. attention (q/k norm + RoPE, K/V append) with the split merge in the same launch
         DattnArgs da = cache_dattn(g->cache, l, eps, g->qkv, g->part);
         da.splits = kGraphSplits;
@@ -392,11 +418,19 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         arm();
         OMEGA_HIP(F_SESSION, launch_fp8_rows(o, EPI_RESID, XS_F32, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_O_PROJ));
+        if (tr) {
+            // the same launch shape stored on its own: the o projection's output as added
+            Fp8RowsArgs o2 = o;
+            o2.y = tr + kTrAttn;
+            OMEGA_HIP(F_SESSION, launch_fp8_rows(o2, EPI_STORE, XS_F32, st));
+            OMEGA_HIP(F_SESSION, trace_copy(kTrMid, g->x, kHidden * 4));
+        }
         // 5. router logits and x'
         RouterArgs ra = router_args(g->router, l, g->x, eps, g->cfg.norm_topk, 1.0f);
         arm();
         OMEGA_HIP(F_SESSION, launch_router_logits(ra, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ROUTER));
+        if (tr) OMEGA_HIP(F_SESSION, trace_copy(kTrPost, ra.xout, kHidden * 4));
         // 6. ranking + gate|up of the 8 routed experts + SwiGLU
         GateUpArgs gu;
         gu.w = L.gu->w;
@@ -434,6 +468,17 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
         OMEGA_HIP(F_SESSION, hipGetLastError());
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_DOWN));
+        if (tr) {
+            // the combine alone (no residual read) is the sum the fused launch added
+            DownArgs d2 = dn;
+            d2.xin = nullptr;
+            d2.x = tr + kTrMoe;
+            OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, d2);
+            OMEGA_HIP(F_SESSION, hipGetLastError());
+            OMEGA_HIP(F_SESSION, trace_copy(kTrIds, ra.ids, kTopK * 4));
+            OMEGA_HIP(F_SESSION, trace_copy(kTrW, ra.weights, kTopK * 4));
+            OMEGA_HIP(F_SESSION, trace_copy(kTrOut, g->x, kHidden * 4));
+        }
     }
     // final norm + lm_head + argmax
     Bf16RowsArgs b;
@@ -731,7 +776,7 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
     for (hipEvent_t e : g->kevents) (void)hipEventDestroy(e);
     void *ps[] = {g->x, g->qkv, g->attn, g->part, g->act, g->hidden, g->logits, g->io,
                   g->final_norm, g->route_log, g->route_log_w, g->forced, g->flags,
-                  g->players, g->words, g->pflags, g->pstamps};
+                  g->players, g->words, g->pflags, g->pstamps, g->trace};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     for (auto &L : g->layers)
@@ -808,14 +853,16 @@ int run_token(OmegaGpuDecodeGraph *g, const float *x_embed, uint32_t token_in, u
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     // graph variant: x from the host or by token id; stamped (event nodes between kernels) or not;
     // the persistent form unless stamps or direct launches ask for the chain
-    const bool pers = g->persistent && ((!g->stamps && g->flush_each == 0) || g->flush_each == 3);
+    // a layer trace runs the chain as direct launches
+    const bool tracing = g->trace != nullptr;
+    const bool pers = g->persistent && !tracing && ((!g->stamps && g->flush_each == 0) || g->flush_each == 3);
     const int v = pers ? 4 + (x_embed ? 0 : 1) : (x_embed ? 0 : 1) + (g->stamps ? 2 : 0);
     g->stamps_valid = false;
     g->stage_valid = false;
     uint64_t record_ns = 0;
     // flush_each runs the same kernels as direct launches (with stamps: events between them and
     // each launch timed by its dispatch); otherwise the graph is replayed
-    const bool eager = g->flush_each != 0;
+    const bool eager = g->flush_each != 0 || tracing;
     if (!eager && (g->dirty_v[v] || !g->exec_v[v])) {
         const uint64_t r0 = now_ns();
         int rc = rebuild(g, c, v);
@@ -978,6 +1025,62 @@ void omega_gpu_decode_graph_set_flush_each(OmegaGpuDecodeGraph *g, int on) {
     // 3: the persistent form as direct launches (each dispatch timed in stamp mode); the chain
     // where the persistent form is off
     g->flush_each = on == 2 ? 2 : on == 3 ? (g->persistent ? 3 : 2) : (on != 0 ? 1 : 0);
+}
+
+int omega_gpu_decode_graph_test_set_trace(OmegaGpuDecodeGraph *g, const uint32_t *layers, uint32_t n) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g || (n && !layers) || n > kTrMaxLayers) {
+        set_error(F_SESSION, "decode graph trace: a graph and at most %u layers", kTrMaxLayers);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        bool repeat = false;
+        for (uint32_t j = 0; j < i; ++j) repeat |= layers[j] == layers[i];
+        if (layers[i] >= g->cfg.layers || repeat) {
+            set_error(F_SESSION, "decode graph trace: layer %u outside 0..%u or repeated", layers[i],
+                      g->cfg.layers - 1);
+            return OMEGA_GPU_BAD_ARGS;
+        }
+    }
+    Ctx *c = ctx(F_SESSION);
+    if (!c) return OMEGA_GPU_CHIP_FAIL;
+    OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
+    if (g->trace) OMEGA_HIP(F_SESSION, hipFree(g->trace));
+    g->trace = nullptr;
+    g->trace_layers.assign(layers, layers + n);
+    if (n) {
+        OMEGA_HIP(F_SESSION, hipMalloc(&g->trace, (size_t)n * kTrWords * 4));
+        OMEGA_HIP(F_SESSION, hipMemset(g->trace, 0, (size_t)n * kTrWords * 4));
+    }
+    return OMEGA_GPU_OK;
+}
+
+int omega_gpu_decode_graph_test_read_trace(OmegaGpuDecodeGraph *g, uint32_t i, float *x_in,
+                                           float *attn_proj, float *x_mid, float *post,
+                                           uint32_t *experts, float *weights, float *moe_out,
+                                           float *x_out) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    clear_error(F_SESSION);
+    if (!g || !g->trace || i >= g->trace_layers.size()) {
+        set_error(F_SESSION, "decode graph trace read: no trace record %u", i);
+        return OMEGA_GPU_BAD_ARGS;
+    }
+    Ctx *c = ctx(F_SESSION);
+    if (!c) return OMEGA_GPU_CHIP_FAIL;
+    std::vector<float> rec(kTrWords);
+    OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
+    OMEGA_HIP(F_SESSION, hipMemcpy(rec.data(), g->trace + (size_t)i * kTrWords, kTrWords * 4,
+                                   hipMemcpyDeviceToHost));
+    const struct {
+        void *dst;
+        size_t at, n;
+    } parts[] = {{x_in, kTrX, kHidden},     {attn_proj, kTrAttn, kHidden}, {x_mid, kTrMid, kHidden},
+                 {post, kTrPost, kHidden},  {moe_out, kTrMoe, kHidden},    {x_out, kTrOut, kHidden},
+                 {experts, kTrIds, kTopK},  {weights, kTrW, kTopK}};
+    for (const auto &p : parts)
+        if (p.dst) memcpy(p.dst, rec.data() + p.at, p.n * 4);
+    return OMEGA_GPU_OK;
 }
 
 void omega_gpu_decode_graph_test_set_mutant(OmegaGpuDecodeGraph *g, int mutant) {

@@ -267,6 +267,8 @@ SIGNATURES = {
     "omega_gpu_pf_moe_plan": (i32, [u32, u32, u32, P, P, P, P, P, P, P]),
     "omega_gpu_decode_graph_read_routes": (i32, [P, P, P]),
     "omega_gpu_decode_graph_test_force_routes": (i32, [P, P]),
+    "omega_gpu_decode_graph_test_set_trace": (i32, [P, P, u32]),
+    "omega_gpu_decode_graph_test_read_trace": (i32, [P, u32, P, P, P, P, P, P, P, P]),
     "omega_gpu_decode_graph_kernel_ns": (i32, [P, U64P, u32]),
     "omega_gpu_decode_graph_set_persistent": (i32, [P, i32]),
     "omega_gpu_decode_graph_set_stage_stamps": (None, [P, i32]),
@@ -778,6 +780,27 @@ class DecodeGraph:
         a = np.ascontiguousarray(ids, dtype=np.uint32)
         check_len("decode graph forced routes", self.layers * 8, a.size)
         self._rc(lib().omega_gpu_decode_graph_test_force_routes(self.h, ptr(a)), "force_routes")
+
+    def set_trace(self, layers):
+        """Layer trace for parity tests: the following tokens run the chain as direct launches
+        and record each listed layer's rows (at most 8 layers); None or [] turns it off."""
+        a = np.ascontiguousarray(list(layers or []), dtype=np.uint32)
+        self._rc(lib().omega_gpu_decode_graph_test_set_trace(self.h, ptr(a) if a.size else None,
+                                                             a.size), "set_trace")
+
+    def read_trace(self, i):
+        """The last token's record of the i-th traced layer: a dict of x_in, attn_proj, x_mid
+        (the residual after the attention), post (the router's normed row), experts, weights,
+        moe_out and x_out."""
+        rows = {k: np.empty(DGRAPH_HIDDEN, np.float32)
+                for k in ("x_in", "attn_proj", "x_mid", "post", "moe_out", "x_out")}
+        rows["experts"] = np.empty(8, np.uint32)
+        rows["weights"] = np.empty(8, np.float32)
+        self._rc(lib().omega_gpu_decode_graph_test_read_trace(
+            self.h, i, ptr(rows["x_in"]), ptr(rows["attn_proj"]), ptr(rows["x_mid"]),
+            ptr(rows["post"]), ptr(rows["experts"]), ptr(rows["weights"]), ptr(rows["moe_out"]),
+            ptr(rows["x_out"])), "read_trace")
+        return rows
 
     def set_stamps(self, on):
         lib().omega_gpu_decode_graph_set_stamps(self.h, int(on))

@@ -296,7 +296,11 @@ int omega_gpu_decode_graph_read(OmegaGpuDecodeGraph *g, float *x, float *hidden,
  * directly without the graph and without waits */
 void omega_gpu_decode_graph_set_flush_each(OmegaGpuDecodeGraph *g, int on);
 /* :469-480: 0 off; 1 SwiGLU reads the wrong half; 2 combine skips expert 7; 3 attention written
- * at scale 1 (TEST ONLY) */
+ * at scale 2; extensions, on the chain form: 4 every routed expert e computed and reported as
+ * (e + 1) % 128 (the engine's routing_mutant, qwen3_moe_omega.rs:3604-3608, a control of
+ * own30b_check.rs:690-712); 5 the experts' FP8 block scales read as 1 (its scales-dropped
+ * control, FP8 kernel mutant 1); on both forms: 9 every in-launch wait gives up at once
+ * (TEST ONLY) */
 void omega_gpu_decode_graph_test_set_mutant(OmegaGpuDecodeGraph *g, int mutant); /* :153 */
 void omega_gpu_decode_graph_set_stamps(OmegaGpuDecodeGraph *g, int on);      /* :154 */
 /* :155-160: launches + 1 GPU timestamps (ns) and one kind per launch; returns launches or rc<0 */
@@ -656,6 +660,19 @@ int omega_gpu_decode_graph_kernel_ns(const OmegaGpuDecodeGraph *g, uint64_t *ns,
  * oracle past a routing near-tie. */
 #define OMEGA_GPU_DGRAPH_RANK 0xFFFFFFFFu
 int omega_gpu_decode_graph_test_force_routes(OmegaGpuDecodeGraph *g, const uint32_t *ids);
+/* Layer trace for parity tests (not in the reference ABI; the engine's trace_layers and
+ * LayerTrace, qwen3_moe_omega.rs:3227-3243, read by own30b_check.rs:632-700): with n layers
+ * (<= 8, distinct) every following token runs the chain form as direct launches and records, per
+ * traced layer, the residual row entering it, the o projection's output, the residual after the
+ * attention (x'), the router's normed row, the routed ids and weights in slot order, the MoE
+ * output (the slot-order combine, no residual) and the residual leaving it. n = 0 turns the trace
+ * off. read_trace copies the last token's record of the i-th traced layer; any pointer may be
+ * NULL ([2048] floats each, ids and weights [8]). */
+int omega_gpu_decode_graph_test_set_trace(OmegaGpuDecodeGraph *g, const uint32_t *layers, uint32_t n);
+int omega_gpu_decode_graph_test_read_trace(OmegaGpuDecodeGraph *g, uint32_t i, float *x_in,
+                                           float *attn_proj, float *x_mid, float *post,
+                                           uint32_t *experts, float *weights, float *moe_out,
+                                           float *x_out);
 /* The decode graph's form (not in the reference ABI; the one-submission contract of
  * crates/aien-omega-dgraph/src/lib.rs:16-30 holds either way). on = 0 (the default): the chain of
  * six launches per layer; on = 1, where the device holds all 256 workgroups at once: each token's

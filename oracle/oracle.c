@@ -804,8 +804,16 @@ struct oref_model {
 /* tensor ids of the generator: one per (layer, kind) plus the model-wide ones */
 static uint64_t tid(int layer, int kind) { return 1000ull + (uint64_t)layer * 16 + (uint64_t)kind; }
 
+oref_model *oref_model_synth_layers(const oref_config *c, uint64_t seed, float sigma,
+                                    float norm_sigma, int threads, const int *layer_ids);
+
 oref_model *oref_model_synth(const oref_config *c, uint64_t seed, float sigma, float norm_sigma,
                              int threads) {
+    return oref_model_synth_layers(c, seed, sigma, norm_sigma, threads, NULL);
+}
+
+oref_model *oref_model_synth_layers(const oref_config *c, uint64_t seed, float sigma,
+                                    float norm_sigma, int threads, const int *layer_ids) {
 #ifdef _OPENMP
     if (threads > 0) omp_set_num_threads(threads);
 #else
@@ -825,20 +833,21 @@ oref_model *oref_model_synth(const oref_config *c, uint64_t seed, float sigma, f
     m->router = calloc((size_t)L, sizeof(void *));
     int norm_len[4] = {h, h, hd, hd};
     for (int l = 0; l < L; l++) {
+        const int src = layer_ids ? layer_ids[l] : l;  /* the full model's layer this one holds */
         for (int t = 0; t < 4; t++) {
             size_t nw = (size_t)es[t] * ns[t] * ks[t];
             m->w[t][l] = malloc(nw);
             m->s[t][l] = malloc(sizeof(uint16_t) * (size_t)es[t] * (ns[t] / 128) * (ks[t] / 128));
-            oref_synth_fp8(seed, tid(l, t), es[t], ns[t], ks[t], sigma, m->w[t][l], m->s[t][l]);
+            oref_synth_fp8(seed, tid(src, t), es[t], ns[t], ks[t], sigma, m->w[t][l], m->s[t][l]);
             m->norms[t][l] = malloc(sizeof(float) * (size_t)norm_len[t]);
             /* norm weights are bf16 in the checkpoint, widened to f32 by the loader */
             uint16_t *tmp = malloc(sizeof(uint16_t) * (size_t)norm_len[t]);
-            oref_synth_bf16(seed, tid(l, 4 + t), (size_t)norm_len[t], norm_sigma, 1, tmp);
+            oref_synth_bf16(seed, tid(src, 4 + t), (size_t)norm_len[t], norm_sigma, 1, tmp);
             for (int i = 0; i < norm_len[t]; i++) m->norms[t][l][i] = oref_bf16_to_f32(tmp[i]);
             free(tmp);
         }
         m->router[l] = malloc(sizeof(uint16_t) * (size_t)c->experts * h);
-        oref_synth_bf16(seed, tid(l, 8), (size_t)c->experts * h, sigma, 0, m->router[l]);
+        oref_synth_bf16(seed, tid(src, 8), (size_t)c->experts * h, sigma, 0, m->router[l]);
     }
     m->embed = malloc(sizeof(uint16_t) * (size_t)c->vocab * h);
     m->lm_head = malloc(sizeof(uint16_t) * (size_t)c->vocab * h);

@@ -180,6 +180,12 @@ typedef struct oref_model oref_model;
  * splits the work; the values do not depend on the thread count). */
 oref_model *oref_model_synth(const oref_config *cfg, uint64_t seed, float sigma, float norm_sigma,
                              int threads);
+/* The same model's layers layer_ids[0..cfg->layers) only: layer i of the result holds exactly the
+ * tensors of layer layer_ids[i] of the model oref_model_synth makes with the same seed (the
+ * embedding, lm_head and final norm as oref_model_synth makes them at cfg->vocab). Lets a check of
+ * a few layers of a large model hold only those layers. */
+oref_model *oref_model_synth_layers(const oref_config *cfg, uint64_t seed, float sigma,
+                                    float norm_sigma, int threads, const int *layer_ids);
 void oref_model_free(oref_model *m);
 /* Raw views for upload. kind: 0 qkv, 1 o, 2 gate_up, 3 down (w and s), 4 router (bf16 in w),
  * 5 input_norm, 6 post_norm, 7 q_norm, 8 k_norm (f32 in w). Returns the pointer. */

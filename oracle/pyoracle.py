@@ -114,6 +114,7 @@ def lib():
             "oref_dattn_write_rows": (None, [P, i32, i32, i32, i32, P, P]),
             "oref_set_mutant": (None, [i32]),
             "oref_model_synth": (P, [P, u64, f32, f32, i32]),
+            "oref_model_synth_layers": (P, [P, u64, f32, f32, i32, P]),
             "oref_model_free": (None, [P]),
             "oref_model_tensor": (P, [P, i32, i32, P]),
             "oref_model_embed": (P, [P]),
@@ -591,9 +592,21 @@ class Model:
     """Synthetic random-init model and the whole-step engine of the oracle."""
 
     def __init__(self, cfg: dict, seed: int, sigma: float = 0.02, norm_sigma: float = 0.0,
-                 threads: int = 1):
+                 threads: int = 1, layer_ids=None):
+        """layer_ids: hold only those layers of the model cfg describes (cfg["layers"] is the
+        full model's count; layer i of this object is its layer layer_ids[i])."""
+        cfg = dict(cfg)
+        if layer_ids is not None:
+            ids = np.ascontiguousarray(layer_ids, dtype=np.int32)
+            if ids.size == 0 or ids.min() < 0 or ids.max() >= cfg["layers"]:
+                raise ValueError(f"layer_ids {list(ids)} outside 0..{cfg['layers'] - 1}")
+            cfg["layers"] = int(ids.size)
         self.cfg = Config(**cfg)
-        self.h = lib().oref_model_synth(C.byref(self.cfg), seed, sigma, norm_sigma, threads)
+        if layer_ids is None:
+            self.h = lib().oref_model_synth(C.byref(self.cfg), seed, sigma, norm_sigma, threads)
+        else:
+            self.h = lib().oref_model_synth_layers(C.byref(self.cfg), seed, sigma, norm_sigma,
+                                                   threads, ptr(ids))
 
     def tensor(self, layer: int, kind: int):
         """kind 0..3: (w, s) of qkv, o, gate_up, down; 4: router bf16; 5..8: norms."""

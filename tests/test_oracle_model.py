@@ -159,3 +159,24 @@ def test_rmsnorm_closed_form(oracle):
     for h in range(2):
         v = np.arange(h * 128, (h + 1) * 128, dtype=np.float64)
         assert np.abs(heads[h * 128:(h + 1) * 128] - v / np.sqrt((v ** 2).mean() + 1e-6)).max() < 1e-5
+
+
+def test_layer_subset_holds_the_full_models_layers(oracle):
+    # oref_model_synth_layers: layer i of the subset is layer ids[i] of the whole model, every
+    # tensor kind bit for bit (the full-size layer trace checks hold three of 48 layers this way)
+    cfg = dict(layers=4, hidden=256, q_heads=2, kv_heads=1, head_dim=128, experts=4, top_k=2,
+               inter=128, vocab=64, eps=1e-6, rope_theta=1e6)
+    whole = oracle.Model(cfg, 77, sigma=0.02, norm_sigma=0.1, threads=8)
+    ids = [3, 0, 2]
+    part = oracle.Model(cfg, 77, sigma=0.02, norm_sigma=0.1, threads=8, layer_ids=ids)
+    assert part.cfg.layers == 3
+    for i, l in enumerate(ids):
+        for kind in range(9):
+            a, b = part.tensor(i, kind), whole.tensor(l, kind)
+            for u, v in zip(a if kind < 4 else (a,), b if kind < 4 else (b,)):
+                np.testing.assert_array_equal(u, v)
+    # different layers really differ (the map is not the identity by accident)
+    assert not np.array_equal(part.tensor(0, 2)[0], whole.tensor(0, 2)[0])
+    np.testing.assert_array_equal(part.embed(), whole.embed())
+    with pytest.raises(ValueError):
+        oracle.Model(cfg, 77, layer_ids=[4])
