@@ -84,20 +84,20 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     if (s >= 8) return;
     // Merge of q head 8 h + s: wait until every split of kv head h has flagged this epoch (every
     // split is resident: at most 4 x 64 one-wavefront workgroups), with a bounded number of polls
-    // (a wait that runs out is counted and the merge goes on).
+    // (a wait that runs out is counted and the merge goes on; merge_spins 0, a test knob, gives up
+    // without a poll).
     {
         const uint32_t *fl = a.flags + h * kDattnSplits;
+        bool in_time = a.merge_spins != 0;
         uint32_t spins = 0;
-        while (true) {
+        while (in_time) {
             const uint32_t f = lane < active ? __hip_atomic_load(fl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                                              : epoch;
             if (__all(f == epoch)) break;
-            if (++spins >= kDattnMergeSpins) {
-                if (lane == 0) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+            if (++spins >= a.merge_spins) in_time = false;
+            else __builtin_amdgcn_s_sleep(1);
         }
+        if (!in_time && lane == 0) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint32_t hq = h * 8 + s;
     float o0, o1;
@@ -1304,6 +1304,7 @@ DattnArgs cache_dattn(OmegaGpuDecodeAttnCache *c, uint32_t layer, float eps, con
     a.tiles_per_split = knobs().dattn_per_split / kDattnPage;
     a.part = part;
     a.mutant = knobs().dattn_mutant;
+    a.merge_spins = a.mutant == 9 ? 0u : kDattnMergeSpins;  // test mutant 9: the merge gives up
     return a;
 }
 uint32_t cache_layers(const OmegaGpuDecodeAttnCache *c) { return c->layers; }

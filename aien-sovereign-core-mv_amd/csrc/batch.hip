@@ -49,7 +49,8 @@ struct BdIo {
     uint32_t tok[kBdMaxSeqs];
     uint32_t pos[kBdMaxSeqs];           // the token's position: its KV slot; context = pos + 1
     ItemPlan plan;                      // the step's attention work items
-    uint32_t moe_late[2];               // [0]: MoE planner waits that ran out this step
+    uint32_t moe_late;                  // MoE planner waits that ran out this step
+    uint32_t plan_epoch;                // the step's MoE planner epoch base (layer l: * 64 + l)
     unsigned long long argmax[kBdMaxSeqs][kArgmaxSlots];
 };
 static_assert(offsetof(BdIo, argmax) % 8 == 0, "argmax slots 8-byte aligned");
@@ -485,7 +486,7 @@ struct OmegaGpuBatchDecode {
     std::vector<uint32_t> table_pages;  // per sequence: the leading table entries that name a page
     bool keep_logits = false;
     bool eager = false;  // launch the kernels directly (profilers that cannot follow graph capture)
-    std::map<uint32_t, hipGraphExec_t> exec;  // key: seqs | keep_logits << 8
+    std::map<uint32_t, hipGraphExec_t> exec;  // key: seqs | keep_logits << 8 | MoE mutant << 9
     std::vector<hipGraph_t> graphs;
 };
 
@@ -584,7 +585,10 @@ int bd_enqueue(OmegaGpuBatchDecode *b, uint32_t T, hipStream_t st) {
         m.ids = b->route_ids + (size_t)l * kBdMaxSeqs * 8;
         m.weights = b->route_w + (size_t)l * kBdMaxSeqs * 8;
         m.mutant = knobs().moe_mutant;
-        m.errc = &b->io->moe_late[0];
+        m.errc = &b->io->moe_late;
+        m.epoch_dev = &b->io->plan_epoch;
+        m.epoch_sub = l;
+        m.plan_spins = m.mutant == 9 ? 0u : kMoePlanSpins;
         m.defer_combine = 1;  // the next layer's rows launch (or the final norm) adds the MoE rows
         OMEGA_HIP(F_SESSION, launch_moe_batch(m, st));
         a.moe_dp = m.dp;
@@ -611,12 +615,13 @@ bool fp8_is(const OmegaGpuFp8Tensor *t, uint32_t experts, uint32_t n, uint32_t k
     return t && t->experts == experts && t->n == n && t->k == k;
 }
 
-// After the step's copy back: the next tokens, or an error when a MoE planner's wait ran out (its
-// layer added nothing, so the step's logits are not the model's)
+// After the step's copy back: the next tokens, or an error when a MoE planner's wait ran out (that
+// layer's MoE rows, the step's later K/V rows and its logits are not the model's: the caller runs
+// the step again)
 int bd_finish(const BdIo *p, uint32_t seqs, uint32_t *next_tokens) {
-    if (p->moe_late[0]) {
+    if (p->moe_late) {
         set_error(F_SESSION, "batch decode step: %u MoE plans timed out waiting for their rankings",
-                  p->moe_late[0]);
+                  p->moe_late);
         return OMEGA_GPU_CHIP_FAIL;
     }
     for (uint32_t s = 0; s < seqs; ++s) next_tokens[s] = argmax_from_slots(p->argmax[s]);
@@ -876,16 +881,18 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
     plan_items(first, seqs, p->plan);
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
+    if (plan_epoch_take(F_SESSION, c->stream, &p->plan_epoch)) return OMEGA_GPU_CHIP_FAIL;
     if (b->eager) {
         OMEGA_HIP(F_SESSION, hipMemcpyAsync(b->io, p, sizeof(BdIo), hipMemcpyHostToDevice, c->stream));
         int rc = bd_enqueue(b, seqs, c->stream);
         if (rc) return rc;
-        OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->moe_late, b->io->moe_late, bd_back_bytes(seqs),
+        OMEGA_HIP(F_SESSION, hipMemcpyAsync(&p->moe_late, &b->io->moe_late, bd_back_bytes(seqs),
                                             hipMemcpyDeviceToHost, c->stream));
         OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
         return bd_finish(p, seqs, next_tokens);
     }
-    const uint32_t key = seqs | (b->keep_logits ? 256u : 0u);
+    // the recorded launches carry the MoE test mutant they were recorded with
+    const uint32_t key = seqs | (b->keep_logits ? 256u : 0u) | ((uint32_t)knobs().moe_mutant << 9);
     auto it = b->exec.find(key);
     if (it == b->exec.end()) {
         // built node by node (no stream capture)
@@ -899,7 +906,7 @@ int omega_gpu_batch_decode_step(OmegaGpuBatchDecode *b, uint32_t seqs, const uin
     }
     OMEGA_HIP(F_SESSION, hipMemcpyAsync(b->io, p, sizeof(BdIo), hipMemcpyHostToDevice, c->stream));
     OMEGA_HIP(F_SESSION, hipGraphLaunch(it->second, c->stream));
-    OMEGA_HIP(F_SESSION, hipMemcpyAsync(p->moe_late, b->io->moe_late, bd_back_bytes(seqs),
+    OMEGA_HIP(F_SESSION, hipMemcpyAsync(&p->moe_late, &b->io->moe_late, bd_back_bytes(seqs),
                                         hipMemcpyDeviceToHost, c->stream));
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
     return bd_finish(p, seqs, next_tokens);

@@ -403,6 +403,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         da.epoch_dev = &g->io->epoch;
         da.out = g->attn;
         da.out_scale = g->mutant == 3 ? 2.0f : 1.0f;
+        if (g->mutant == 9) da.merge_spins = 0;  // every merge gives up at once (counted)
         arm();
         OMEGA_HIP(F_SESSION, launch_dattn(da, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_ATTN));

@@ -136,6 +136,7 @@ __host__ __device__ inline void attn_split_plan(uint32_t tiles, uint32_t splits,
 // Fused decode attention over the cache: per (split, kv head) one wavefront prepares the 8 q
 // heads (RMSNorm, RoPE) from the raw q|k|v row, runs the matrix-core flash-decoding of its tiles
 // of the tokens before `pos`, and split 0 also appends this token's K/V and folds it in.
+constexpr uint32_t kDattnMergeSpins = 1u << 22;  // bounded wait of the split merge (seconds)
 struct DattnArgs {
     const float *qkv = nullptr;      // raw q|k|v [5120]
     uint8_t *pool = nullptr;
@@ -161,12 +162,12 @@ struct DattnArgs {
     float out_scale = 1.0f;
     int mutant = 0;  // 1: no RoPE; 2: V written one position late; 3: K/V not written; 4: maxima ignored
     uint32_t splits = kDattnSplits;  // split workgroups per kv head (the launch's grid y, <= kDattnSplits)
+    uint32_t merge_spins = kDattnMergeSpins;  // the merge's bounded wait; 0: gives up at once (counted)
 };
 // The decode graph cuts a kv head's pages into at most this many splits in both of its forms (the
 // persistent launch holds two splits per attention workgroup), so the two forms give the same bits
 // at every position.
 constexpr uint32_t kGraphSplits = 64;
-constexpr uint32_t kDattnMergeSpins = 1u << 22;  // bounded wait of the split merge (seconds)
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st);
 
 // Paged flash-decoding over an external pool: grid (splits, kv heads, seqs), one wavefront
@@ -213,6 +214,7 @@ constexpr uint32_t kMoeMaxTokens = 64;
 // below this token count the expert projections run as grouped GEMVs on f32 activations (each
 // segment's weights held in registers across its rows); from it on, on the FP8 matrix cores
 constexpr uint32_t kMoeGemvMax = 16;
+constexpr uint32_t kMoePlanSpins = 1u << 22;  // bounded wait of the planner (seconds)
 struct MoeArgs {
     const float *h = nullptr;          // [T][2048] residual rows
     const float *norm_w = nullptr;     // post-attention RMSNorm weights [2048]
@@ -240,6 +242,13 @@ struct MoeArgs {
     float *logits = nullptr;           // [T][128]
     uint32_t *plan = nullptr;          // [0]: segments, [1]: 1 when the planner's wait ran out
     uint32_t *errc = nullptr;          // optional: counts the planner's waits that ran out
+    // the planner's launch epoch (its flags carry it): *epoch_dev * 64 + epoch_sub when epoch_dev
+    // is set (a word the host writes before each replay of a recorded graph), else epoch_host;
+    // every launch on the device takes a value no earlier launch used (plan_epoch_take)
+    const uint32_t *epoch_dev = nullptr;
+    uint32_t epoch_sub = 0;
+    uint32_t epoch_host = 0;
+    uint32_t plan_spins = kMoePlanSpins;  // the planner's bounded wait; 0: gives up at once
     int defer_combine = 0;             // 1: no combine launch; the caller adds the dp rows
     uint32_t *seg_expert = nullptr, *seg_start = nullptr, *seg_count = nullptr;  // [128]
     uint32_t *pair_row = nullptr;      // [T * 8]: grouped row of pair t * 8 + s
@@ -249,9 +258,14 @@ struct MoeArgs {
     float *as = nullptr;               // [T * 8][6][4]
     float *dp = nullptr;               // [T * 8][2048] down rows
     int mutant = 0;  // 1: rank mask id^1; 2: weights not normalised; 5: gate/up swapped;
-                     // 6: slot 7 dropped; 7: one activation term
+                     // 6: slot 7 dropped; 7: one activation term; 9: the planner's wait gives up
+                     // at once (plan_spins 0)
 };
 hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st);
+// A fresh planner epoch base for the next launch(es) on the device's stream st: launches use
+// base * 64 + sub with sub < 64, or base * 64. Before the bases wrap the flags are cleared on st
+// and the bases start again from 1. Call outside graph recording (it may enqueue a memset).
+int plan_epoch_take(int family, hipStream_t st, uint32_t *base);  // family: an omega::Family
 size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens);
 size_t moe_work_bytes(uint32_t tokens);
 

@@ -123,15 +123,14 @@ __global__ __launch_bounds__(64) void k_moe_router(const MoeArgs a) {
 // and weights, and once those stores are acknowledged flag the token with this launch's epoch.
 // Workgroup T, dispatched after every ranking workgroup (so nothing it waits for can be queued
 // behind it), waits (bounded) for the T flags, then groups the pairs: expert masks, counts, the
-// prefix sums and every pair's row. The epoch lives in device memory: each launch reads the word
-// the previous launch's grouping workgroup left and flags with one more; the grouping workgroup
-// writes it back as it finishes, so consecutive launches (one stream, kernel boundaries between
-// them) never mistake an old flag for a new one. Up to kPlanSolo tokens the launch is one
-// workgroup whose wavefronts rank the tokens side by side straight into LDS (no handoff).
-constexpr uint32_t kPlanSpins = 1u << 22;  // bounded wait (seconds)
+// prefix sums and every pair's row. The launch's epoch comes from its arguments (a value the host
+// fixed before the launch started, plan_epoch_take), so a ranking workgroup of a launch whose wait
+// ran out can only ever flag that launch's own epoch, never a later one's. Up to kPlanSolo tokens
+// the launch is one workgroup whose wavefronts rank the tokens side by side straight into LDS (no
+// handoff).
 constexpr uint32_t kPlanSolo = 4;           // up to this many tokens: one workgroup, no handoff
-// [0] the last launch's epoch, [32 + t] token t's flag; zero at load, one array per device
-static __device__ __align__(256) uint32_t g_plan_sync[32 + kMoeMaxTokens];
+// token t's flag: the epoch of the launch that ranked it; zero at load, one array per device
+static __device__ __align__(256) uint32_t g_plan_flags[kMoeMaxTokens];
 
 // The grouping from the pairs' expert ids (sid) and expert masks in LDS: per-expert counts, the
 // row and segment prefix sums, the segment tables and every pair's grouped row.
@@ -214,7 +213,7 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
         moe_group(a, sid, mask, scan, tid, pairs);
         return;
     }
-    const uint32_t epoch = __hip_atomic_load(&g_plan_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const uint32_t epoch = a.epoch_dev ? *as_global_u32(a.epoch_dev) * 64u + a.epoch_sub : a.epoch_host;
     if (blockIdx.x < T) {
         if (tid >= 64) return;
         const uint32_t t = blockIdx.x;
@@ -228,22 +227,24 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (lane == 0) __hip_atomic_store(&g_plan_sync[32 + t], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(&g_plan_flags[t], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     for (uint32_t i = tid; i < kME * kWords; i += 256) (&mask[0][0])[i] = 0u;
     __shared__ uint32_t late;
     if (tid < 64) {
+        // plan_spins 0 (a test knob) gives up without a poll
+        bool in_time = a.plan_spins != 0;
         uint32_t spins = 0;
-        while (true) {
-            const uint32_t f = lane < T ? __hip_atomic_load(&g_plan_sync[32 + lane], __ATOMIC_RELAXED,
+        while (in_time) {
+            const uint32_t f = lane < T ? __hip_atomic_load(&g_plan_flags[lane], __ATOMIC_RELAXED,
                                                             __HIP_MEMORY_SCOPE_AGENT)
                                         : epoch;
             if (__all(f == epoch)) break;
-            if (++spins >= kPlanSpins) break;
-            __builtin_amdgcn_s_sleep(1);
+            if (++spins >= a.plan_spins) in_time = false;
+            else __builtin_amdgcn_s_sleep(1);
         }
-        if (tid == 0) late = spins >= kPlanSpins ? 1u : 0u;
+        if (tid == 0) late = in_time ? 0u : 1u;
     }
     __syncthreads();  // every token flagged (or the wait ran out); the masks cleared
     if (late) {
@@ -257,7 +258,6 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
             a.plan[0] = 0u;
             a.plan[1] = 1u;
             if (a.errc) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
@@ -268,9 +268,6 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     }
     __syncthreads();
     moe_group(a, sid, mask, scan, tid, pairs);
-    // the epoch this launch used, for the next launch (every wavefront here is past its reads of
-    // the flags; the ranking workgroups are done)
-    if (tid == 0) __hip_atomic_store(&g_plan_sync[0], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ 4/6. grouped FP8 GEMMs on the matrix cores
@@ -617,9 +614,11 @@ __global__ __launch_bounds__(256) void k_moe_dn_rows(const MoeArgs a) {
 }
 
 // ------------------------------------------------------------------ 7. combine (slot order from zero) [+ residual]
-// each token's moe row: its slots' down rows weighted, summed in slot order from zero
+// each token's moe row: its slots' down rows weighted, summed in slot order from zero (nothing
+// after a plan whose wait ran out: no down row was computed, the residual is written alone)
 __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
     const uint32_t t = blockIdx.x, c = blockIdx.y * 256 + threadIdx.x;
+    const bool late = *as_global_u32(a.plan + 1) != 0u;
     float moe = 0.f;
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
@@ -627,6 +626,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(const MoeArgs a) {
         const float w = (a.mutant == 6 && s == kTopK - 1) ? 0.f : a.weights[t * kTopK + s];
         moe += w * a.dp[(size_t)row * kMH + c];
     }
+    if (late) moe = 0.f;  // the rows read were not written by this launch (every pair on row 0)
     const size_t o = (size_t)t * kMH + c;
     a.out[o] = a.resid ? a.resid[o] + moe : moe;
 }
@@ -681,6 +681,22 @@ size_t moe_work_carve(MoeArgs &a, void *base, uint32_t tokens) {
     return o;
 }
 
+// The planner's epoch bases: one sequence for every launch on the device (its flags are one array
+// per device). A base times 64 stays below 2^32; before it would not, the flags are cleared on the
+// stream and the bases start again from 1. The library drives one device.
+int plan_epoch_take(int family, hipStream_t st, uint32_t *base) {
+    static uint32_t next = 0;
+    static uint32_t *flags = nullptr;
+    const Family f = static_cast<Family>(family);
+    if (next + 1 >= (1u << 26)) {
+        if (!flags) OMEGA_HIP(f, hipGetSymbolAddress(reinterpret_cast<void **>(&flags), HIP_SYMBOL(g_plan_flags)));
+        OMEGA_HIP(f, hipMemsetAsync(flags, 0, sizeof(g_plan_flags), st));
+        next = 0;
+    }
+    *base = ++next;
+    return OMEGA_GPU_OK;
+}
+
 }  // namespace omega
 
 using namespace omega;
@@ -718,8 +734,10 @@ int moe_check(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tensor *
 }
 
 MoeArgs moe_args(const OmegaGpuRouter *r, uint32_t layer, const OmegaGpuFp8Tensor *gu,
-                 const OmegaGpuFp8Tensor *dn, uint32_t tokens, float eps, int norm_topk) {
+                 const OmegaGpuFp8Tensor *dn, uint32_t tokens, float eps, int norm_topk, uint32_t epoch_base) {
     MoeArgs a;
+    a.epoch_host = epoch_base * 64u;
+    a.plan_spins = knobs().moe_mutant == 9 ? 0u : kMoePlanSpins;
     RouterArgs ra = router_args(r, layer, nullptr, eps, norm_topk, 1.0f);
     a.gate = ra.gate;
     a.norm_w = ra.norm_w;
@@ -776,7 +794,9 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
     Ctx *c = ctx(F_GEMM);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     if (!ensure_scratch(F_GEMM, c, moe_work_bytes(tokens))) return OMEGA_GPU_CHIP_FAIL;
-    MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk);
+    uint32_t epoch_base = 0;
+    if (plan_epoch_take(F_GEMM, c->stream, &epoch_base)) return OMEGA_GPU_CHIP_FAIL;
+    MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk, epoch_base);
     moe_work_carve(a, c->scratch, tokens);
     a.h = h_dev;
     a.resid = resid_dev;
@@ -812,7 +832,9 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
     if (!ensure_pinned(F_GEMM, c, hb + 2 * ib + 4)) return OMEGA_GPU_CHIP_FAIL;
     uint8_t *d = static_cast<uint8_t *>(c->scratch);
     uint8_t *pin = static_cast<uint8_t *>(c->pin);
-    MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk);
+    uint32_t epoch_base = 0;
+    if (plan_epoch_take(F_GEMM, c->stream, &epoch_base)) return OMEGA_GPU_CHIP_FAIL;
+    MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk, epoch_base);
     moe_work_carve(a, d, tokens);
     a.h = reinterpret_cast<float *>(d + o_h);
     a.out = reinterpret_cast<float *>(d + o_out);

@@ -200,7 +200,8 @@ const char *omega_gpu_decode_attn_rc_name(int rc);        /* :111 */
 void omega_gpu_decode_attn_set_depth(uint32_t depth);     /* :112 */
 void omega_gpu_decode_attn_set_per_split(uint32_t per_split); /* :113 */
 /* :406-417: 0 off; 1 no RoPE; 2 V read one position late; 3 new K/V not written; 4 split
- * combine ignores the max (TEST ONLY) */
+ * combine ignores the max; 9 (an extension) the in-launch split merge gives up at once, so the
+ * call reports CHIP_FAIL with its message (TEST ONLY) */
 void omega_gpu_decode_attn_test_set_mutant(int mutant);   /* :114 */
 /* :117-125 and dattn/src/rows.rs:98-130: count consecutive bf16 K and V rows of (layer,kv_head) */
 int omega_gpu_decode_attn_cache_write(OmegaGpuDecodeAttnCache *c, uint32_t layer,
@@ -697,13 +698,17 @@ int omega_gpu_moe_batch_f32(const OmegaGpuRouter *router, uint32_t layer, const 
                             const OmegaGpuFp8Tensor *down, uint32_t tokens, const float *h, float eps,
                             int norm_topk, uint32_t *ids, float *weights, float *moe_out);
 /* the same on device pointers, enqueued on the library's stream; out = resid + moe when resid_dev
- * is not NULL (resid_dev may equal out_dev) */
+ * is not NULL (resid_dev may equal out_dev). It returns before the work completes, so a grouping
+ * planner whose bounded wait runs out is not reported here: the block then adds no expert rows
+ * (out = resid, or 0 without resid) and the ids / weights are the rankings' own. The f32 entry
+ * and the batched decode step report that case as CHIP_FAIL. */
 int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const OmegaGpuFp8Tensor *gate_up,
                             const OmegaGpuFp8Tensor *down, uint32_t tokens, const float *h_dev, float eps,
                             int norm_topk, const float *resid_dev, uint32_t *ids_dev, float *weights_dev,
                             float *out_dev);
 /* test mutants of the batched MoE block: 1 rank mask on id^1, 2 weights not normalised, 5 gate and
- * up swapped, 6 slot 7 dropped from the combine, 7 one activation term (a plain fp8 cast) */
+ * up swapped, 6 slot 7 dropped from the combine, 7 one activation term (a plain fp8 cast), 9 the
+ * grouping planner's wait (more than 4 tokens) gives up at once (TEST ONLY) */
 void omega_gpu_moe_test_set_mutant(int mutant);
 /* Batched serving decode (not in the reference ABI; the multi-sequence decode that
  * crates/aien-serve-http's Engine::concurrency / generate_group would drive for the 30B,

@@ -173,6 +173,37 @@ def test_batch_invariance(omega, oracle, small):
     assert e <= TOL, e
 
 
+def test_a_planner_wait_that_runs_out_fails_the_step_and_the_step_runs_again(omega, small):
+    # test MoE mutant 9: every layer's grouping planner gives up at once (no poll; 8 sequences, so
+    # the planner hands off between workgroups). The step reports CHIP_FAIL; the same step run
+    # again (fresh epochs from the host, its K/V rows rewritten) gives the bits it gave before.
+    m, bm = small
+    rng = np.random.default_rng(41)
+    S = 8
+    bm.bd.set_tables(tables_for(rng, S, 16, 1024))
+    bm.bd.set_keep_logits(True)
+    toks = rng.integers(0, 8192, (6, S))
+    lib = omega.lib()
+    try:
+        for p in range(5):
+            bm.bd.step(list(toks[p]), [p] * S)
+        want = bm.bd.step(list(toks[5]), [5] * S).copy()
+        _, _, want_logits, _ = bm.bd.read(S, logits=True)
+        lib.omega_gpu_moe_test_set_mutant(9)
+        try:
+            with pytest.raises(omega.OmegaGpuError, match="timed out"):
+                bm.bd.step(list(toks[5]), [5] * S)
+        finally:
+            lib.omega_gpu_moe_test_set_mutant(0)
+        for _ in range(2):
+            got = bm.bd.step(list(toks[5]), [5] * S)
+            _, _, logits, _ = bm.bd.read(S, logits=True)
+            np.testing.assert_array_equal(got, want)
+            np.testing.assert_array_equal(logits.view(np.uint32), want_logits.view(np.uint32))
+    finally:
+        bm.bd.set_keep_logits(False)
+
+
 def test_refusals(omega, small):
     m, bm = small
     with pytest.raises(omega.OmegaGpuError):

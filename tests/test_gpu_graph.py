@@ -181,6 +181,32 @@ def test_graph_mutants_are_caught(omega, oracle, small, mutant):
     assert worst > 0.01
 
 
+def test_chain_merge_wait_that_runs_out_is_reported_and_the_next_token_recovers(omega, small):
+    # test mutant 9 on the chain: every attention split merge gives up at once (no poll); the token
+    # reports CHIP_FAIL with the count, the flags are cleared and the epochs restart, and the
+    # same positions run again give the bits they gave before the failure
+    m, g = small
+    graph = g.graph
+    rng = np.random.default_rng(31)
+    toks = [int(t) for t in rng.integers(0, m.cfg.vocab, 12)]
+    before = []
+    for pos, tok in enumerate(toks):
+        graph.token(g.x_embed(tok), pos)
+        if pos >= 10:
+            before.append(graph.read(x=True, logits=True))
+    graph.test_set_mutant(9)
+    try:
+        with pytest.raises(omega.OmegaGpuError, match=r"waits ran out \(chain form\)"):
+            graph.token(g.x_embed(toks[11]), 11)
+    finally:
+        graph.test_set_mutant(0)
+    for i, pos in enumerate((10, 11)):
+        graph.token(g.x_embed(toks[pos]), pos)
+        x, _, lg = graph.read(x=True, logits=True)
+        np.testing.assert_array_equal(x.view(np.uint32), before[i][0].view(np.uint32))
+        np.testing.assert_array_equal(lg.view(np.uint32), before[i][2].view(np.uint32))
+
+
 def test_routes_match_per_layer(omega, oracle, small):
     # the router's device state after a token holds the last layer's routing
     m, g = small

@@ -133,3 +133,34 @@ def test_moe_mutants_are_caught(omega, oracle, model, T, mutant):
               not np.allclose(w, want_w, rtol=1e-6, atol=0) or
               max(rel_err(out[t], want[t]) for t in range(T)) > TOL)
     assert caught
+
+
+@pytest.mark.parametrize("T", [8, 32])
+def test_a_planner_wait_that_runs_out_is_reported_and_the_next_call_recovers(omega, oracle, model, T):
+    # test mutant 9: the grouping planner's bounded wait gives up at once (no poll), as when the
+    # rankings never arrive. The f32 entry reports it; the device entry cannot (it returns before
+    # the work ends) and adds no expert rows: out = resid. The next calls take fresh epochs.
+    h = bf16_rows(oracle, np.random.default_rng(13), T)
+    good, good_ids, good_w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    lib = omega.lib()
+    hd = omega.DeviceBuffer.from_array(h)
+    od = omega.DeviceBuffer(h.nbytes)
+    idd = omega.DeviceBuffer(T * 8 * 4)
+    wd = omega.DeviceBuffer(T * 8 * 4)
+    lib.omega_gpu_moe_test_set_mutant(9)
+    try:
+        with pytest.raises(omega.OmegaGpuError, match="timed out"):
+            omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+        rc = lib.omega_gpu_moe_batch_dev(model["router"].as_raw(), 0, model["gu"].as_raw(),
+                                         model["dn"].as_raw(), T, hd.ptr, 1e-6, 1, hd.ptr, idd.ptr,
+                                         wd.ptr, od.ptr)
+        assert rc == 0
+        np.testing.assert_array_equal(od.download(np.float32, T * H).reshape(T, H), h)
+        np.testing.assert_array_equal(idd.download(np.uint32, T * 8).reshape(T, 8), good_ids)
+    finally:
+        lib.omega_gpu_moe_test_set_mutant(0)
+    for _ in range(2):
+        out, ids, w = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+        np.testing.assert_array_equal(ids, good_ids)
+        np.testing.assert_array_equal(w.view(np.uint32), good_w.view(np.uint32))
+        np.testing.assert_array_equal(out.view(np.uint32), good.view(np.uint32))

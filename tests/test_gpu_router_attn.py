@@ -237,6 +237,35 @@ def test_decode_attention_mutants_are_caught(omega, oracle, mutant):
     c.free()
 
 
+def test_decode_attention_merge_wait_that_runs_out_is_reported(omega, oracle):
+    # test mutant 9: every split merge gives up at once (no poll), as when a split never flags;
+    # the call reports CHIP_FAIL with its message and the next call at the same position (a new
+    # epoch) matches the oracle
+    layers, max_pos, theta = 1, 256, 1e6
+    c = omega.DecodeAttnCache(layers, max_pos, theta)
+    ref = oracle.Dattn(layers, max_pos, theta)
+    rng = np.random.default_rng(21)
+    qn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    c.set_norms(0, qn, kn)
+    ref.set_norms(0, qn, kn)
+    rows = [_qkv_row(rng) for _ in range(40)]
+    for pos in range(39):
+        c.attend(0, pos, rows[pos], 1e-6)
+        ref.attend(0, pos, rows[pos], 1e-6)
+    lib = omega.lib()
+    lib.omega_gpu_decode_attn_test_set_mutant(9)
+    try:
+        with pytest.raises(omega.OmegaGpuError, match="ran out of waits"):
+            c.attend(0, 39, rows[39], 1e-6)
+    finally:
+        lib.omega_gpu_decode_attn_test_set_mutant(0)
+    out, _ = c.attend(0, 39, rows[39], 1e-6)
+    want = ref.attend(0, 39, rows[39], 1e-6)
+    assert rel_err(out, want) <= TOL
+    c.free()
+
+
 def _paged_pool(oracle, rng, nb, layers, kvh=4):
     lay = oracle.kv_layout(nb, 16, layers, kvh, 128)
     pool = oracle.f32_to_bf16(rng.standard_normal(lay.pool_bytes // 2).astype(np.float32))
