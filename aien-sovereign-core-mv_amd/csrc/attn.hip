@@ -185,14 +185,16 @@ __device__ __forceinline__ void paged_stage_v(const PagedRegs &R, uint32_t tok0,
 }
 
 // The 8 q heads of kv head h (f32 rows q[8][128]) as the bf16 hi/lo B operand of S^T = K q^T.
-__device__ __forceinline__ void paged_q(const float *q, uint32_t lane, uint16_t (*qhl)[8][128], bf16x8 (&qop)[4]) {
-    const uint32_t g = lane >> 4, n = lane & 15;
-    float q0[8], q1[8];
+__device__ __forceinline__ void paged_q_load(const float *q, uint32_t lane, float (&q0)[8], float (&q1)[8]) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         q0[r] = *as_global_f32(q + r * 128 + lane);
         q1[r] = *as_global_f32(q + r * 128 + 64 + lane);
     }
+}
+__device__ __forceinline__ void paged_q_stage(const float (&q0)[8], const float (&q1)[8], uint32_t lane,
+                                              uint16_t (*qhl)[8][128], bf16x8 (&qop)[4]) {
+    const uint32_t g = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         qhl[0][r][lane] = bf16_split_hi(q0[r]);
@@ -204,6 +206,11 @@ __device__ __forceinline__ void paged_q(const float *q, uint32_t lane, uint16_t 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
         qop[ks] = as_bf16x8(*reinterpret_cast<const u32x4 *>(&qhl[n >> 3][n & 7][32 * ks + 8 * g]));
+}
+__device__ __forceinline__ void paged_q(const float *q, uint32_t lane, uint16_t (*qhl)[8][128], bf16x8 (&qop)[4]) {
+    float q0[8], q1[8];
+    paged_q_load(q, lane, q0, q1);
+    paged_q_stage(q0, q1, lane, qhl, qop);
 }
 
 // Pages [p_begin, p_end) of a sequence of `ctx` tokens (table tab): the online softmax of the 8 q
@@ -375,17 +382,19 @@ __device__ __forceinline__ void paged4_stage(const Paged4Regs &R, uint32_t tok0,
     }
 }
 
-// pages [p_begin, p_end) of all four kv heads: the two-set straight-path loop of paged_pages
+// pages [p_begin, p_end) of all four kv heads: the two-set straight-path loop of paged_pages;
+// blk0 / blk1: the page ids of p_begin and min(p_begin + 1, p_end - 1), read by the caller
 template <int MUT>
 __device__ __forceinline__ void paged4_pages(const PagedSrc &src, const int32_t *tab, uint32_t w, uint32_t p_begin,
-                                             uint32_t p_end, uint32_t ctx, const bf16x8 (&qop)[4], uint8_t *kt,
-                                             uint8_t *vt, uint32_t lane, float &m_l, float &l_l, f32x4 (&O)[8]) {
+                                             uint32_t p_end, uint32_t ctx, uint32_t blk0, uint32_t blk1,
+                                             const bf16x8 (&qop)[4], uint8_t *kt, uint8_t *vt, uint32_t lane,
+                                             float &m_l, float &l_l, f32x4 (&O)[8]) {
     const uint32_t g = lane >> 4, n = lane & 15, last = p_end - 1;
     const cu32 *ctab = as_const_u32(tab);
     Paged4Regs A, B;
     const uint32_t p1 = min(p_begin + 1, last);
-    paged4_load<MUT>(src, ctab, ctab[p_begin], p_begin, ctx, w, lane, A);
-    paged4_load<MUT>(src, ctab, ctab[p1], p1, ctx, w, lane, B);
+    paged4_load<MUT>(src, ctab, blk0, p_begin, ctx, w, lane, A);
+    paged4_load<MUT>(src, ctab, blk1, p1, ctx, w, lane, B);
     m_l = -INFINITY;
     l_l = 0.f;
 #pragma unroll
@@ -397,10 +406,12 @@ __device__ __forceinline__ void paged4_pages(const PagedSrc &src, const int32_t 
         const uint32_t ctx_b = p + 1 < p_end ? ctx : 0u;  // 0: the null page
         paged4_stage(A, p * 16, ctx, w, lane, kt, vt, T);
         dattn_page<false>(T, qop, p * 16, ctx, g, n, m_l, l_l, O);
-        paged4_load<MUT>(src, ctab, blk_a, pa, ctx, w, lane, A);
+        // the next pair's pages, only those that exist (a load past the split's last page would be
+        // waited for by the partials' stores)
+        if (p + 2 < p_end) paged4_load<MUT>(src, ctab, blk_a, pa, ctx, w, lane, A);
         paged4_stage(B, (p + 1) * 16, ctx_b, w, lane, kt, vt, T);
         dattn_page<false>(T, qop, (p + 1) * 16, ctx_b, g, n, m_l, l_l, O);
-        paged4_load<MUT>(src, ctab, blk_b, pb, ctx, w, lane, B);
+        if (p + 3 < p_end) paged4_load<MUT>(src, ctab, blk_b, pb, ctx, w, lane, B);
     }
 }
 
@@ -422,10 +433,197 @@ __global__ __launch_bounds__(256) void k_paged4(const AttnArgs a) {
     const PagedSrc src{a.pool, a.g, a.layer};
     float m_l, l_l;
     f32x4 O[8];
-    paged4_pages<MUT>(src, a.block_tables + (size_t)b * a.max_blocks, w, p_begin, p_end, ctx, qop, kt, vt, lane, m_l,
-                      l_l, O);
+    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
+    const cu32 *ctab = as_const_u32(tab);
+    paged4_pages<MUT>(src, tab, w, p_begin, p_end, ctx, ctab[p_begin], ctab[min(p_begin + 1, p_end - 1)], qop, kt,
+                      vt, lane, m_l, l_l, O);
     paged_store(a.part + (((size_t)b * a.qh + w * 8) * a.splits + c) * kPartStride, (size_t)a.splits * kPartStride,
                 lane, m_l, l_l, O);
+}
+
+// The configuration-3 form with the split combine in the same launch, for launches whose
+// workgroups are all resident at once (grid <= the kernel's occupancy x CUs). Every split stores
+// its partials with agent-scope stores (dims d and d + 64 side by side, as the fused kernel's), and
+// once they are acknowledged flags (sequence, split) with the launch's epoch. Workgroup c of a
+// sequence then merges q heads c, c + active, .. < 32 once every one of the sequence's `active`
+// splits has flagged: its 4 wavefronts take the splits' 16-split chunks in turn (every load of a
+// wavefront in one round trip) and their sums meet in LDS in wavefront order. A wait that runs
+// out (bounded; merge_spins 0 gives up at once) is counted in errc and the heads of that workgroup
+// are written as NaN.
+constexpr uint32_t kPagedFoldMax = 1024;  // (sequence, split) flags of one launch
+constexpr uint32_t kPagedFoldMaxSplits = 256;
+// the flags, then at [kPagedFoldMax] the give-up count; zero at load, one array per device
+static __device__ __align__(256) uint32_t g_paged_fold[kPagedFoldMax + 64];
+
+__device__ __forceinline__ void paged_store_agent(float *part, size_t stride, uint32_t lane, float m_l, float l_l,
+                                                  const f32x4 (&O)[8]) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    const uint32_t hg = g & 1, nb_off = (g >> 1) * 4;  // as paged_store
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float *pp = part + (size_t)(4 * hg + i) * stride;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const uint32_t d = 16 * (nb + nb_off) + n;
+            __hip_atomic_store(pp + 4 + 2 * (d & 63) + (d >> 6), pair_sum<32>(O[nb][i], O[nb + 4][i]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (lane < 8) {
+        float *pp = part + (size_t)lane * stride;
+        __hip_atomic_store(pp, m_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + 1, l_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Merge of q head hq of sequence b over its `active` splits (all four wavefronts; the caller has
+// seen every split's flag). Every wavefront computes the maximum and the sum over all splits from
+// lane j's (m, l) of splits j + 64 k and keeps the weights in its own LDS row; wavefront w sums
+// the splits of chunks w, w + 4, .. (16 splits each; the launch's split count is a multiple of
+// 16, so a chunk's slots all exist). Slots past `active` hold whatever an earlier launch left:
+// their values are masked to +0 (an all-zero mask word in the same LDS row) before their weight
+// 0 applies.
+__device__ __forceinline__ void paged_fold_merge(const AttnArgs &a, uint32_t b, uint32_t hq, uint32_t active,
+                                                 bool ok, uint32_t w, uint32_t lane, float (*osum)[128],
+                                                 float (*wsh)[kPagedFoldMaxSplits],
+                                                 uint32_t (*msk)[kPagedFoldMaxSplits]) {
+    const float *base = a.part + ((size_t)b * 32 + hq) * a.splits * kPartStride;
+    float mk[4], lk[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t j = min(lane + 64 * k, a.splits - 1);
+        const uint64_t ml = __hip_atomic_load(reinterpret_cast<const uint64_t *>(base + (size_t)j * kPartStride),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mk[k] = __uint_as_float((uint32_t)ml);
+        lk[k] = __uint_as_float((uint32_t)(ml >> 32));
+    }
+    const uint64_t *ob = reinterpret_cast<const uint64_t *>(base + 4 + 2 * lane);
+    constexpr uint32_t kStride64 = kPartStride / 2;
+    uint64_t xo[4][16];
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t) {
+        const uint32_t ch = w + 4 * t;
+        if (ch * 16 >= active) break;
+        // the chunk's address as one per-lane value: the 16 loads are constant offsets from it
+        // (kept out of scalar registers, 16 live offsets per chunk would not fit there)
+        uintptr_t pv = reinterpret_cast<uintptr_t>(ob + (size_t)(ch * 16) * kStride64);
+        asm volatile("" : "+v"(pv));
+        const uint64_t *pc = reinterpret_cast<const uint64_t *>(pv);
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i)
+            xo[t][i] = __hip_atomic_load(pc + i * kStride64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) M = fmaxf(M, lane + 64 * k < active ? mk[k] : -INFINITY);
+    M = row16_max(M);
+    M = fmaxf(fmaxf(readlane_f32(M, 0), readlane_f32(M, 16)), fmaxf(readlane_f32(M, 32), readlane_f32(M, 48)));
+    float lw = 0.f;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const bool mine = lane + 64 * k < active;
+        const float wk = mine ? (a.mutant == 4 ? 1.f : expf(mk[k] - M)) : 0.f;
+        lw += wk * (mine ? lk[k] : 0.f);
+        wsh[w][64 * k + lane] = wk;  // this wavefront's own rows: read back below by the same wavefront
+        msk[w][64 * k + lane] = mine ? 0xffffffffu : 0u;
+    }
+    const float L = wave_sum(lw);
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (uint32_t t = 0; t < 4; ++t) {
+        const uint32_t ch = w + 4 * t;
+        if (ch * 16 >= active) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t si = ch * 16 + i;
+            const float wi = wsh[w][si];
+            const uint32_t m = msk[w][si];
+            a0 = fmaf(wi, __uint_as_float((uint32_t)xo[t][i] & m), a0);
+            a1 = fmaf(wi, __uint_as_float((uint32_t)(xo[t][i] >> 32) & m), a1);
+        }
+    }
+    osum[w][lane] = a0;
+    osum[w][lane + 64] = a1;
+    __syncthreads();
+    if (w == 0) {
+        const float sc = a.out_scale / L;
+        float *o = a.out + ((size_t)b * 32 + hq) * 128;
+        const float o0 = ((osum[0][lane] + osum[1][lane]) + (osum[2][lane] + osum[3][lane])) * sc;
+        const float o1 = ((osum[0][lane + 64] + osum[1][lane + 64]) + (osum[2][lane + 64] + osum[3][lane + 64])) * sc;
+        o[lane] = ok ? o0 : __builtin_nanf("");
+        o[lane + 64] = ok ? o1 : __builtin_nanf("");
+    }
+    __syncthreads();  // osum is read before the next head's sums land
+}
+
+template <int MUT>
+__global__ __launch_bounds__(256) void k_paged4f(const AttnArgs a) {
+    __shared__ __align__(16) uint16_t qhl[4][2][8][128];
+    __shared__ __align__(16) uint8_t kt[16 * kRow4];
+    __shared__ __align__(16) uint8_t vt[16 * kRow4];
+    __shared__ float osum[4][128];
+    __shared__ float wsh[4][kPagedFoldMaxSplits];
+    __shared__ uint32_t msk[4][kPagedFoldMaxSplits];
+    __shared__ uint32_t in_time_sh;
+    const uint32_t lane = lane_id(), c = blockIdx.x, b = blockIdx.y;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int32_t *tab = a.block_tables + (size_t)b * a.max_blocks;
+    const cu32 *ctab = as_const_u32(tab);
+    // The split of the host's context hint (the call's max_context; every sequence of a uniform
+    // batch has it): its first two page ids go out with the context length and the q rows, one
+    // round trip for all three; a sequence whose context plans otherwise reads its own.
+    const uint32_t pages_h = min(max((a.ctx_hint + 15) / 16, 1u), a.max_blocks);
+    uint32_t active_h, pps_h;
+    attn_split_plan(pages_h, a.splits, 0, active_h, pps_h);
+    const uint32_t pb_h = min(c * pps_h, pages_h - 1), p1_h = min(pb_h + 1, pages_h - 1);
+    const uint32_t blk0_h = ctab[pb_h], blk1_h = ctab[p1_h];
+    const uint32_t ctx = (uint32_t)a.context_lens[b];
+    float q0[8], q1[8];
+    paged_q_load(a.q + ((size_t)b * a.qh + w * 8) * 128, lane, q0, q1);
+    const uint32_t pages = (ctx + 15) / 16;
+    uint32_t active, pps;
+    attn_split_plan(pages, a.splits, 0, active, pps);
+    if (c >= active) return;  // uniform over the workgroup
+    const uint32_t p_begin = c * pps, p_end = min(pages, p_begin + pps), p1 = min(p_begin + 1, p_end - 1);
+    const bool hinted = p_begin == pb_h && p1 == p1_h;
+    const uint32_t blk0 = hinted ? blk0_h : ctab[p_begin], blk1 = hinted ? blk1_h : ctab[p1];
+    bf16x8 qop[4];
+    paged_q_stage(q0, q1, lane, qhl[w], qop);
+    const PagedSrc src{a.pool, a.g, a.layer};
+    float m_l, l_l;
+    f32x4 O[8];
+    paged4_pages<MUT>(src, tab, w, p_begin, p_end, ctx, blk0, blk1, qop, kt, vt, lane, m_l, l_l, O);
+    paged_store_agent(a.part + (((size_t)b * a.qh + w * 8) * a.splits + c) * kPartStride,
+                      (size_t)a.splits * kPartStride, lane, m_l, l_l, O);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wavefront's partials acknowledged
+    __syncthreads();                                   // and every other wavefront's
+    uint32_t *fl = a.flags + b * a.splits;
+    if (threadIdx.x == 0) __hip_atomic_store(fl + c, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c >= 32) return;
+    if (w == 0) {
+        bool in_time = a.merge_spins != 0;
+        uint32_t spins = 0;
+        while (in_time) {
+            bool mine = true;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t j = lane + 64 * k;
+                const uint32_t f = j < active ? __hip_atomic_load(fl + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                              : a.epoch;
+                mine = mine && f == a.epoch;
+            }
+            if (__all(mine)) break;
+            if (++spins >= a.merge_spins) in_time = false;
+            else __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) {
+            in_time_sh = in_time ? 1u : 0u;
+            if (!in_time) __hip_atomic_fetch_add(a.errc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    const bool ok = in_time_sh != 0;
+    for (uint32_t hq = c; hq < 32; hq += active) paged_fold_merge(a, b, hq, active, ok, w, lane, osum, wsh, msk);
 }
 
 // Balanced work items (the batched decode step): workgroup r serves items [run_off[r],
@@ -448,8 +646,10 @@ __global__ __launch_bounds__(256) void k_paged_items(const PagedItemsArgs a) {
         paged_q(a.q + ((size_t)s * 32 + w * 8) * 128, lane, qhl[w], qop);
         float m_l, l_l;
         f32x4 O[8];
-        paged4_pages<0>(src, a.tables + (size_t)s * a.max_blocks, w, p_begin, p_end, ctx, qop, kt, vt, lane, m_l,
-                        l_l, O);
+        const int32_t *tab = a.tables + (size_t)s * a.max_blocks;
+        const cu32 *ctab = as_const_u32(tab);
+        paged4_pages<0>(src, tab, w, p_begin, p_end, ctx, ctab[p_begin], ctab[min(p_begin + 1, p_end - 1)], qop, kt,
+                        vt, lane, m_l, l_l, O);
         paged_store(a.part + ((size_t)it * 32 + w * 8) * kPartStride, kPartStride, lane, m_l, l_l, O);
     }
 }
@@ -956,6 +1156,63 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     }
     return hipGetLastError();
 }
+
+namespace {
+struct FoldState {
+    uint32_t *dev = nullptr;  // g_paged_fold's address on the library's device
+    uint32_t epoch = 0;
+    int capacity = -1;        // workgroups of k_paged4f resident at once
+    bool on = true;
+};
+FoldState &fold_state() {
+    static FoldState f;
+    return f;
+}
+}  // namespace
+
+// The paged call: the folded single launch (k_paged4f) where its grid is resident at once and
+// the launch is not recorded into a graph (its epoch is per call), else the split launch and the
+// combine launch. *folded tells which ran.
+hipError_t launch_paged_call(AttnArgs a, const CombineArgs &cb, int cus, hipStream_t st, bool *folded) {
+    FoldState &f = fold_state();
+    *folded = false;
+    const bool shape = f.on && paged_mfma(a.qh, a.kvh, a.g.block_size) && a.kvh == 4 && a.qh == 32 &&
+                       a.splits % 16 == 0 && a.splits <= kPagedFoldMaxSplits &&
+                       (size_t)a.splits * a.seqs <= kPagedFoldMax && a.out;
+    if (shape && !stream_recording(st)) {
+        hipError_t e = hipSuccess;
+        if (f.capacity < 0) {
+            int per_cu = 0;
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_paged4f<0>), 256, 0);
+            if (e != hipSuccess) return e;
+            f.capacity = per_cu * cus;
+        }
+        if (!f.dev && (e = hipGetSymbolAddress(reinterpret_cast<void **>(&f.dev), HIP_SYMBOL(g_paged_fold))) != hipSuccess)
+            return e;
+        if ((int)(a.splits * a.seqs) <= f.capacity) {
+            if (++f.epoch >= (1u << 31)) {  // the flags restart with the epochs
+                if ((e = hipMemsetAsync(f.dev, 0, kPagedFoldMax * 4, st)) != hipSuccess) return e;
+                f.epoch = 1;
+            }
+            a.flags = f.dev;
+            a.errc = f.dev + kPagedFoldMax;
+            a.epoch = f.epoch;
+            a.out_scale = cb.out_scale;
+            a.merge_spins = a.mutant == 9 ? 0u : kDattnMergeSpins;
+            const dim3 grid(a.splits, a.seqs);
+            if (a.mutant == 2) hipLaunchKernelGGL(k_paged4f<2>, grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL(k_paged4f<0>, grid, dim3(256), 0, st, a);
+            *folded = true;
+            return hipGetLastError();
+        }
+    }
+    hipError_t e = launch_attention(a, st);
+    if (e == hipSuccess) e = launch_attn_combine(cb, st);
+    return e;
+}
+
+// the give-up count of the folded launches (device address), for the entries that report it
+uint32_t *paged_fold_errc() { return fold_state().dev ? fold_state().dev + kPagedFoldMax : nullptr; }
 
 // ------------------------------------------------------------------------ split combine
 // Paged partials are interleaved dim pairs (o[2 l], o[2 l + 1] from lane l) for the VALU kernel
@@ -2088,12 +2345,24 @@ static int paged_batch(const float *q, const void *pool, const OmegaGpuKvLayout 
     cb.qh = qh;
     cb.out = od;
     cb.mutant = a.mutant;
+    a.out = od;
+    a.ctx_hint = (uint32_t)*std::max_element(lens, lens + seqs);
+    // the folded launch's give-up count, cleared before and read back after (through the pinned
+    // table words, whose upload is ahead in the stream)
+    uint32_t *errc = paged_fold_errc();
+    if (errc) OMEGA_HIP(F_ATTN, hipMemsetAsync(errc, 0, 4, cx->stream));
+    bool folded = false;
     OMEGA_HIP(F_ATTN, hipEventRecord(cx->ev0, cx->stream));
-    OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
-    OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
+    OMEGA_HIP(F_ATTN, launch_paged_call(a, cb, cx->cus, cx->stream, &folded));
     OMEGA_HIP(F_ATTN, hipEventRecord(cx->ev1, cx->stream));
     OMEGA_HIP(F_ATTN, hipMemcpyAsync(pin, od, qf * 4, hipMemcpyDeviceToHost, cx->stream));
+    uint32_t *late = reinterpret_cast<uint32_t *>(pin + p_tab);
+    if (folded) OMEGA_HIP(F_ATTN, hipMemcpyAsync(late, paged_fold_errc(), 4, hipMemcpyDeviceToHost, cx->stream));
     OMEGA_HIP(F_ATTN, hipStreamSynchronize(cx->stream));
+    if (folded && *late) {
+        set_error(F_ATTN, "paged attention: the in-launch split merge ran out of waits (%u)", *late);
+        return OMEGA_GPU_ATTN_CHIP_FAIL;
+    }
     memcpy(out, pin, qf * 4);
     if (info) {
         memset(info, 0, sizeof(*info));
@@ -2270,12 +2539,19 @@ static int paged_batch_dev(const char *what, const float *q_dev, const void *poo
     cb.qh = num_q_heads;
     cb.out = out_dev;
     cb.mutant = a.mutant;
-    OMEGA_HIP(F_ATTN, launch_attention(a, cx->stream));
-    OMEGA_HIP(F_ATTN, launch_attn_combine(cb, cx->stream));
+    a.out = out_dev;
+    a.ctx_hint = max_context;
+    bool folded = false;
+    OMEGA_HIP(F_ATTN, launch_paged_call(a, cb, cx->cus, cx->stream, &folded));
     return OMEGA_GPU_ATTN_OK;
 }
 }  // namespace
 }  // namespace omega
+
+void omega_gpu_paged_attention_set_folded(int on) {
+    std::lock_guard<std::recursive_mutex> lk(big_lock());
+    fold_state().on = on != 0;
+}
 
 int omega_gpu_paged_attention_batch_dev(const float *q_dev, const void *pool_dev,
                                         const OmegaGpuKvLayout *layout,

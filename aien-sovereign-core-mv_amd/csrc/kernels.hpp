@@ -183,7 +183,16 @@ struct AttnArgs {
     uint32_t seqs = 1, qh = 32, kvh = 4;
     uint32_t splits = 1;
     float *part = nullptr;                  // [seqs][qh][splits][kPartStride]
-    int mutant = 0;                         // 2: V one position late
+    int mutant = 0;                         // 2: V one position late; 4: merge ignores the maxima
+    // the folded form (the split merge in the same launch): out, the (sequence, split) flags,
+    // this launch's epoch, the merge's bounded wait (0: gives up at once) and its give-up count
+    float *out = nullptr;                   // [seqs][qh][128]
+    float out_scale = 1.0f;
+    uint32_t *flags = nullptr;
+    uint32_t *errc = nullptr;
+    uint32_t epoch = 0;
+    uint32_t merge_spins = kDattnMergeSpins;
+    uint32_t ctx_hint = 0;  // the call's longest context: the split plan the page ids are read for early
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 // GQA group 8 over 16-token pages runs on the matrix cores (k_paged), other shapes on the VALU

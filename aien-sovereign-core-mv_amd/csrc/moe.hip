@@ -190,12 +190,12 @@ __global__ __launch_bounds__(256) void k_moe_plan(const MoeArgs a) {
     // mutant 1: the pick's mask hits id ^ 1; mutant 2: weights not normalised
     const int rm = a.mutant == 1 ? 2 : (a.mutant == 2 ? 4 : 0);
     if (gridDim.x == 1) {
-        // up to kPlanSolo tokens: this workgroup's wavefront t ranks token t straight into LDS,
-        // with no handoff between workgroups
+        // one workgroup (up to kPlanSolo tokens, or any count while launches are recorded into
+        // a graph): wavefront w ranks tokens w, w + 4, .. straight into LDS, with no handoff
+        // between workgroups
         for (uint32_t i = tid; i < kME * kWords; i += 256) (&mask[0][0])[i] = 0u;
         __syncthreads();  // masks cleared before any wavefront marks its pairs
-        const uint32_t t = tid >> 6;
-        if (t < T) {
+        for (uint32_t t = tid >> 6; t < T; t += 4) {
             Route r;
             route_topk<kME / 64>(a.logits + (size_t)t * kME, 0, a.norm_topk, rm, r);
 #pragma unroll
@@ -636,7 +636,10 @@ hipError_t launch_moe_batch(const MoeArgs &a, hipStream_t st) {
     const uint32_t segs_max = P < kME ? P : kME;
     OMEGA_LAUNCH(k_moe_prep, dim3(T), dim3(256), 0, st, a);
     OMEGA_LAUNCH(k_moe_router, dim3(kME, (T + 3) / 4), dim3(64), 0, st, a);
-    OMEGA_LAUNCH(k_moe_plan, dim3(T <= kPlanSolo ? 1 : T + 1), dim3(256), 0, st, a);
+    // the handoff form needs this launch's own epoch: from the word the host writes before each
+    // replay, or from the host per call when the launch is not recorded
+    const bool solo = T <= kPlanSolo || (!a.epoch_dev && stream_recording(st));
+    OMEGA_LAUNCH(k_moe_plan, dim3(solo ? 1 : T + 1), dim3(256), 0, st, a);
     if (T < kMoeGemvMax) {
         // one workgroup per (segment, 16 gate+up row pairs) / (segment, 32 down rows)
         OMEGA_LAUNCH(k_moe_gu_rows, dim3(segs_max * (kMI / 4) / 4), dim3(256), 0, st, a);
@@ -794,8 +797,9 @@ int omega_gpu_moe_batch_dev(const OmegaGpuRouter *router, uint32_t layer, const 
     Ctx *c = ctx(F_GEMM);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     if (!ensure_scratch(F_GEMM, c, moe_work_bytes(tokens))) return OMEGA_GPU_CHIP_FAIL;
+    // recorded launches plan in one workgroup and need no epoch
     uint32_t epoch_base = 0;
-    if (plan_epoch_take(F_GEMM, c->stream, &epoch_base)) return OMEGA_GPU_CHIP_FAIL;
+    if (!stream_recording(c->stream) && plan_epoch_take(F_GEMM, c->stream, &epoch_base)) return OMEGA_GPU_CHIP_FAIL;
     MoeArgs a = moe_args(router, layer, gate_up, down, tokens, eps, norm_topk, epoch_base);
     moe_work_carve(a, c->scratch, tokens);
     a.h = h_dev;

@@ -153,6 +153,12 @@ GraphRecorder *&graph_recorder() {
     return r;
 }
 
+bool stream_recording(hipStream_t st) {
+    if (graph_recorder()) return true;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+}
+
 uint64_t event_ns(Ctx *c) {
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, c->ev0, c->ev1) != hipSuccess) return 0;

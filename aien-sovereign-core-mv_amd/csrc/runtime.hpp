@@ -96,6 +96,9 @@ struct GraphRecorder {
     uint32_t nodes = 0;
 };
 GraphRecorder *&graph_recorder();  // per thread; null when not recording
+// Launches enqueued on st now are recorded into a graph (this library's recorder or a caller's
+// stream capture) and may be replayed: no launch argument may then carry a per-call value.
+bool stream_recording(hipStream_t st);
 
 template <typename... P, typename... A>
 void record_kernel(void (*kern)(P...), dim3 grid, dim3 block, unsigned shm, A &&...args) {

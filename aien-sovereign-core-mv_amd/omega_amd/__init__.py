@@ -177,6 +177,7 @@ SIGNATURES = {
     "omega_gpu_decode_attn_set_depth": (None, [u32]),
     "omega_gpu_decode_attn_set_per_split": (None, [u32]),
     "omega_gpu_decode_attn_test_set_mutant": (None, [i32]),
+    "omega_gpu_paged_attention_set_folded": (None, [i32]),
     "omega_gpu_decode_attn_cache_write": (i32, [P, u32, u32, u32, u32, P, P]),
     "omega_gpu_decode_attn_cache_read": (i32, [P, u32, u32, u32, P, P]),
     "omega_gpu_decode_attn_cache_payload_len": (u64, [P, u32]),

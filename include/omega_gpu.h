@@ -461,6 +461,14 @@ int omega_gpu_paged_attention_bf16(const float *q, const void *pool, const Omega
                                    uint32_t context_len, uint32_t layer_idx, uint32_t num_q_heads,
                                    uint32_t num_kv_heads, uint32_t head_dim, float *out,
                                    OmegaGpuAttnInfo *info);
+/* The form of the paged calls (not in the reference ABI). on = 1 (the default): where a call's
+ * split workgroups fit the device at once and its stream is not being captured into a graph,
+ * the splits are merged inside the same launch (one launch per call); on = 0: always the split
+ * launch and a combine launch. Both give the same results to f32 rounding. A merge whose bounded
+ * wait runs out (test mutant 9 of omega_gpu_decode_attn_test_set_mutant makes it give up at
+ * once) is reported as CHIP_FAIL by the host-buffer entries; the device-pointer entries return
+ * before the work ends and write that call's merged heads as NaN. */
+void omega_gpu_paged_attention_set_folded(int on);
 /* ffi.rs:448-462: batched; block_tables [num_seqs][max_blocks_per_seq] (negative = none),
  * context_lens [num_seqs]; q/out [num_seqs][num_q_heads][head_dim] */
 int omega_gpu_paged_attention_batch_bf16(const float *q, const void *pool,

@@ -165,6 +165,91 @@ def test_paged_mutants_are_caught(omega, oracle, mutant):
     assert max(rel_err(clean[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) for b in range(2)) <= TOL
 
 
+# ---------------------------------------------------------------- the folded form
+# Where a call's split workgroups all fit the device at once (split count a multiple of 16, at
+# most 1024 (sequence, split) pairs), the splits are merged in the same launch; the configuration-3
+# shapes above run that way. The two forms merge in different orders and agree to f32 rounding.
+def run_forms(omega, pool, q, tabs, lens, layer):
+    lib = omega.lib()
+    try:
+        lib.omega_gpu_paged_attention_set_folded(0)
+        split = run_dev(omega, pool, q, tabs, lens, layer)
+    finally:
+        lib.omega_gpu_paged_attention_set_folded(1)
+    return run_dev(omega, pool, q, tabs, lens, layer), split
+
+
+@pytest.mark.parametrize("case", ["1x2048", "1x8192", "ragged8", "32x2048"])
+def test_folded_and_split_forms_agree(omega, oracle, case):
+    rng = np.random.default_rng(71)
+    nb = 1024
+    pool = Pool(omega, oracle, rng, nb, 1)
+    if case == "ragged8":  # 64 splits planned; a sequence of 1 page keeps one split and merges 32 heads
+        lens = np.array([1, 16, 100, 513, 700, 2047, 3000, 4096], np.int32)
+    else:
+        seqs, ctx = map(int, case.split("x"))
+        lens = np.full(seqs, ctx, np.int32)
+    maxb = int((lens.max() + 15) // 16)
+    tabs = np.stack([rng.permutation(nb)[:maxb] for _ in range(lens.size)]).astype(np.int32)
+    q = rng.standard_normal((lens.size, QH * HD)).astype(np.float32)
+    folded, split = (o.reshape(lens.size, QH * HD) for o in run_forms(omega, pool, q, tabs, lens, 0))
+    assert np.isfinite(folded).all()
+    assert rel_err(folded, split) <= 1e-5
+    for b in range(lens.size):
+        assert rel_err(folded[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) <= TOL, b
+
+
+@pytest.mark.parametrize("mutant", [2, 4])
+def test_folded_mutants_are_caught(omega, oracle, mutant):
+    # 2 sequences of 2048: 64 splits each, folded
+    rng = np.random.default_rng(72)
+    nb = 512
+    pool = Pool(omega, oracle, rng, nb, 1)
+    lens = np.array([2048, 1900], np.int32)
+    tabs = np.stack([rng.permutation(nb)[:128] for _ in range(2)]).astype(np.int32)
+    q = (3.0 * rng.standard_normal((2, QH * HD))).astype(np.float32)
+    lib = omega.lib()
+    lib.omega_gpu_decode_attn_test_set_mutant(mutant)
+    try:
+        out = run_dev(omega, pool, q, tabs, lens, 0).reshape(2, QH * HD)
+    finally:
+        lib.omega_gpu_decode_attn_test_set_mutant(0)
+    errs = [rel_err(out[b], oracle_out(oracle, pool, q[b], tabs[b], lens[b], 0)) for b in range(2)]
+    assert max(errs) > TOL, errs
+
+
+def test_folded_merge_wait_that_runs_out(omega, oracle):
+    # test mutant 9: every in-launch merge gives up at once (no poll). The host-buffer entry
+    # reports CHIP_FAIL with its message; the device-pointer entry (it returns before the work
+    # ends) writes the merged heads as NaN; the next calls match the oracle.
+    rng = np.random.default_rng(73)
+    nb = 512
+    pool = Pool(omega, oracle, rng, nb, 1)
+    lens = np.array([2048], np.int32)
+    tabs = rng.permutation(nb)[:128].astype(np.int32).reshape(1, 128)
+    q = rng.standard_normal((1, QH * HD)).astype(np.float32)
+    lib = omega.lib()
+    out = np.zeros(QH * HD, np.float32)
+    info = omega.AttnInfo()
+
+    def host_call():
+        return lib.omega_gpu_paged_attention_batch_bf16(omega.ptr(q), omega.ptr(pool.host), C.byref(pool.L),
+                                                        omega.ptr(tabs), omega.ptr(lens), 128, 1, 0, QH, KVH,
+                                                        HD, omega.ptr(out), C.byref(info))
+
+    lib.omega_gpu_decode_attn_test_set_mutant(9)
+    try:
+        assert host_call() == -4
+        assert "ran out of waits" in omega._s(lib.omega_gpu_attention_last_error())
+        assert np.isnan(run_dev(omega, pool, q, tabs, lens, 0)).all()
+    finally:
+        lib.omega_gpu_decode_attn_test_set_mutant(0)
+    want = oracle_out(oracle, pool, q[0], tabs[0], 2048, 0)
+    assert host_call() == 0
+    assert rel_err(out, want) <= TOL
+    assert rel_err(run_dev(omega, pool, q, tabs, lens, 0), want) <= TOL
+
+
 # ---------------------------------------------------------------- the serving step's balanced items
 def run_items(omega, pool, q, tabs, lens, layer):
     """omega_gpu_paged_attention_items_dev: sequence b attends over positions 0..lens[b]-1."""
