@@ -13,7 +13,10 @@ refined f64 router) runs every prompt token and every generated token one step a
 first generated token is the argmax after the last prompt token. Recorded per generated step:
 the token, the top-2 margin (own30b_check.rs:181-193), the top 16 (index, value) pairs, the
 logits at 1024 seeded vocabulary indices, the smallest rank-8 / rank-9 routing margin over the
-48 layers and its layer; plus the full logits of the first generated step. Recorded per processed
+48 layers and its layer; plus the full logits of the first generated step. Recorded at every
+prompt position too (each reads a different context, so the stream is not a greedy repetition):
+the argmax, the top-2 margin, the top 16 (index, value) pairs and the logits at 256 of the seeded
+indices (every fourth). Recorded per processed
 token (the 512 prompt tokens, then the first 63 generated ones), per layer: the routed expert ids
 in slot order and the smallest logit gap between consecutive ranks of the top 9 (the rank-8 /
 rank-9 margin, and ln(w_k / w_k+1) inside the top 8), which bounds how close the routing was to
@@ -69,12 +72,23 @@ def main():
     steps = PROMPT + NEW - 1
     step_routes = np.zeros((steps, L, TOPK), np.uint8)
     step_gap = np.zeros((steps, L), np.float32)
+    psub = subset[::4]
+    p_top1 = np.empty(PROMPT, np.int64)
+    p_margin = np.empty(PROMPT, np.float32)
+    p_top_idx = np.empty((PROMPT, 16), np.int64)
+    p_top_val = np.empty((PROMPT, 16), np.float32)
+    p_sub_val = np.empty((PROMPT, psub.size), np.float32)
     t1 = time.time()
     hidden = None
     for p, tok in enumerate(prompt.tolist()):
         hidden = eng.step(int(tok))
         prompt_margin[p] = eng.last_routes()[2]
         step_routes[p], step_gap[p] = route_record(eng)
+        logits = eng.logits(hidden)
+        p_top1[p], p_margin[p], order = top2(logits)
+        p_top_idx[p] = order
+        p_top_val[p] = logits[order]
+        p_sub_val[p] = logits[psub]
         if p % 64 == 63:
             print(f"prompt {p + 1}/{PROMPT}, {(time.time() - t1) / (p + 1):.2f} s/step", flush=True)
     tokens = np.empty(NEW, np.int64)
@@ -113,7 +127,9 @@ def main():
                         sub_val=sub_val, first_logits=first_logits.astype(np.float32),
                         prompt_route_margin=prompt_margin, gen_route_margin=gen_margin,
                         route_min=route_min, route_layer=route_layer, step_routes=step_routes,
-                        step_gap=step_gap)
+                        step_gap=step_gap, prompt_top1=p_top1, prompt_margin=p_margin,
+                        prompt_top_idx=p_top_idx, prompt_top_val=p_top_val,
+                        prompt_subset=psub, prompt_sub_val=p_sub_val)
     print(f"wrote {args.out} in {time.time() - t0:.0f} s", flush=True)
 
 

@@ -18,7 +18,11 @@ histories are different computations. Hence two tests:
 1. Free-running, the reference's own full-size bar (own30b_check,
    crates/aien-inference-abi/src/bin/own30b_check.rs:181-193, 986-1006): the 512 prompt tokens
    and 64 greedy tokens with nothing forced; every generated token equals the oracle's, or the
-   first divergence sits at an oracle top-2 margin below the 1e-3 floor.
+   first divergence sits at an oracle top-2 margin below the 1e-3 floor. Up to the first token
+   at which any layer routes to another expert set than the oracle (the two histories are the
+   same computation until then; here that is processed token 4), the prompt positions' logits
+   are held to test 2's prompt bar. (The random-init model's greedy stream repeats a few ids;
+   test 2's 512 prompt positions each read a different context.)
 2. Routing forced only near ties: at every processed token, each layer whose oracle
    consecutive-rank gap of the top 9 (rank-8 / rank-9 logit margin and ln(w_k / w_k+1) inside the
    top 8) is below 1e-2, ten times the measured drift, takes the oracle's expert ids (teacher
@@ -29,7 +33,13 @@ histories are different computations. Hence two tests:
    divergence passes only at an oracle top-2 margin below 1e-3), logits within 2e-3 relative (max
    |gpu - cpu| over max |cpu|) at 1024 seeded vocabulary indices plus the oracle's top 16 at every
    step and over the whole vocabulary at the first generated step, top-2 margins within 2 x 2e-3
-   of max |logit|.
+   of max |logit|. The logits of all 512 prompt positions (each a different context) are held to
+   the same bar at 256 seeded indices and the oracle's top 16, except positions 0..3 at 4e-3: they
+   attend over at most four bf16 V rows, so one rounding flip weighs up to a quarter of the
+   attention output (measured 2.8e-3 at position 0, 1.8e-3 at most from position 4, 8.2e-4 from
+   64). A prompt position's argmax may differ from the oracle's only where the oracle's top-2
+   margin is within twice the measured absolute error of the top 16 (the most that error can
+   move a margin).
 """
 import os
 
@@ -96,6 +106,26 @@ class StepCheck:
         return True
 
 
+def prompt_bar(t):
+    return 4e-3 if t < 4 else TOL
+
+
+def check_prompt_position(golden, t, logits):
+    """Prompt position t's logits against the fixture: 256 seeded indices and the oracle's top 16
+    within prompt_bar(t); the argmax equal unless the oracle's top-2 margin is within twice the
+    measured absolute error of the top 16. Returns the relative error."""
+    ti, tv = golden["prompt_top_idx"][t], golden["prompt_top_val"][t]
+    e = max(rel_err(logits[golden["prompt_subset"]], golden["prompt_sub_val"][t]), rel_err(logits[ti], tv))
+    assert e <= prompt_bar(t), f"prompt position {t}: logits rel err {e:.2e}"
+    top, want = int(np.argmax(logits)), int(golden["prompt_top1"][t])
+    if top != want:
+        abs_err = float(np.abs(logits[ti] - tv).max())
+        m = float(golden["prompt_margin"][t])
+        assert m <= 2 * abs_err, (f"prompt position {t}: argmax {top}, oracle {want} at margin {m:.2e} "
+                                  f"(measured abs error {abs_err:.2e})")
+    return e
+
+
 def decode(g, golden, forced, on_step):
     """The 512 prompt tokens, then the first 63 generated tokens, one decode step each (575
     processed tokens); on_step(t, tok) after processed token t with the greedy token it produced
@@ -121,7 +151,7 @@ def test_config4_routes_match_except_at_near_ties(omega, golden, model):
     n_gen = len(golden["tokens"])
     routes = golden["step_routes"].astype(np.uint32)
     near = golden["step_gap"] < ROUTE_NEAR                  # [steps][layers]
-    state = {"diverged": None, "ranked": 0, "forced": int(near.sum())}
+    state = {"diverged": None, "ranked": 0, "forced": int(near.sum()), "prompt_worst": 0.0}
     prompt = golden["prompt"]
     pos, tok = 0, None
     try:
@@ -138,6 +168,9 @@ def test_config4_routes_match_except_at_near_ties(omega, golden, model):
                     f"step {t} layer {l}: routed {ids[l].tolist()}, oracle {routes[t, l].tolist()} " \
                     f"(oracle gap {float(golden['step_gap'][t, l]):.2e})"
                 state["ranked"] += 1
+            if t < npr:
+                _, _, logits = g.read(logits=True)
+                state["prompt_worst"] = max(state["prompt_worst"], check_prompt_position(golden, t, logits))
             if t >= npr - 1:
                 s = t - (npr - 1)
                 _, _, logits = g.read(logits=True)
@@ -147,7 +180,8 @@ def test_config4_routes_match_except_at_near_ties(omega, golden, model):
     finally:
         g.force_routes(None)
     print(f"routing forced at {state['forced']} near-tie (step, layer) points, {state['ranked']} ranked "
-          f"by the device and equal to the oracle; {chk.compared} of {n_gen} greedy tokens identical "
+          f"by the device and equal to the oracle; prompt logits rel err <= {state['prompt_worst']:.2e} "
+          f"over {npr} positions; {chk.compared} of {n_gen} greedy tokens identical "
           f"(divergence at {state['diverged']}), logits rel err <= {chk.worst:.2e}, margins within "
           f"{chk.worst_margin:.2e} of max |logit|")
     assert state["diverged"] is not None or chk.compared == n_gen
@@ -157,16 +191,29 @@ def test_config4_free_running_greedy_tokens(omega, golden, model):
     g = model.graph
     g.force_routes(None)
     npr, n_gen = len(golden["prompt"]), len(golden["tokens"])
-    state = {"diverged": None, "worst": 0.0}
+    routes = golden["step_routes"].astype(np.uint32)
+    state = {"diverged": None, "worst": 0.0, "route_apart": None, "prompt_worst": 0.0, "prompt_checked": 0}
     got = []
 
     def on_step(t, tok):
+        ids, _ = g.read_routes()
+        # the expert sets (an order swap inside the top 8 only reorders the combine's sum)
+        if state["route_apart"] is None and not np.array_equal(np.sort(ids, axis=1), np.sort(routes[t], axis=1)):
+            state["route_apart"] = t
+        if t < npr and state["route_apart"] is None:
+            # the same history so far: this prompt position's logits on the prompt bar
+            _, _, logits = g.read(logits=True)
+            state["prompt_worst"] = max(state["prompt_worst"], check_prompt_position(golden, t, logits))
+            state["prompt_checked"] += 1
         if t < npr - 1:
             return True
         s = t - (npr - 1)
         got.append(tok)
         _, _, logits = g.read(logits=True)
-        state["worst"] = max(state["worst"], rel_err(logits[golden["subset"]], golden["sub_val"][s]))
+        e = rel_err(logits[golden["subset"]], golden["sub_val"][s])
+        state["worst"] = max(state["worst"], e)
+        if state["route_apart"] is None:
+            assert e <= TOL, f"generated step {s}: logits rel err {e:.2e}"
         if tok != int(golden["tokens"][s]):
             m = float(golden["margins"][s])
             assert m < NEAR_TIE, (f"greedy token {s} is {tok}, oracle {int(golden['tokens'][s])} at oracle "
@@ -176,6 +223,9 @@ def test_config4_free_running_greedy_tokens(omega, golden, model):
         return True
 
     decode(g, golden, False, on_step)
-    print(f"free-running: {len(got) - (state['diverged'] is not None)} of {n_gen} greedy tokens identical "
-          f"(divergence at {state['diverged']}); logits rel err <= {state['worst']:.2e} with the histories apart")
+    print(f"free-running: routing first apart at processed token {state['route_apart']}; "
+          f"{state['prompt_checked']} prompt positions on the logit bar (rel err <= "
+          f"{state['prompt_worst']:.2e}); {len(got) - (state['diverged'] is not None)} of {n_gen} greedy "
+          f"tokens identical (divergence at {state['diverged']}); generated logits rel err <= "
+          f"{state['worst']:.2e}")
     assert state["diverged"] is not None or len(got) == n_gen
