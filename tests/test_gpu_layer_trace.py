@@ -14,9 +14,10 @@ and FP8 block scales dropped move the MoE cosine below 0.99; the decode attentio
 moves the attention cosine below 0.99; router kernel mutants make the MoE replay disagree.
 
 Here: the full 48-layer model synthesised on the device (the seed of tests/golden/
-config4_greedy.npz), layers 0, 23 and 47 traced over the first 32 tokens of configuration 4's
-prompt; on the host the oracle holds just those three layers (oref_model_synth_layers, the same
-generator) and replays them: q|k|v and o with fp8_grouped (oref_fp8_grouped), the decode
+config4_greedy.npz), layers 0, 23 and 47 traced at every processed position of configuration 4's
+decode: the 512 prompt tokens, then 63 greedy tokens the device chooses (575 positions); on the
+host the oracle holds just those three layers (oref_model_synth_layers, the same generator) and
+replays them: q|k|v and o with fp8_grouped (oref_fp8_grouped), the decode
 attention over the layer's own bf16 K/V (oref_dattn_attend), the router (oref_router_logits_f64),
 the plan (oref_moe_plan) and the FP8 MoE arm (oref_moe_block). Router mutant 1 (norm weight
 ignored) is the identity on this model's unit norm weights and router mutant 3 moves only the
@@ -31,9 +32,9 @@ pytestmark = pytest.mark.gpu
 
 FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_greedy.npz")
 LAYERS = [0, 23, 47]
-TOKENS = 32
+GENERATED = 63
 CONTROL_TOKENS = 4
-MAX_POS = 256
+MAX_POS = 1024
 THREADS = 16
 
 
@@ -47,7 +48,7 @@ def cosine(a, e):
 def setup(omega, oracle):
     z = np.load(FIXTURE)  # numpy arrays only (allow_pickle off)
     seed = int(z["seed"])
-    prompt = [int(t) for t in z["prompt"][:TOKENS]]
+    prompt = [int(t) for t in z["prompt"]]
     dev = omega.SynthDecodeModel(seed, MAX_POS)
     cfg = dict(dev.cfg)
     host = oracle.Model(dict(layers=cfg["layers"], hidden=cfg["hidden"], q_heads=cfg["q_heads"],
@@ -59,25 +60,35 @@ def setup(omega, oracle):
     dev.free()
 
 
-def run_traced(dev, tokens, layers):
+def run_traced(dev, tokens, layers, generate=0):
+    """Trace the given layers over the tokens, then `generate` greedy tokens; returns the records
+    per layer and the token fed at every position."""
     g = dev.graph
     g.set_trace(layers)
     recs = [[] for _ in layers]
+    fed = []
     try:
-        for pos, tok in enumerate(tokens):
-            print(f"traced token pos {pos}", flush=True)
-            g.token_id(tok, pos)
+        tok = None
+        for pos in range(len(tokens) + generate):
+            if pos % 64 == 0:
+                print(f"traced token pos {pos}", flush=True)
+            tok_in = tokens[pos] if pos < len(tokens) else tok
+            fed.append(tok_in)
+            tok, _ = g.token_id(tok_in, pos)
             for i in range(len(layers)):
                 recs[i].append(g.read_trace(i))
     finally:
         g.set_trace(None)
-    return recs
+    return recs, fed
 
 
 def replay(oracle, host, i, recs, eps, theta):
     """The host replay of subset layer i over consecutive traced positions 0..n-1: per position
     the attention cosine, the MoE cosine, whether the expert sets agree, the weight error and the
-    router x' error."""
+    router x' error. The attention runs position by position (its K/V cache grows); the MoE of
+    every position is independent and runs on a pool of host threads."""
+    from concurrent.futures import ThreadPoolExecutor
+
     qw, qs = host.tensor(i, 0)
     ow, os_ = host.tensor(i, 1)
     gw, gs = host.tensor(i, 2)
@@ -85,12 +96,15 @@ def replay(oracle, host, i, recs, eps, theta):
     gate, in_norm, post_norm = host.tensor(i, 4), host.tensor(i, 5), host.tensor(i, 6)
     cache = oracle.Dattn(1, MAX_POS, theta)
     cache.set_norms(0, host.tensor(i, 7), host.tensor(i, 8))
-    out = []
+    attn = []
     for t, r in enumerate(recs):
         xn = oracle.rmsnorm(r["x_in"], in_norm, eps)
         qkv = oracle.fp8_grouped(qw, qs, [0], xn, THREADS)[0]
         att = cache.attend(0, t, qkv, eps)
-        proj = oracle.fp8_grouped(ow, os_, [0], att, THREADS)[0]
+        attn.append(cosine(r["attn_proj"], oracle.fp8_grouped(ow, os_, [0], att, THREADS)[0]))
+
+    def moe(t):
+        r = recs[t]
         post = oracle.rmsnorm(r["x_mid"], post_norm, eps)
         xprime = float(np.max(np.abs(r["post"] - post) / (1.0 + np.abs(post))))
         logits = oracle.router_logits(gate, post, refined=True)
@@ -99,10 +113,12 @@ def replay(oracle, host, i, recs, eps, theta):
         want = oracle.moe_block(gw, gs, dw, ds, ids, wts, post)
         host_w = dict(zip(ids.tolist(), wts.tolist()))
         wt_err = max(abs(float(w) - host_w.get(int(e), 0.0)) for e, w in zip(r["experts"], r["weights"]))
-        out.append(dict(attn=cosine(r["attn_proj"], proj), moe=cosine(r["moe_out"], want),
-                        routing=sorted(r["experts"].tolist()) == sorted(ids.tolist()),
-                        wt_err=wt_err, xprime=xprime))
-    return out
+        return dict(attn=attn[t], moe=cosine(r["moe_out"], want),
+                    routing=sorted(r["experts"].tolist()) == sorted(ids.tolist()), wt_err=wt_err,
+                    xprime=xprime)
+
+    with ThreadPoolExecutor(THREADS) as ex:
+        return list(ex.map(moe, range(len(recs))))
 
 
 def summary(rows):
@@ -114,7 +130,8 @@ def summary(rows):
 def test_traced_layers_replay_on_the_reference_bar(oracle, setup):
     dev, host, prompt = setup
     c = dev.cfg
-    recs = run_traced(dev, prompt, LAYERS)
+    recs, fed = run_traced(dev, prompt, LAYERS, GENERATED)
+    assert len(recs[0]) == len(prompt) + GENERATED
     g = dev.graph
     for i, l in enumerate(LAYERS):
         for t, r in enumerate(recs[i]):
@@ -135,10 +152,10 @@ def test_traced_layers_replay_on_the_reference_bar(oracle, setup):
     last = recs[-1][-1]
     np.testing.assert_array_equal(ids[LAYERS[-1]], last["experts"])
     np.testing.assert_array_equal(w[LAYERS[-1]].view(np.uint32), last["weights"].view(np.uint32))
-    # the trace does not change the arithmetic: the same prompt replayed by the graph (no trace)
-    # ends on the same residual row and the same token
+    # the trace does not change the arithmetic: the same tokens replayed by the graph (no trace)
+    # end on the same residual row and the same logits
     xa, _, la = g.read(x=True, logits=True)
-    for pos, tok in enumerate(prompt):
+    for pos, tok in enumerate(fed):
         g.token_id(tok, pos)
     xb, _, lb = g.read(x=True, logits=True)
     np.testing.assert_array_equal(xa.view(np.uint32), xb.view(np.uint32))
@@ -165,7 +182,7 @@ def test_negative_controls_are_caught(omega, oracle, setup, name):
     on, off = sets[name]
     on()  # the traced tokens run as direct launches: each launch reads the mutant it is given
     try:
-        recs = run_traced(dev, prompt[:CONTROL_TOKENS], [LAYERS[0]])[0]
+        recs = run_traced(dev, prompt[:CONTROL_TOKENS], [LAYERS[0]])[0][0]
     finally:
         off()
     s = summary(replay(oracle, host, 0, recs, c["eps"], c["rope_theta"]))
