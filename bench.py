@@ -11,8 +11,9 @@ hipGraph replay (token id in, greedy token out). value = tokens / second.
 
 The JSON line also carries:
   roofline: the dominant launch's algorithmic bytes over its average duration. The timed form
-            is the default chain of six launches per layer (or, with --persistent, every layer in
-            one persistent launch, "decode_layers", then the lm_head). The durations come from
+            is the default chain of launches per layer (the router rows inside the gate|up launch:
+            five per layer; or, with --persistent, every layer in one persistent launch,
+            "decode_layers", then the lm_head). The durations come from
             further decode steps made as direct launches, each launch's start and end recorded by
             its own dispatch (hipExtLaunchKernel events on the library stream); peak 8 TB/s.
             traffic comes from the committed rocprofv3 PMC summary for that kernel when one exists
@@ -75,11 +76,25 @@ def algorithmic_bytes(kind, ctx):
         return TOPK * (2048 * 768 + 16 * 6 * 4) + TOPK * I * 4 + 2 * H * 4
     if kind == "lm_head":      # 151936 x 2048 bf16 + x + final norm + logits
         return V * H * 2 + 2 * H * 4 + V * 4
+    if kind == "route_gate_up":  # the router rows and gate|up in one launch
+        return algorithmic_bytes("router", ctx) + algorithmic_bytes("gate_up", ctx)
     return 0
 
 
-# the decode graph's launches per layer, in order, then the lm_head
+# the decode graph's kernels of one layer (the router rows in their own launch or in gate|up's),
+# then the lm_head
 LAYER_KINDS = ["qkv", "attn", "o_proj", "router", "gate_up", "down"]
+# launch kinds the graph records per launch (include/omega_gpu.h OMEGA_GPU_DGRAPH_K_*)
+KIND_NAMES = {1: "qkv", 2: "attn", 3: "o_proj", 5: "router", 6: "gate_up", 8: "down", 10: "lm_head"}
+
+
+def launch_names(kinds):
+    """Names of a token's launches from the kinds the graph recorded; a gate|up launch with no
+    router launch in the token carries the router rows too."""
+    names = [KIND_NAMES.get(int(k), f"kind{int(k)}") for k in kinds]
+    if "router" not in names:
+        names = ["route_gate_up" if n == "gate_up" else n for n in names]
+    return names
 
 
 def build_model(om, max_pos):
@@ -936,6 +951,7 @@ def main():
         pos += 1
     om.sync()
     elapsed = time.perf_counter() - t0
+    launches = int(st.launches)
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
 
@@ -959,7 +975,7 @@ def main():
     def kind_names(n):
         if persistent:
             return ["decode_layers", "lm_head"]
-        return [LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head" for i in range(n)]
+        return launch_names(g.stamps()[1])[:n]
 
     dispatch = {}
     g.set_stamps(True)
@@ -987,11 +1003,11 @@ def main():
         tok, _ = g.token_id(tok, pos)
         pos += 1
         top2(g.read(logits=True)[2])
-        st_, _ = g.stamps()
-        for i, dt in enumerate(g.kernel_ns()):
-            k = LAYER_KINDS[i % len(LAYER_KINDS)] if i < len(LAYER_KINDS) * L else "lm_head"
+        st_, kinds_ = g.stamps()
+        for k, dt in zip(launch_names(kinds_), g.kernel_ns()):
             spans.setdefault(k, []).append(int(dt))
         spans.setdefault("_token", []).append(int(st_[-1]))
+        n_nodes = len(kinds_) + 1
     g.set_stamps(False)
     dom = max(kernels, key=lambda k: kernels[k]["dispatch_us_per_token"])
     dk = kernels[dom]
@@ -1022,7 +1038,7 @@ def main():
     chain_ms = ms_per_step if not persistent else (other["ms_per_step"] if other else None)
     ev_ns = 0.0
     if chain_ms:
-        ev_ns = max(0.0, float(np.mean(spans["_token"])) - chain_ms * 1e6) / (len(LAYER_KINDS) * L + 2)
+        ev_ns = max(0.0, float(np.mean(spans["_token"])) - chain_ms * 1e6) / n_nodes
     chain_graph_us = {k: round(max(0.0, float(np.mean(v)) - ev_ns) / 1e3, 3)
                       for k, v in spans.items() if k != "_token"}
     stage_us = None
@@ -1059,7 +1075,8 @@ def main():
         "config": {
             "workload": "Qwen3-30B-A3B FP8 decode step, bs=1, "
                         + ("direct kernel launches" if args.eager else "one hipGraph per token")
-                        + (" (every layer in one persistent launch)" if persistent else " (six launches per layer)")
+                        + (" (every layer in one persistent launch)" if persistent
+                           else f" ({(launches - 1) // L} launches per layer)")
                         + f", {args.prompt}-token prompt then greedy decode",
             "layers": L, "hidden": H, "q_heads": QH, "kv_heads": KVH, "head_dim": HD,
             "experts": E, "top_k": TOPK, "moe_intermediate": I, "vocab": V,
@@ -1080,9 +1097,9 @@ def main():
             "algorithmic_bytes_per_token": step_bytes,
             "achieved_GBs": round(step_bytes / (ms_per_step * 1e6), 1),
             "frac": round(step_bytes / (ms_per_step * 1e6) / PEAK_GBS, 4),
-            "launches_per_token": 2 if persistent else len(LAYER_KINDS) * L + 1,
+            "launches_per_token": launches,
             "form": "persistent (every layer in one launch) + lm_head" if persistent
-                    else "chain of six launches per layer + lm_head",
+                    else f"chain of {(launches - 1) // L} launches per layer + lm_head",
             "chain_graph_span_us": chain_graph_us,
         },
         "kernels": kernels,
