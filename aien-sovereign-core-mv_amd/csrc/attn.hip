@@ -1602,20 +1602,20 @@ int omega_gpu_decode_attn_cache_alloc(uint32_t layers, uint32_t max_pos, double 
     const size_t pool_bytes = (size_t)(max_pos / 16) * c->g.block_stride;
     std::vector<float> cs((size_t)max_pos * 64), sn((size_t)max_pos * 64);
     rope_table(rope_theta, max_pos, cs.data(), sn.data());
-    hipError_t e = hipMalloc(&c->pool, pool_bytes);
+    hipError_t e = dev_malloc(&c->pool, pool_bytes);
     if (e == hipSuccess) e = hipMemset(c->pool, 0, pool_bytes);
-    if (e == hipSuccess) e = hipMalloc(&c->q_norm, (size_t)layers * 128 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->k_norm, (size_t)layers * 128 * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->q_norm, (size_t)layers * 128 * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->k_norm, (size_t)layers * 128 * 4);
     if (e == hipSuccess) e = hipMemset(c->q_norm, 0, (size_t)layers * 128 * 4);
     if (e == hipSuccess) e = hipMemset(c->k_norm, 0, (size_t)layers * 128 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->rope_cos, cs.size() * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->rope_sin, sn.size() * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->rope_cos, cs.size() * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->rope_sin, sn.size() * 4);
     if (e == hipSuccess) e = hipMemcpy(c->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(c->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMalloc(&c->qkv, 5120 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->out, 4096 * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->part, (size_t)32 * kDattnSplits * kPartStride * 4);
-    if (e == hipSuccess) e = hipMalloc(&c->flags, (4 * kDattnSplits + 1) * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->qkv, 5120 * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->out, 4096 * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->part, (size_t)32 * kDattnSplits * kPartStride * 4);
+    if (e == hipSuccess) e = dev_malloc(&c->flags, (4 * kDattnSplits + 1) * 4);
     if (e == hipSuccess) e = hipMemset(c->flags, 0, (4 * kDattnSplits + 1) * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -1635,7 +1635,7 @@ void omega_gpu_decode_attn_cache_free(OmegaGpuDecodeAttnCache *c) {
     if (cx) (void)hipStreamSynchronize(cx->stream);
     void *ps[] = {c->pool, c->q_norm, c->k_norm, c->rope_cos, c->rope_sin, c->qkv, c->out, c->part, c->flags};
     for (void *p : ps)
-        if (p) (void)hipFree(p);
+        if (p) (void)dev_free(p);
     delete c;
 }
 
@@ -2147,7 +2147,7 @@ int omega_gpu_attention_pool_alloc(size_t bytes, void **cpu) {
         return OMEGA_GPU_ATTN_BAD_ARGS;
     }
     if (!ctx(F_ATTN)) return OMEGA_GPU_ATTN_CHIP_FAIL;
-    hipError_t e = hipHostMalloc(&g_pool_host, bytes, hipHostMallocMapped);
+    hipError_t e = host_malloc(&g_pool_host, bytes, hipHostMallocMapped);
     if (e != hipSuccess) {
         g_pool_host = nullptr;
         set_error(F_ATTN, "attention pool of %zu bytes: %s", bytes, hipGetErrorString(e));
@@ -2163,7 +2163,7 @@ void omega_gpu_attention_pool_free(void) {
     if (!g_pool_host) return;
     Ctx *cx = ctx(F_ATTN);
     if (cx) (void)hipStreamSynchronize(cx->stream);
-    (void)hipHostFree(g_pool_host);
+    (void)host_free(g_pool_host);
     g_pool_host = nullptr;
 }
 

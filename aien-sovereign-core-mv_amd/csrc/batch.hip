@@ -681,7 +681,7 @@ int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpu
     const uint32_t T = cfg->max_seqs;
     hipError_t e = hipSuccess;
     auto M = [&](void **p, size_t bytes) {
-        if (e == hipSuccess) e = hipMalloc(p, bytes);
+        if (e == hipSuccess) e = dev_malloc(p, bytes);
         if (e == hipSuccess) e = hipMemset(*p, 0, bytes);
     };
     M((void **)&b->x, (size_t)T * kBdH * 4);
@@ -711,7 +711,7 @@ int omega_gpu_batch_decode_create(const OmegaGpuBatchDecodeConfig *cfg, OmegaGpu
         M((void **)&L.q_norm, 128 * 4);
         M((void **)&L.k_norm, 128 * 4);
     }
-    if (e == hipSuccess) e = hipHostMalloc((void **)&b->pin, sizeof(BdIo), hipHostMallocDefault);
+    if (e == hipSuccess) e = host_malloc((void **)&b->pin, sizeof(BdIo), hipHostMallocDefault);
     if (e == hipSuccess) {
         std::vector<float> cs((size_t)cfg->max_pos * 64), sn((size_t)cfg->max_pos * 64);
         rope_table(cfg->rope_theta, cfg->max_pos, cs.data(), sn.data());
@@ -739,13 +739,13 @@ void omega_gpu_batch_decode_free(OmegaGpuBatchDecode *b) {
                   b->hid_hi, b->hid_lo, b->logits, b->tables, b->moe, b->route_ids, b->route_w, b->io,
                   b->final_norm, b->rope_cos, b->rope_sin};
     for (void *p : ps)
-        if (p) (void)hipFree(p);
+        if (p) (void)dev_free(p);
     for (auto &L : b->layers) {
-        if (L.in_norm) (void)hipFree(L.in_norm);
-        if (L.q_norm) (void)hipFree(L.q_norm);
-        if (L.k_norm) (void)hipFree(L.k_norm);
+        if (L.in_norm) (void)dev_free(L.in_norm);
+        if (L.q_norm) (void)dev_free(L.q_norm);
+        if (L.k_norm) (void)dev_free(L.k_norm);
     }
-    if (b->pin) (void)hipHostFree(b->pin);
+    if (b->pin) (void)host_free(b->pin);
     delete b;
 }
 

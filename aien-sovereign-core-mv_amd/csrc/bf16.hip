@@ -266,13 +266,14 @@ int bf16_ensure_tiled(Family f, OmegaGpuBf16Tensor *t) {
     Ctx *c = ctx(f);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     const size_t elems = (size_t)t->n * t->k, pieces = elems / 8;
-    OMEGA_HIP(f, hipMalloc(&t->wt, elems * 2));
+    if (seal_refuses(f, "bf16 tiled weight twin", elems * 2)) return OMEGA_GPU_TOO_LARGE;
+    OMEGA_HIP(f, dev_malloc(&t->wt, elems * 2));
     hipLaunchKernelGGL(k_bf16_tile, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, c->stream, t->w, t->wt,
                        t->n, t->k, pieces);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
-        (void)hipFree(t->wt);
+        (void)dev_free(t->wt);
         t->wt = nullptr;
         set_error(f, "bf16 tiled twin: %s", hipGetErrorString(e));
         return OMEGA_GPU_CHIP_FAIL;
@@ -305,18 +306,18 @@ int omega_gpu_bf16_tensor_upload(uint32_t n, uint32_t k, const uint16_t *w_bf16,
     const size_t count = (size_t)n * k;
     uint32_t *flag = nullptr;
     uint32_t bad = 0;
-    hipError_t e = hipMalloc(&t->w, count * 2);
-    if (e == hipSuccess) e = hipMalloc(&flag, 4);
+    hipError_t e = dev_malloc(&t->w, count * 2);
+    if (e == hipSuccess) e = dev_malloc(&flag, 4);
     if (e == hipSuccess) e = hipMemsetAsync(flag, 0, 4, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(t->w, w_bf16, count * 2, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = launch_bf16_scan(t->w, count, flag, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (flag) (void)hipFree(flag);
+    if (flag) (void)dev_free(flag);
     if (e != hipSuccess || bad) {
         if (e != hipSuccess) set_error(F_BF16, "bf16 upload: %s", hipGetErrorString(e));
         else set_error(F_BF16, "bf16 upload: a NaN or infinite weight");
-        if (t->w) (void)hipFree(t->w);
+        if (t->w) (void)dev_free(t->w);
         delete t;
         return e != hipSuccess ? OMEGA_GPU_CHIP_FAIL : OMEGA_GPU_BAD_ARGS;
     }
@@ -338,12 +339,12 @@ int omega_gpu_bf16_tensor_synth(uint32_t n, uint32_t k, uint64_t seed, uint64_t 
     t->n = n;
     t->k = k;
     t->n_pad = n;
-    hipError_t e = hipMalloc(&t->w, (size_t)n * k * 2);
+    hipError_t e = dev_malloc(&t->w, (size_t)n * k * 2);
     if (e == hipSuccess) e = launch_bf16_synth(t->w, n, k, seed, tensor_id, sigma, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         set_error(F_BF16, "bf16 synth: %s", hipGetErrorString(e));
-        if (t->w) (void)hipFree(t->w);
+        if (t->w) (void)dev_free(t->w);
         delete t;
         return OMEGA_GPU_CHIP_FAIL;
     }
@@ -356,8 +357,8 @@ void omega_gpu_bf16_tensor_free(OmegaGpuBf16Tensor *t) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *c = ctx(F_BF16);
     if (c) (void)hipStreamSynchronize(c->stream);
-    if (t->w) (void)hipFree(t->w);
-    if (t->wt) (void)hipFree(t->wt);
+    if (t->w) (void)dev_free(t->w);
+    if (t->wt) (void)dev_free(t->wt);
     delete t;
 }
 

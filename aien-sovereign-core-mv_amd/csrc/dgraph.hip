@@ -726,7 +726,7 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     g->layers.resize(cfg->layers);
     hipError_t e = hipSuccess;
     auto M = [&](void **p, size_t bytes) {
-        if (e == hipSuccess) e = hipMalloc(p, bytes);
+        if (e == hipSuccess) e = dev_malloc(p, bytes);
         if (e == hipSuccess) e = hipMemset(*p, 0, bytes);
     };
     M((void **)&g->x, kHidden * 4);
@@ -749,7 +749,7 @@ int omega_gpu_decode_graph_create(const OmegaGpuDecodeGraphConfig *cfg, OmegaGpu
     M((void **)&g->words, g->words_bytes);
     M((void **)&g->pflags, (size_t)cfg->layers * 4 * kDattnSplits * 4);
     M((void **)&g->pstamps, (size_t)(1 + cfg->layers * kTokStampsPerLayer) * 8);
-    if (e == hipSuccess) e = hipHostMalloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
+    if (e == hipSuccess) e = host_malloc((void **)&g->pin, sizeof(GraphIo) + kHidden * 4, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         set_error(F_SESSION, "decode graph create: %s", hipGetErrorString(e));
@@ -779,10 +779,10 @@ void omega_gpu_decode_graph_free(OmegaGpuDecodeGraph *g) {
                   g->final_norm, g->route_log, g->route_log_w, g->forced, g->flags,
                   g->players, g->words, g->pflags, g->pstamps, g->trace};
     for (void *p : ps)
-        if (p) (void)hipFree(p);
+        if (p) (void)dev_free(p);
     for (auto &L : g->layers)
-        if (L.input_norm) (void)hipFree(L.input_norm);
-    if (g->pin) (void)hipHostFree(g->pin);
+        if (L.input_norm) (void)dev_free(L.input_norm);
+    if (g->pin) (void)host_free(g->pin);
     delete g;
 }
 
@@ -1047,11 +1047,11 @@ int omega_gpu_decode_graph_test_set_trace(OmegaGpuDecodeGraph *g, const uint32_t
     Ctx *c = ctx(F_SESSION);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     OMEGA_HIP(F_SESSION, hipStreamSynchronize(c->stream));
-    if (g->trace) OMEGA_HIP(F_SESSION, hipFree(g->trace));
+    if (g->trace) OMEGA_HIP(F_SESSION, dev_free(g->trace));
     g->trace = nullptr;
     g->trace_layers.assign(layers, layers + n);
     if (n) {
-        OMEGA_HIP(F_SESSION, hipMalloc(&g->trace, (size_t)n * kTrWords * 4));
+        OMEGA_HIP(F_SESSION, dev_malloc(&g->trace, (size_t)n * kTrWords * 4));
         OMEGA_HIP(F_SESSION, hipMemset(g->trace, 0, (size_t)n * kTrWords * 4));
     }
     return OMEGA_GPU_OK;

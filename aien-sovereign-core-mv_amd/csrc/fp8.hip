@@ -420,11 +420,12 @@ int fp8_ensure_tiled(Family f, OmegaGpuFp8Tensor *t) {
     Ctx *c = ctx(f);
     if (!c) return OMEGA_GPU_CHIP_FAIL;
     const size_t bytes = (size_t)t->experts * t->n * t->k;
-    OMEGA_HIP(f, hipMalloc(&t->wt, bytes));
+    if (seal_refuses(f, "fp8 tiled weight twin", bytes)) return OMEGA_GPU_TOO_LARGE;
+    OMEGA_HIP(f, dev_malloc(&t->wt, bytes));
     hipError_t e = launch_fp8_tile(t->w, t->wt, t->experts, t->n, t->k, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
-        (void)hipFree(t->wt);
+        (void)dev_free(t->wt);
         t->wt = nullptr;
         set_error(f, "fp8 tiled twin: %s", hipGetErrorString(e));
         return OMEGA_GPU_CHIP_FAIL;
@@ -529,9 +530,9 @@ int omega_gpu_fp8_tensor_upload(uint32_t experts, uint32_t n, uint32_t k, const 
     t->n = n;
     t->k = k;
     uint32_t *flag = nullptr;
-    hipError_t e = hipMalloc(&t->w, wbytes);
-    if (e == hipSuccess) e = hipMalloc(&t->s, ns * 4);
-    if (e == hipSuccess) e = hipMalloc(&flag, 4);
+    hipError_t e = dev_malloc(&t->w, wbytes);
+    if (e == hipSuccess) e = dev_malloc(&t->s, ns * 4);
+    if (e == hipSuccess) e = dev_malloc(&flag, 4);
     if (e == hipSuccess) e = hipMemsetAsync(flag, 0, 4, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(t->w, w, wbytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(t->s, sf.data(), ns * 4, hipMemcpyHostToDevice, c->stream);
@@ -539,18 +540,18 @@ int omega_gpu_fp8_tensor_upload(uint32_t experts, uint32_t n, uint32_t k, const 
     uint32_t nan_seen = 0;
     if (e == hipSuccess) e = hipMemcpyAsync(&nan_seen, flag, 4, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (flag) (void)hipFree(flag);
+    if (flag) (void)dev_free(flag);
     if (e != hipSuccess) {
         set_error(F_FP8, "fp8 upload of %zu bytes: %s", wbytes, hipGetErrorString(e));
-        if (t->w) (void)hipFree(t->w);
-        if (t->s) (void)hipFree(t->s);
+        if (t->w) (void)dev_free(t->w);
+        if (t->s) (void)dev_free(t->s);
         delete t;
         return e == hipErrorOutOfMemory ? OMEGA_GPU_TOO_LARGE : OMEGA_GPU_CHIP_FAIL;
     }
     if (nan_seen) {
         set_error(F_FP8, "NAN_WEIGHT: an e4m3 NaN code (0x7f/0xff) in the weights");
-        (void)hipFree(t->w);
-        (void)hipFree(t->s);
+        (void)dev_free(t->w);
+        (void)dev_free(t->s);
         delete t;
         return OMEGA_GPU_BAD_ARGS;
     }
@@ -612,14 +613,14 @@ int omega_gpu_fp8_tensor_synth(uint32_t experts, uint32_t n, uint32_t k, uint64_
     t->k = k;
     const size_t wbytes = (size_t)experts * n * k;
     const size_t ns = (size_t)experts * (n / 128) * (k / 128);
-    hipError_t e = hipMalloc(&t->w, wbytes);
-    if (e == hipSuccess) e = hipMalloc(&t->s, ns * 4);
+    hipError_t e = dev_malloc(&t->w, wbytes);
+    if (e == hipSuccess) e = dev_malloc(&t->s, ns * 4);
     if (e == hipSuccess) e = launch_fp8_synth(t->w, t->s, experts, n, k, seed, tensor_id, sigma, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         set_error(F_FP8, "fp8 synth: %s", hipGetErrorString(e));
-        if (t->w) (void)hipFree(t->w);
-        if (t->s) (void)hipFree(t->s);
+        if (t->w) (void)dev_free(t->w);
+        if (t->s) (void)dev_free(t->s);
         delete t;
         return e == hipErrorOutOfMemory ? OMEGA_GPU_TOO_LARGE : OMEGA_GPU_CHIP_FAIL;
     }
@@ -632,9 +633,9 @@ void omega_gpu_fp8_tensor_free(OmegaGpuFp8Tensor *t) {
     std::lock_guard<std::recursive_mutex> lk(big_lock());
     Ctx *c = ctx(F_FP8);
     if (c) (void)hipStreamSynchronize(c->stream);
-    if (t->w) (void)hipFree(t->w);
-    if (t->s) (void)hipFree(t->s);
-    if (t->wt) (void)hipFree(t->wt);
+    if (t->w) (void)dev_free(t->w);
+    if (t->s) (void)dev_free(t->s);
+    if (t->wt) (void)dev_free(t->wt);
     delete t;
 }
 

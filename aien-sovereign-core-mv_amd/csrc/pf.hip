@@ -512,19 +512,19 @@ static int pf_alloc(size_t bytes, OmegaGpuMem *out, bool host) {
     void *p = nullptr, *dp = nullptr;
     if (host) {
         // host-visible, not cached by the GPU: the CPU reads and writes it in place
-        OMEGA_HIP(F_SESSION, hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocCoherent));
+        OMEGA_HIP(F_SESSION, host_malloc(&p, bytes, hipHostMallocMapped | hipHostMallocCoherent));
         hipError_t e = hipHostGetDevicePointer(&dp, p, 0);
         if (e != hipSuccess) {
-            (void)hipHostFree(p);
+            (void)host_free(p);
             set_error(F_SESSION, "pf alloc host: hipHostGetDevicePointer: %s", hipGetErrorString(e));
             return OMEGA_GPU_CHIP_FAIL;
         }
         memset(p, 0, bytes);
     } else {
-        OMEGA_HIP(F_SESSION, hipMalloc(&dp, bytes));
+        OMEGA_HIP(F_SESSION, dev_malloc(&dp, bytes));
         hipError_t e = hipMemset(dp, 0, bytes);
         if (e != hipSuccess) {
-            (void)hipFree(dp);
+            (void)dev_free(dp);
             set_error(F_SESSION, "pf alloc dev: hipMemset: %s", hipGetErrorString(e));
             return OMEGA_GPU_CHIP_FAIL;
         }
@@ -549,8 +549,8 @@ void omega_gpu_pf_free(OmegaGpuMem *m) {
     if (!m || !m->va) return;
     Ctx *c = ctx(F_SESSION);
     if (c) (void)hipStreamSynchronize(c->stream);
-    if (m->kind == 1) (void)hipHostFree(m->cpu);
-    else (void)hipFree((void *)(uintptr_t)m->va);
+    if (m->kind == 1) (void)host_free(m->cpu);
+    else (void)dev_free((void *)(uintptr_t)m->va);
     memset(m, 0, sizeof(*m));
 }
 

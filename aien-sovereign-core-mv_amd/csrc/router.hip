@@ -164,17 +164,17 @@ int omega_gpu_router_alloc_shape(uint32_t layers, uint32_t experts, uint32_t sha
     r->shared = shared;
     r->rows = experts + shared;
     r->slots = 8 + shared;
-    hipError_t e = hipMalloc(&r->gate, (size_t)layers * r->rows * 2048 * 2);
-    if (e == hipSuccess) e = hipMalloc(&r->norm, (size_t)layers * 2048 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->dir_gu, (size_t)layers * r->rows * 16);
-    if (e == hipSuccess) e = hipMalloc(&r->dir_dn, (size_t)layers * r->rows * 16);
-    if (e == hipSuccess) e = hipMalloc(&r->xin, 2048 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->xout, 2048 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->logits, 512 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->weights, 16 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->ids, 16 * 4);
-    if (e == hipSuccess) e = hipMalloc(&r->tab_gu, 16 * 16);
-    if (e == hipSuccess) e = hipMalloc(&r->tab_dn, 16 * 16);
+    hipError_t e = dev_malloc(&r->gate, (size_t)layers * r->rows * 2048 * 2);
+    if (e == hipSuccess) e = dev_malloc(&r->norm, (size_t)layers * 2048 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->dir_gu, (size_t)layers * r->rows * 16);
+    if (e == hipSuccess) e = dev_malloc(&r->dir_dn, (size_t)layers * r->rows * 16);
+    if (e == hipSuccess) e = dev_malloc(&r->xin, 2048 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->xout, 2048 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->logits, 512 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->weights, 16 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->ids, 16 * 4);
+    if (e == hipSuccess) e = dev_malloc(&r->tab_gu, 16 * 16);
+    if (e == hipSuccess) e = dev_malloc(&r->tab_dn, 16 * 16);
     if (e == hipSuccess) e = hipMemset(r->gate, 0, (size_t)layers * r->rows * 2048 * 2);
     if (e == hipSuccess) e = hipMemset(r->norm, 0, (size_t)layers * 2048 * 4);
     if (e == hipSuccess) e = hipMemset(r->dir_gu, 0, (size_t)layers * r->rows * 16);
@@ -200,7 +200,7 @@ void omega_gpu_router_free(OmegaGpuRouter *r) {
     void *ps[] = {r->gate, r->norm, r->dir_gu, r->dir_dn, r->xin, r->xout, r->logits,
                   r->weights, r->ids, r->tab_gu, r->tab_dn};
     for (void *p : ps)
-        if (p) (void)hipFree(p);
+        if (p) (void)dev_free(p);
     delete r;
 }
 

@@ -97,25 +97,51 @@ static bool sealed_refusal(Family f, const char *what, size_t bytes, size_t held
     return true;
 }
 
+bool seal_refuses(Family f, const char *what, size_t bytes) { return sealed_refusal(f, what, bytes, 0); }
+
+static hipError_t counted(hipError_t e, size_t bytes) {
+    if (e == hipSuccess) {
+        ++alloc_counters().allocs;
+        alloc_counters().alloc_bytes += bytes;
+    } else {
+        ++alloc_counters().alloc_failures;
+    }
+    return e;
+}
+
+hipError_t dev_malloc(void **p, size_t bytes) { return counted(hipMalloc(p, bytes), bytes); }
+
+hipError_t host_malloc(void **p, size_t bytes, unsigned flags) {
+    return counted(hipHostMalloc(p, bytes, flags), bytes);
+}
+
+hipError_t dev_free(void *p) {
+    if (!p) return hipSuccess;
+    ++alloc_counters().frees;
+    return hipFree(p);
+}
+
+hipError_t host_free(void *p) {
+    if (!p) return hipSuccess;
+    ++alloc_counters().frees;
+    return hipHostFree(p);
+}
+
 bool ensure_pinned(Family f, Ctx *c, size_t bytes) {
     if (c->pin_bytes >= bytes) return true;
     if (sealed_refusal(f, "pinned staging", bytes, c->pin_bytes)) return false;
     if (c->pin) {
         (void)hipStreamSynchronize(c->stream);
-        (void)hipHostFree(c->pin);
-        ++alloc_counters().frees;
+        (void)host_free(c->pin);
     }
     c->pin = nullptr;
     c->pin_bytes = 0;
     size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    hipError_t e = hipHostMalloc(&c->pin, want, hipHostMallocDefault);
+    hipError_t e = host_malloc(&c->pin, want, hipHostMallocDefault);
     if (e != hipSuccess) {
-        ++alloc_counters().alloc_failures;
         set_error(f, "pinned staging of %zu bytes: %s", want, hipGetErrorString(e));
         return false;
     }
-    ++alloc_counters().allocs;
-    alloc_counters().alloc_bytes += want;
     c->pin_bytes = want;
     return true;
 }
@@ -125,20 +151,16 @@ bool ensure_scratch(Family f, Ctx *c, size_t bytes) {
     if (sealed_refusal(f, "device scratch", bytes, c->scratch_bytes)) return false;
     if (c->scratch) {
         (void)hipStreamSynchronize(c->stream);
-        (void)hipFree(c->scratch);
-        ++alloc_counters().frees;
+        (void)dev_free(c->scratch);
     }
     c->scratch = nullptr;
     c->scratch_bytes = 0;
     size_t want = bytes < (4u << 20) ? (4u << 20) : bytes;
-    hipError_t e = hipMalloc(&c->scratch, want);
+    hipError_t e = dev_malloc(&c->scratch, want);
     if (e != hipSuccess) {
-        ++alloc_counters().alloc_failures;
         set_error(f, "device scratch of %zu bytes: %s", want, hipGetErrorString(e));
         return false;
     }
-    ++alloc_counters().allocs;
-    alloc_counters().alloc_bytes += want;
     c->scratch_bytes = want;
     return true;
 }

@@ -49,10 +49,29 @@ Ctx *ctx(Family f);
 // Grow helpers; return false (error set) on allocation failure.
 bool ensure_pinned(Family f, Ctx *c, size_t bytes);
 bool ensure_scratch(Family f, Ctx *c, size_t bytes);
+// Every allocation the library makes goes through these, so the allocation counters
+// (omega_gpu_session_alloc_stats: allocations, bytes, failures, frees since the process started)
+// cover all of them. A null pointer is not freed and not counted.
+hipError_t dev_malloc(void **p, size_t bytes);
+hipError_t host_malloc(void **p, size_t bytes, unsigned flags);
+hipError_t dev_free(void *p);
+hipError_t host_free(void *p);
+template <typename T>
+hipError_t dev_malloc(T **p, size_t bytes) {
+    return dev_malloc(reinterpret_cast<void **>(p), bytes);
+}
+template <typename T>
+hipError_t host_malloc(T **p, size_t bytes, unsigned flags) {
+    return host_malloc(reinterpret_cast<void **>(p), bytes, flags);
+}
+// An allocation that a call makes on its own (not at create / upload time: the tiled weight
+// twins a tensor gets on its first batched use) while the serving reservation is sealed: refused,
+// counted as a stale refusal, the family's error set. Returns true when refused.
+bool seal_refuses(Family f, const char *what, size_t bytes);
 
 // The serving reservation (omega_gpu_reserve_serving / _seal / _release): while sealed, the grow
-// helpers above refuse to allocate (counted as stale refusals); the counters cover every
-// allocation they make.
+// helpers above and the calls' own allocations (seal_refuses) refuse to allocate (counted as
+// stale refusals).
 struct ServingState {
     bool reserved = false, sealed = false;
     OmegaGpuServingBounds bounds{};

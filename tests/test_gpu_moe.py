@@ -164,3 +164,37 @@ def test_a_planner_wait_that_runs_out_is_reported_and_the_next_call_recovers(ome
         np.testing.assert_array_equal(ids, good_ids)
         np.testing.assert_array_equal(w.view(np.uint32), good_w.view(np.uint32))
         np.testing.assert_array_equal(out.view(np.uint32), good.view(np.uint32))
+
+
+def test_allocations_are_counted_and_a_sealed_call_builds_no_twin(omega, oracle, model):
+    # every allocation the library makes is counted (omega_gpu_session_alloc_stats, "driver
+    # allocation counters since the process started", aien-omega-gpu/src/lib.rs:1165-1178); while
+    # the serving reservation is sealed, a call that would build a tensor's tiled twin (its first
+    # batched use) is refused with TOO_LARGE and counted as a stale refusal; release lifts it
+    h = bf16_rows(oracle, np.random.default_rng(17), 32)
+    want, want_ids, _ = omega.moe_batch(model["router"], 0, model["gu"], model["dn"], h, 1e-6)
+    s0 = omega.alloc_stats()  # the scratch and staging of 32 rows exist now
+    gu = omega.Fp8Tensor.synth(E, 2 * I, H, SEED, 2)
+    dn = omega.Fp8Tensor.synth(E, H, I, SEED, 3)
+    s1 = omega.alloc_stats()
+    gu_bytes = E * 2 * I * H + E * (2 * I // 128) * (H // 128) * 4
+    dn_bytes = E * H * I + E * (H // 128) * (I // 128) * 4
+    assert s1["allocs"] == s0["allocs"] + 4                      # weights and scales of each
+    assert s1["alloc_bytes"] == s0["alloc_bytes"] + gu_bytes + dn_bytes
+    try:
+        omega.serving_seal()
+        with pytest.raises(omega.OmegaGpuError, match="reservation exceeded"):
+            omega.moe_batch(model["router"], 0, gu, dn, h, 1e-6)
+        assert omega.alloc_stats()["stale_refusals"] == s1["stale_refusals"] + 1
+        assert omega.alloc_stats()["allocs"] == s1["allocs"]
+    finally:
+        omega.serving_release()
+    out, ids, _ = omega.moe_batch(model["router"], 0, gu, dn, h, 1e-6)  # the same seeded tensors
+    np.testing.assert_array_equal(ids, want_ids)
+    np.testing.assert_array_equal(out.view(np.uint32), want.view(np.uint32))
+    s2 = omega.alloc_stats()
+    assert s2["allocs"] == s1["allocs"] + 2                      # the two tiled twins
+    assert s2["alloc_bytes"] == s1["alloc_bytes"] + E * 2 * I * H + E * H * I
+    gu.free()
+    dn.free()
+    assert omega.alloc_stats()["frees"] == s2["frees"] + 6       # weights, scales and twin of each
