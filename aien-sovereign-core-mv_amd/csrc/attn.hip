@@ -41,7 +41,10 @@
 namespace omega {
 
 
-__global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
+// q|k|v, the position word and the layer's q / k norm weights come in as leading scalar arguments
+// (preloaded into SGPRs), so their loads go out at the first instruction.
+__global__ __launch_bounds__(64) void k_dattn(const float *qkv, const uint32_t *pos_dev, const float *q_norm,
+                                              const float *k_norm, const DattnArgs a) {
     __shared__ __align__(16) DattnLds lds;
     const uint32_t lane = threadIdx.x, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
     // Every load below is issued unconditionally, the page stream last: vector-memory waits
@@ -49,21 +52,21 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
     // here would make the preparation math wait on the page stream. The q|k|v row and the norm
     // weights do not depend on the position, so they go out before the position is read (they
     // travel while it arrives) rather than after the split plan that needs it.
-    const float *qraw = a.qkv + h * 8 * 128;
+    const float *qraw = qkv + h * 8 * 128;
     float q0[8], q1[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
         q0[r] = *as_global_f32(qraw + r * 128 + lane);
         q1[r] = *as_global_f32(qraw + r * 128 + 64 + lane);
     }
-    const float qw0 = *as_global_f32(a.q_norm + lane), qw1 = *as_global_f32(a.q_norm + 64 + lane);
-    const float k0 = *as_global_f32(a.qkv + 4096 + h * 128 + lane);
-    const float k1 = *as_global_f32(a.qkv + 4096 + h * 128 + 64 + lane);
-    const float v0 = *as_global_f32(a.qkv + 4608 + h * 128 + lane);
-    const float v1 = *as_global_f32(a.qkv + 4608 + h * 128 + 64 + lane);
-    const float kw0 = *as_global_f32(a.k_norm + lane);
-    const float kw1 = *as_global_f32(a.k_norm + 64 + lane);
-    const uint32_t pos = a.pos_dev ? *as_global_u32(a.pos_dev) : a.pos_host;
+    const float qw0 = *as_global_f32(q_norm + lane), qw1 = *as_global_f32(q_norm + 64 + lane);
+    const float k0 = *as_global_f32(qkv + 4096 + h * 128 + lane);
+    const float k1 = *as_global_f32(qkv + 4096 + h * 128 + 64 + lane);
+    const float v0 = *as_global_f32(qkv + 4608 + h * 128 + lane);
+    const float v1 = *as_global_f32(qkv + 4608 + h * 128 + 64 + lane);
+    const float kw0 = *as_global_f32(k_norm + lane);
+    const float kw1 = *as_global_f32(k_norm + 64 + lane);
+    const uint32_t pos = pos_dev ? *as_global_u32(pos_dev) : a.pos_host;
     const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
     uint32_t active, pps;
     attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(64) void k_dattn(const DattnArgs a) {
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_dattn, dim3(4, a.splits), dim3(64), 0, st, a);
+    OMEGA_LAUNCH(k_dattn, dim3(4, a.splits), dim3(64), 0, st, a.qkv, a.pos_dev, a.q_norm, a.k_norm, a);
     return hipGetLastError();
 }
 

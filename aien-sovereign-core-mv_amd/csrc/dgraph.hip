@@ -67,7 +67,11 @@ struct GateUpArgs {
 
 constexpr uint32_t kGuPairs = 2;  // gate/up row pairs per wavefront
 
-__global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
+// The logits and the normed row come in as leading scalar arguments (preloaded into SGPRs), so
+// the two loads every workgroup waits on go out at the first instruction. FORCED: the parity
+// tests' forced routes (a.forced set), decided at launch.
+template <bool FORCED>
+__global__ __launch_bounds__(256) void k_gate_up(const float *logits, const float *xn, const GateUpArgs a) {
     using S = Fp8Slab<kHidden, kGuPairs>;
     constexpr int P = S::P;
     __shared__ uint32_t sh_id[kTopK];
@@ -77,15 +81,15 @@ __global__ __launch_bounds__(256) void k_gate_up(const GateUpArgs a) {
     const uint32_t item = blockIdx.x * 4 + wid;
     const uint32_t slot = item / (kInter / kGuPairs), j0 = (item % (kInter / kGuPairs)) * kGuPairs;
     static_assert(kHidden == 8 * 256, "two float4 of the row per thread");
-    const f32x4 xt0 = *as_global_f32x4(a.xn + 4 * threadIdx.x);
-    const f32x4 xt1 = *as_global_f32x4(a.xn + 1024 + 4 * threadIdx.x);
+    const f32x4 xt0 = *as_global_f32x4(xn + 4 * threadIdx.x);
+    const f32x4 xt1 = *as_global_f32x4(xn + 1024 + 4 * threadIdx.x);
     // wavefront 0 ranks the logits for the workgroup (its logits load goes out right behind the
     // row's: the row is written to LDS after the ranking)
     if (wid == 0) {
         Route r;
         // parity tests: the layer's forced ids, unless its row asks for the ranking
-        if (a.forced && *as_global_u32(a.forced) != OMEGA_GPU_DGRAPH_RANK) route_forced(a.logits, a.forced, r);
-        else route_topk<kExperts / 64>(a.logits, 0, a.norm_topk, a.route_mutant, r);
+        if (FORCED && *as_global_u32(a.forced) != OMEGA_GPU_DGRAPH_RANK) route_forced(logits, a.forced, r);
+        else route_topk<kExperts / 64>(logits, 0, a.norm_topk, a.route_mutant, r);
         if (lane == 0) {
 #pragma unroll
             for (int s = 0; s < kTopK; ++s) {
@@ -157,22 +161,24 @@ struct DownArgs {
 
 constexpr uint32_t kDnRows = 8;  // output rows per workgroup (one wavefront per slot)
 
-__global__ __launch_bounds__(512) void k_down(const DownArgs a) {
+// The route, the SwiGLU rows, the route weights, the residual row and the test mutant come in as
+// leading scalar arguments (preloaded into SGPRs): the route load, which every weight address
+// waits on, goes out at the first instruction.
+__global__ __launch_bounds__(512) void k_down(const uint32_t *ids, const float *act, const float *weights,
+                                              const float *xin, int graph_mutant, const DownArgs a) {
     using S = Fp8Slab<kInter, kDnRows>;
     constexpr int P = S::P;
     __shared__ float red[kTopK][kDnRows];
     const uint32_t lane = lane_id();
     const uint32_t slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: e by s_load
     const uint32_t row0 = blockIdx.x * kDnRows;
-    int graph_mutant = a.graph_mutant;
-    asm volatile("" : "+s"(graph_mutant));  // read with the other arguments, not after the dot
     // every small load goes ahead of the weight stream (the route weights and the residual rows
     // of the epilogue included), so no round trip is left after the dot
-    const uint32_t e = a.ids[slot];
+    const uint32_t e = ids[slot];
     float xr[P][16];
-    S::load_x(a.act + slot * kInter, lane, xr);
-    const float wraw = *as_global_f32(a.weights + (lane & (kTopK - 1)));  // lane s: slot s's weight
-    const float xres = a.xin ? *as_global_f32(a.xin + row0 + (lane & (kDnRows - 1))) : 0.f;
+    S::load_x(act + slot * kInter, lane, xr);
+    const float wraw = *as_global_f32(weights + (lane & (kTopK - 1)));  // lane s: slot s's weight
+    const float xres = xin ? *as_global_f32(xin + row0 + (lane & (kDnRows - 1))) : 0.f;
     float sc[P];
     S::load_scales(a.s + ((size_t)e * (kHidden / 128) + (row0 >> 7)) * (kInter / 128), lane, 1.0f,
                    graph_mutant == 5 ? 1 : 0, sc);
@@ -198,6 +204,19 @@ __global__ __launch_bounds__(512) void k_down(const DownArgs a) {
     }
 }
 
+static hipError_t launch_gate_up(const GateUpArgs &gu, hipStream_t st) {
+    const dim3 grid(kTopK * (kInter / kGuPairs) / 4);
+    if (gu.forced) OMEGA_LAUNCH(k_gate_up<true>, grid, dim3(256), 0, st, gu.logits, gu.xn, gu);
+    else OMEGA_LAUNCH(k_gate_up<false>, grid, dim3(256), 0, st, gu.logits, gu.xn, gu);
+    return hipGetLastError();
+}
+
+static hipError_t launch_down(const DownArgs &dn, hipStream_t st) {
+    OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn.ids, dn.act, dn.weights, dn.xin,
+                 dn.graph_mutant, dn);
+    return hipGetLastError();
+}
+
 // The MoE block of one token as the decode step runs it: router logits and x' (ra), then gate|up
 // with the top-8 ranking in its prologue and SwiGLU, then down with the slot-order combine into
 // out (plus resid when given). ra.ids / ra.weights receive the route; act holds [8][768].
@@ -216,7 +235,8 @@ hipError_t launch_moe_one_token(const RouterArgs &ra, const uint8_t *gu_w, const
     gu.act = act;
     gu.ids = ra.ids;
     gu.weights = ra.weights;
-    OMEGA_LAUNCH(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
+    e = launch_gate_up(gu, st);
+    if (e != hipSuccess) return e;
     DownArgs dn;
     dn.w = dn_w;
     dn.s = dn_s;
@@ -225,8 +245,7 @@ hipError_t launch_moe_one_token(const RouterArgs &ra, const uint8_t *gu_w, const
     dn.act = act;
     dn.xin = resid;
     dn.x = out;
-    OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
-    return hipGetLastError();
+    return launch_down(dn, st);
 }
 
 }  // namespace omega
@@ -452,8 +471,7 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         gu.forced = g->force_on ? g->forced + (size_t)l * 8 : nullptr;
         gu.graph_mutant = g->mutant;
         arm();
-        OMEGA_LAUNCH(k_gate_up, dim3(kTopK * (kInter / kGuPairs) / 4), dim3(256), 0, st, gu);
-        OMEGA_HIP(F_SESSION, hipGetLastError());
+        OMEGA_HIP(F_SESSION, launch_gate_up(gu, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_GATE_UP));
         // 7. down of the 8 experts, weighted combine + residual
         DownArgs dn;
@@ -466,16 +484,14 @@ int enqueue_token(OmegaGpuDecodeGraph *g, hipStream_t st, std::vector<uint8_t> &
         dn.x = g->x;
         dn.graph_mutant = g->mutant;
         arm();
-        OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, dn);
-        OMEGA_HIP(F_SESSION, hipGetLastError());
+        OMEGA_HIP(F_SESSION, launch_down(dn, st));
         OMEGA_HIP(F_SESSION, mark(OMEGA_GPU_DGRAPH_K_DOWN));
         if (tr) {
             // the combine alone (no residual read) is the sum the fused launch added
             DownArgs d2 = dn;
             d2.xin = nullptr;
             d2.x = tr + kTrMoe;
-            OMEGA_LAUNCH(k_down, dim3(kHidden / kDnRows), dim3(512), 0, st, d2);
-            OMEGA_HIP(F_SESSION, hipGetLastError());
+            OMEGA_HIP(F_SESSION, launch_down(d2, st));
             OMEGA_HIP(F_SESSION, trace_copy(kTrIds, ra.ids, kTopK * 4));
             OMEGA_HIP(F_SESSION, trace_copy(kTrW, ra.weights, kTopK * 4));
             OMEGA_HIP(F_SESSION, trace_copy(kTrOut, g->x, kHidden * 4));

@@ -41,8 +41,18 @@ __device__ __forceinline__ void group_tensor(const Fp8RowsArgs &a, uint32_t g, u
 // so the activation row (and the norm weights) is staged once per workgroup in LDS instead of
 // once per wavefront — a CU's loads share one path, and the replicated activation bytes would
 // otherwise double its traffic.
-template <int K, int RPW, int EPI, int XSRC, bool XL>
-__global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
+//
+// ONE: one group, no group table, n / RPW a multiple of 4 (the decode projections): the
+// expert's weight and scale pointers, the activation row, the norm weights, the output row and
+// the test mutant come in as leading scalar kernel arguments, which gfx950 preloads into SGPRs
+// before the wave starts (-amdgpu-kernarg-preload-count), so the loads ahead of the weight
+// stream wait on no scalar round trip; every wavefront is live. The general form reads the
+// group's expert id, then its table entry, from the arguments: a chain of dependent scalar
+// loads (0.29 us per q|k|v launch, measured) ahead of the stream.
+template <int K, int RPW, int EPI, int XSRC, bool XL, bool ONE>
+__device__ __forceinline__ void fp8_rows_body(const Fp8RowsArgs &a, const uint8_t *w1, const float *s1,
+                                              const float *x1, const float *nw1, float *y1,
+                                              int mut1) {
     using S = Fp8Slab<K, RPW>;
     constexpr int P = S::P;
     constexpr int NX = (K / 4 + 255) / 256;  // float4 of the row per thread when staged
@@ -52,14 +62,18 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     // wave-uniform (scalar registers): the group's weight pointer then comes from a scalar
     // kernel-argument load instead of a vector round trip ahead of the weight stream
     const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    const uint32_t per_group = a.n / RPW;
-    const bool live = wave < a.groups * per_group;
+    const uint32_t per_group = ONE ? 0 : a.n / RPW;
+    const bool live = ONE || wave < a.groups * per_group;
     if (!XL && !live) return;  // with XL every thread takes part in the staging and its barrier
     const uint32_t wv = live ? wave : 0;  // a wavefront past the end streams row 0, unused
-    const uint32_t g = wv / per_group, row0 = (wv % per_group) * RPW;
-    const uint8_t *wexp;
-    const float *sexp;
-    group_tensor(a, g, K, wexp, sexp);
+    const uint32_t g = ONE ? 0 : wv / per_group, row0 = (ONE ? wv : wv % per_group) * RPW;
+    const uint8_t *wexp = w1;
+    const float *sexp = s1;
+    if constexpr (!ONE) group_tensor(a, g, K, wexp, sexp);
+    const float *xrow = ONE ? x1 : a.x + (size_t)g * a.x_stride;
+    const float *norm_w = ONE ? nw1 : a.norm_w;
+    float *y = ONE ? y1 : a.y;
+    const int mutant = ONE ? mut1 : a.mutant;
 
     // every small load (activation row or phases, norm weights, block scales) goes ahead of the
     // weight stream: vector-memory waits complete in issue order, so waiting on any of them then
@@ -76,31 +90,31 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
         } else {
 #pragma unroll
             for (int i = 0; i < NX; ++i)
-                xt[i] = *as_global_f32x4(a.x + (size_t)g * a.x_stride + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
+                xt[i] = *as_global_f32x4(xrow + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
         }
         if (XSRC != XS_F32) {
 #pragma unroll
             for (int i = 0; i < NX; ++i)
-                wt[i] = *as_global_f32x4(a.norm_w + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
+                wt[i] = *as_global_f32x4(norm_w + 4 * min(threadIdx.x + 256 * i, (uint32_t)K / 4 - 1));
         }
     } else {
         if (XSRC == XS_EMBED_NORM) {
             const uint32_t tok = *as_global_u32(a.embed_tok) % a.embed_rows;
             S::load_x_bf16(a.embed + (size_t)tok * K, lane, xr);
         } else {
-            S::load_x(a.x + (size_t)g * a.x_stride, lane, xr);
+            S::load_x(xrow, lane, xr);
         }
-        if (XSRC != XS_F32) S::load_x(a.norm_w, lane, nw);
+        if (XSRC != XS_F32) S::load_x(norm_w, lane, nw);
     }
     __builtin_amdgcn_sched_barrier(0);  // the activation loads stay ahead of everything below
     // block scales of row0's 128-row block, and of the last row's when RPW does not divide 128
     float sc[2][P];
-    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc[0]);
+    S::load_scales(sexp + (size_t)(row0 >> 7) * (K >> 7), lane, 1.0f, mutant, sc[0]);
     if constexpr (!S::kOneBlock)
-        S::load_scales(sexp + (size_t)((row0 + RPW - 1) >> 7) * (K >> 7), lane, 1.0f, a.mutant, sc[1]);
+        S::load_scales(sexp + (size_t)((row0 + RPW - 1) >> 7) * (K >> 7), lane, 1.0f, mutant, sc[1]);
     // the residual row of the epilogue, read now rather than after the dot
-    const size_t yrow = (size_t)g * a.n + row0 + min(lane, (uint32_t)RPW - 1);
-    const float yres = EPI == EPI_RESID ? *as_global_f32(a.y + yrow) : 0.f;
+    const size_t yrow = (ONE ? 0 : (size_t)g * a.n) + row0 + min(lane, (uint32_t)RPW - 1);
+    const float yres = EPI == EPI_RESID ? *as_global_f32(y + yrow) : 0.f;
     S slab;
     slab.load(wexp + (size_t)row0 * K, lane);
     // every load is issued before any arithmetic (the scheduler would otherwise sink the weight
@@ -154,7 +168,20 @@ __global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
     if constexpr (S::kOneBlock) slab.dot(xr, sc[0], acc, lane);
     else slab.dot2(xr, sc, row0, acc);
     const float v = reduce_rows(acc, lane) * scale;
-    if (live && lane < (uint32_t)RPW) a.y[yrow] = EPI == EPI_STORE ? v : yres + v;
+    if (live && lane < (uint32_t)RPW) y[yrow] = EPI == EPI_STORE ? v : yres + v;
+}
+
+template <int K, int RPW, int EPI, int XSRC, bool XL>
+__global__ __launch_bounds__(256) void k_fp8_rows(const Fp8RowsArgs a) {
+    fp8_rows_body<K, RPW, EPI, XSRC, XL, false>(a, nullptr, nullptr, nullptr, nullptr, nullptr, 0);
+}
+
+// w and s point at the expert's own rows (the host adds the group's expert offset)
+template <int K, int RPW, int EPI, int XSRC>
+__global__ __launch_bounds__(256) void k_fp8_rows1(const uint8_t *w, const float *s, const float *x,
+                                                  const float *norm_w, float *y, int mutant,
+                                                  const Fp8RowsArgs a) {
+    fp8_rows_body<K, RPW, EPI, XSRC, true, true>(a, w, s, x, norm_w, y, mutant);
 }
 
 // Any k (a multiple of 128 up to 32768): rows per wavefront rpw = 1024 / gcd(k, 1024) <= 8,
@@ -236,8 +263,15 @@ static hipError_t launch_k(const Fp8RowsArgs &a, hipStream_t st) {
     const uint32_t waves = a.groups * (a.n / RPW);
     // the activation row is staged per workgroup when the workgroup's wavefronts share a group
     const bool xl = a.groups == 1 || (a.n / RPW) % 4 == 0;
-    if (xl) OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, true>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
-    else OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, false>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    if (a.groups == 1 && !a.tab && waves % 4 == 0) {
+        const size_t e = a.ids[0];
+        OMEGA_LAUNCH((k_fp8_rows1<K, RPW, EPI, XSRC>), dim3(waves / 4), dim3(256), 0, st,
+                     a.w + e * a.n * K, a.s + e * (a.n >> 7) * (K >> 7), a.x, a.norm_w, a.y, a.mutant, a);
+    } else if (xl) {
+        OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, true>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    } else {
+        OMEGA_LAUNCH((k_fp8_rows<K, RPW, EPI, XSRC, false>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

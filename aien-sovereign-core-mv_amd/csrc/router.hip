@@ -24,17 +24,20 @@ namespace omega {
 
 constexpr uint32_t kRouterHidden = 2048;
 
-__global__ __launch_bounds__(256) void k_router_logits(const RouterArgs a) {
+// x, the norm weights and the gate rows come in as leading scalar arguments (preloaded into
+// SGPRs), so their loads go out at the first instruction.
+__global__ __launch_bounds__(256) void k_router_logits(const float *x, const float *norm_w, const uint16_t *gate,
+                                                       const RouterArgs a) {
     using S = Bf16Slab<kRouterHidden, 1>;
     constexpr int P = S::P;
     const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * 4 + wid;
     const uint32_t rows = a.experts + a.shared;
     float xr[P][8], nw[P][8];
-    S::load_x(a.x, lane, xr);
-    S::load_x(a.norm_w, lane, nw);
+    S::load_x(x, lane, xr);
+    S::load_x(norm_w, lane, nw);
     S slab;
-    if (row < rows) slab.load(a.gate + (size_t)row * kRouterHidden, lane);
+    if (row < rows) slab.load(gate + (size_t)row * kRouterHidden, lane);
     const float scale = rms_scale(phases_sumsq(xr), kRouterHidden, a.eps);
 #pragma unroll
     for (int ph = 0; ph < P; ++ph)
@@ -87,7 +90,7 @@ __global__ __launch_bounds__(64) void k_router_topk(const RouterArgs a) {
 
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st) {
     const uint32_t rows = a.experts + a.shared;
-    OMEGA_LAUNCH(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a);
+    OMEGA_LAUNCH(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a.x, a.norm_w, a.gate, a);
     return hipGetLastError();
 }
 
