@@ -161,9 +161,10 @@ def cpu_baseline(threads, ctx):
                       f"lm_head {one['ms_lm_head']} ms, {one['s_per_token']} s/token"}
 
 
-def committed_traffic(kind):
-    """HBM bytes per launch of `kind` from the committed rocprofv3 PMC summary, if any."""
-    p = os.path.join(REPO, "profiles", f"{kind}_traffic.md")
+def committed_traffic(kind, summary=None):
+    """HBM bytes per launch of `kind` from the committed rocprofv3 PMC summary (profiles/
+    <kind>_traffic.md, or the file `summary` there), if any."""
+    p = os.path.join(REPO, "profiles", summary or f"{kind}_traffic.md")
     if not os.path.exists(p):
         return None
     for line in open(p):
@@ -272,8 +273,9 @@ def bench_gemv(om, args):
         "data": "synthetic N(0, 0.02) weights block-quantised to e4m3, bf16 N(0,1) row",
         "config": {"workload": "q|k|v GEMV 5120 x 2048, 48 weight copies, "
                                + ("48 direct launches" if args.eager else "hipGraph of 48 launches")},
-        "roofline": {"bound": "hbm", "kernel": "k_fp8_rows", "achieved": round(gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "k_fp8_rows1", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4),
+                     "traffic": committed_traffic(None, "gemv_config1_kernel_trace.md")},
         "cpu_baseline": cpu}), flush=True)
     for t in ts:
         t.free()
