@@ -84,18 +84,26 @@ __global__ __launch_bounds__(256) void k_gate_up(const float *logits, const floa
     const f32x4 xt0 = *as_global_f32x4(xn + 4 * threadIdx.x);
     const f32x4 xt1 = *as_global_f32x4(xn + 1024 + 4 * threadIdx.x);
     // wavefront 0 ranks the logits for the workgroup (its logits load goes out right behind the
-    // row's: the row is written to LDS after the ranking)
+    // row's: the row is written to LDS after the ranking). Workgroup 0 ranks all 8 slots and
+    // weighs them (it publishes the route); every other workgroup needs its own slot's id only,
+    // which the first slot + 1 rounds decide, so its stream starts that many rounds in.
     if (wid == 0) {
-        Route r;
         // parity tests: the layer's forced ids, unless its row asks for the ranking
-        if (FORCED && *as_global_u32(a.forced) != OMEGA_GPU_DGRAPH_RANK) route_forced(logits, a.forced, r);
-        else route_topk<kExperts / 64>(logits, 0, a.norm_topk, a.route_mutant, r);
-        if (lane == 0) {
+        const bool forced = FORCED && *as_global_u32(a.forced) != OMEGA_GPU_DGRAPH_RANK;
+        if (forced || blockIdx.x == 0) {
+            Route r;
+            if (forced) route_forced(logits, a.forced, r);
+            else route_topk<kExperts / 64>(logits, 0, a.norm_topk, a.route_mutant, r);
+            if (lane == 0) {
 #pragma unroll
-            for (int s = 0; s < kTopK; ++s) {
-                sh_id[s] = a.graph_mutant == 4 ? (r.id[s] + 1) % kExperts : r.id[s];
-                sh_w[s] = r.w[s];
+                for (int s = 0; s < kTopK; ++s) {
+                    sh_id[s] = a.graph_mutant == 4 ? (r.id[s] + 1) % kExperts : r.id[s];
+                    sh_w[s] = r.w[s];
+                }
             }
+        } else {
+            const uint32_t id = route_slot_id<kExperts / 64>(logits, slot + 1, a.route_mutant);
+            if (lane == 0) sh_id[slot] = a.graph_mutant == 4 ? (id + 1) % kExperts : id;
         }
     }
     reinterpret_cast<f32x4 *>(xs)[threadIdx.x] = xt0;

@@ -60,14 +60,16 @@ __device__ __forceinline__ void route_keys(const float *logits, uint32_t (&k)[Q]
 // logits: Q * 64 expert values (+1 shared), read through `logit(id)` (global memory or an LDS
 // copy), their keys already loaded (the keys are consumed).
 // mutant 2: the mask after a pick hits id ^ 1; mutant 4: weights not normalised.
-template <int Q, typename Logit>
-__device__ __forceinline__ void route_topk_keys_r(uint32_t (&k)[Q], Logit logit, uint32_t shared,
-                                                  int norm_topk, int mutant, Route &r) {
-    constexpr uint32_t experts = 64 * Q;
+// The picks of slots 0 .. rounds - 1 (ids and logits; rounds uniform, 1..kTopK): a slot's pick
+// depends on the earlier rounds only. Returns the last pick's id.
+template <int Q>
+__device__ __forceinline__ uint32_t route_rounds(uint32_t (&k)[Q], uint32_t rounds, int mutant, Route &r,
+                                                 float (&v)[kTopK]) {
     const uint32_t lane = lane_id();
-    float v[kTopK];
+    uint32_t last = 0;
 #pragma unroll
     for (int s = 0; s < kTopK; ++s) {
+        if ((uint32_t)s >= rounds) break;
         uint32_t m = k[0];
 #pragma unroll
         for (int q = 1; q < Q; ++q) m = max(m, k[q]);
@@ -80,12 +82,22 @@ __device__ __forceinline__ void route_topk_keys_r(uint32_t (&k)[Q], Logit logit,
             if (b) id = 64 * q + (uint32_t)(__ffsll((long long)b) - 1);
         }
         r.id[s] = id;
+        last = id;
         v[s] = key_value((int32_t)(m ^ 0x80000000u));
         const uint32_t mask_id = mutant == 2 ? (id ^ 1u) : id;
 #pragma unroll
         for (int q = 0; q < Q; ++q)
             if (lane + 64 * q == mask_id) k[q] = 0;
     }
+    return last;
+}
+
+template <int Q, typename Logit>
+__device__ __forceinline__ void route_topk_keys_r(uint32_t (&k)[Q], Logit logit, uint32_t shared,
+                                                  int norm_topk, int mutant, Route &r) {
+    constexpr uint32_t experts = 64 * Q;
+    float v[kTopK];
+    route_rounds<Q>(k, kTopK, mutant, r, v);
     const float mx = v[0];
     float p[kTopK];
     float sum = 0.f;
@@ -137,6 +149,16 @@ __device__ __forceinline__ void route_forced_r(Logit logit, const uint32_t *forc
 }
 __device__ __forceinline__ void route_forced(const float *logits, const uint32_t *forced, Route &r) {
     route_forced_r([&](uint32_t id) { return *as_global_f32(logits + id); }, forced, r);
+}
+
+// the id of slot rounds - 1 alone (rounds uniform, 1..kTopK), no weights
+template <int Q>
+__device__ __forceinline__ uint32_t route_slot_id(const float *logits, uint32_t rounds, int mutant) {
+    uint32_t k[Q];
+    float v[kTopK];
+    Route r;
+    route_keys<Q>(logits, k);
+    return route_rounds<Q>(k, rounds, mutant, r, v);
 }
 
 template <int Q>
