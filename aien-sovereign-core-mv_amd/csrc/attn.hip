@@ -42,11 +42,16 @@ namespace omega {
 
 
 // q|k|v, the position word and the layer's q / k norm weights come in as leading scalar arguments
-// (preloaded into SGPRs), so their loads go out at the first instruction.
-__global__ __launch_bounds__(64) void k_dattn(const float *qkv, const uint32_t *pos_dev, const float *q_norm,
-                                              const float *k_norm, const DattnArgs a) {
+// (preloaded into SGPRs), so their loads go out at the first instruction. Workgroups of two
+// wavefronts: wavefront 0 is the split; in split 0's workgroup wavefront 1 does this token's part
+// (k's norm and RoPE, the K/V append, the token's score and V row, handed over in LDS) beside the
+// page stream, and in every other workgroup it ends at once.
+__global__ __launch_bounds__(128) void k_dattn(const float *qkv, const uint32_t *pos_dev, const float *q_norm,
+                                               const float *k_norm, const DattnArgs a) {
     __shared__ __align__(16) DattnLds lds;
-    const uint32_t lane = threadIdx.x, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
+    const uint32_t lane = threadIdx.x & 63, h = blockIdx.x, s = blockIdx.y;  // kv head fastest
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wv == 1 && s != 0) return;
     // Every load below is issued unconditionally, the page stream last: vector-memory waits
     // complete in issue order and merge conservatively at branch joins, so a conditional load
     // here would make the preparation math wait on the page stream. The q|k|v row and the norm
@@ -67,6 +72,14 @@ __global__ __launch_bounds__(64) void k_dattn(const float *qkv, const uint32_t *
     const float kw0 = *as_global_f32(k_norm + lane);
     const float kw1 = *as_global_f32(k_norm + 64 + lane);
     const uint32_t pos = pos_dev ? *as_global_u32(pos_dev) : a.pos_host;
+    if (wv == 1) {  // split 0's token wavefront
+        const float rc = *as_global_f32(a.rope_cos + (size_t)pos * 64 + lane);
+        const float rs = *as_global_f32(a.rope_sin + (size_t)pos * 64 + lane);
+        dattn_q_prep(a, q0, q1, qw0, qw1, rc, rs, lane);
+        dattn_token(a, h, pos, q0, q1, k0, k1, v0, v1, kw0, kw1, rc, rs, lds, lane);
+        __syncthreads();  // L.vs / L.sp complete for wavefront 0's token step
+        return;
+    }
     const uint32_t pages = (pos + kDattnPage - 1) / kDattnPage;
     uint32_t active, pps;
     attn_split_plan(pages, gridDim.y, a.tiles_per_split, active, pps);
@@ -82,8 +95,8 @@ __global__ __launch_bounds__(64) void k_dattn(const float *qkv, const uint32_t *
     dattn_load(a, h, p_begin < p_end ? p_begin : 0, lane, T);
     __builtin_amdgcn_sched_barrier(0);  // all of the above is issued before any arithmetic
     const uint32_t epoch = a.epoch_dev ? *as_global_u32(a.epoch_dev) * 64u + a.layer : a.epoch_host;
-    dattn_split(a, h, s, pos, holds, p_begin, p_end, q0, q1, k0, k1, v0, v1, qw0, qw1, kw0, kw1, rc, rs, T, lds,
-                epoch, lane);
+    dattn_split<true>(a, h, s, pos, holds, p_begin, p_end, q0, q1, k0, k1, v0, v1, qw0, qw1, kw0, kw1, rc, rs, T,
+                      lds, epoch, lane);
     if (s >= 8) return;
     // Merge of q head 8 h + s: wait until every split of kv head h has flagged this epoch (every
     // split is resident: at most 4 x 64 one-wavefront workgroups), with a bounded number of polls
@@ -110,7 +123,7 @@ __global__ __launch_bounds__(64) void k_dattn(const float *qkv, const uint32_t *
 }
 
 hipError_t launch_dattn(const DattnArgs &a, hipStream_t st) {
-    OMEGA_LAUNCH(k_dattn, dim3(4, a.splits), dim3(64), 0, st, a.qkv, a.pos_dev, a.q_norm, a.k_norm, a);
+    OMEGA_LAUNCH(k_dattn, dim3(4, a.splits), dim3(128), 0, st, a.qkv, a.pos_dev, a.q_norm, a.k_norm, a);
     return hipGetLastError();
 }
 

@@ -107,36 +107,27 @@ struct DattnLds {
     float sp[8];              // split 0: this token's score per head
 };
 
-// One (split s, kv head h) wavefront, from its kv head's raw q|k|v values (lane l holds dims l
-// and l + 64 of the 8 q heads in q0 / q1, of k in k0 / k1 and of v in v0 / v1), the layer's
-// q / k norm weights (the same dims), the position's RoPE factors (pair l) and the split's first
-// page already loading in T. The 8 heads' RMSNorm scales come from one transposed f64
-// reduction; split 0 appends this token's K/V to the cache and scores it; the split's pages
-// [p_begin, p_end) run on the matrix cores, each with the next page's loads in flight. When the
-// split holds pages or is split 0 (`holds`), its partial goes out with agent-scope stores (written
-// through the XCD's L2) and, once they are acknowledged, its flag carries `epoch`. Only this
-// wavefront touches L.
-__device__ __forceinline__ void dattn_split(const DattnArgs &a, uint32_t h, uint32_t s, uint32_t pos, bool holds,
-                                            uint32_t p_begin, uint32_t p_end, float (&q0)[8], float (&q1)[8],
-                                            float k0, float k1, float v0, float v1, float qw0, float qw1,
-                                            float kw0, float kw1, float rc, float rs, DattnPage &T,
-                                            DattnLds &L, uint32_t epoch, uint32_t lane) {
-    const uint32_t g = lane >> 4, n = lane & 15;
-    // the 8 heads' f64 sums of squares in one reduction; lane l then holds head l / 8's scale
+// The 8 q heads' RMSNorm and RoPE in place: the f64 sums of squares in one reduction, after which
+// lane l holds head l / 8's scale.
+__device__ __forceinline__ void dattn_q_prep(const DattnArgs &a, float (&q0)[8], float (&q1)[8], float qw0,
+                                             float qw1, float rc, float rs, uint32_t lane) {
     const bool rope = a.mutant != 1;
     double ss[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) ss[r] = (double)q0[r] * (double)q0[r] + (double)q1[r] * (double)q1[r];
     const float scale_l = rms_scale(head_sums8(ss, lane), 128, a.eps);
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        head_scale_rope(q0[r], q1[r], readlane_f32(scale_l, 8 * r), qw0, qw1, rc, rs, rope);
-        L.qhl[0][r][lane] = bf16_split_hi(q0[r]);
-        L.qhl[1][r][lane] = bf16_split_lo(q0[r]);
-        L.qhl[0][r][lane + 64] = bf16_split_hi(q1[r]);
-        L.qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
-    }
-    if (s == 0) {
+    for (int r = 0; r < 8; ++r) head_scale_rope(q0[r], q1[r], readlane_f32(scale_l, 8 * r), qw0, qw1, rc, rs, rope);
+}
+
+// This token's part of split 0, from the prepared q heads: k's RMSNorm and RoPE, the bf16 K/V
+// append to the cache, the token's V row (as stored) and its score per head into L.
+__device__ __forceinline__ void dattn_token(const DattnArgs &a, uint32_t h, uint32_t pos, const float (&q0)[8],
+                                            const float (&q1)[8], float k0, float k1, float v0, float v1,
+                                            float kw0, float kw1, float rc, float rs, DattnLds &L,
+                                            uint32_t lane) {
+    const bool rope = a.mutant != 1;
+    {
         const float kscale = rms_scale(wave_sum_f64((double)k0 * (double)k0 + (double)k1 * (double)k1), 128, a.eps);
         head_scale_rope(k0, k1, kscale, kw0, kw1, rc, rs, rope);
         const uint16_t kb0 = bf16_rne(k0), kb1 = bf16_rne(k1);
@@ -162,6 +153,36 @@ __device__ __forceinline__ void dattn_split(const DattnArgs &a, uint32_t h, uint
         const float sp = head_sums8(d, lane) * kInvSqrt128;
         if ((lane & 7) == 0) L.sp[lane >> 3] = sp;
     }
+}
+
+// One (split s, kv head h) wavefront, from its kv head's raw q|k|v values (lane l holds dims l
+// and l + 64 of the 8 q heads in q0 / q1, of k in k0 / k1 and of v in v0 / v1), the layer's
+// q / k norm weights (the same dims), the position's RoPE factors (pair l) and the split's first
+// page already loading in T. The 8 heads' RMSNorm scales come from one transposed f64
+// reduction; split 0 appends this token's K/V to the cache and scores it; the split's pages
+// [p_begin, p_end) run on the matrix cores, each with the next page's loads in flight. When the
+// split holds pages or is split 0 (`holds`), its partial goes out with agent-scope stores (written
+// through the XCD's L2) and, once they are acknowledged, its flag carries `epoch`. Only this
+// wavefront touches L (with TOK_SEPARATE, the token wavefront writes L.vs / L.sp).
+// TOK_SEPARATE: split 0's token part (dattn_token) runs on a second wavefront of the workgroup,
+// which writes L.vs / L.sp and then meets this one at a barrier just before the token's
+// online-softmax step; this wavefront streams its pages meanwhile. The values are the same.
+template <bool TOK_SEPARATE = false>
+__device__ __forceinline__ void dattn_split(const DattnArgs &a, uint32_t h, uint32_t s, uint32_t pos, bool holds,
+                                            uint32_t p_begin, uint32_t p_end, float (&q0)[8], float (&q1)[8],
+                                            float k0, float k1, float v0, float v1, float qw0, float qw1,
+                                            float kw0, float kw1, float rc, float rs, DattnPage &T,
+                                            DattnLds &L, uint32_t epoch, uint32_t lane) {
+    const uint32_t g = lane >> 4, n = lane & 15;
+    dattn_q_prep(a, q0, q1, qw0, qw1, rc, rs, lane);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        L.qhl[0][r][lane] = bf16_split_hi(q0[r]);
+        L.qhl[1][r][lane] = bf16_split_lo(q0[r]);
+        L.qhl[0][r][lane + 64] = bf16_split_hi(q1[r]);
+        L.qhl[1][r][lane + 64] = bf16_split_lo(q1[r]);
+    }
+    if (s == 0 && !TOK_SEPARATE) dattn_token(a, h, pos, q0, q1, k0, k1, v0, v1, kw0, kw1, rc, rs, L, lane);
     // qhl / vs / sp complete: one wavefront wrote them, so its own LDS operations finishing is
     // enough (the page stream stays in flight)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -205,6 +226,7 @@ __device__ __forceinline__ void dattn_split(const DattnArgs &a, uint32_t h, uint
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov[nb][i] = pair_sum<32>(O[nb][i], O[nb + 4][i]);
     if (s == 0) {
+        if constexpr (TOK_SEPARATE) __syncthreads();  // the token wavefront's L.vs / L.sp
         // this token: one more online-softmax step with score sp and value vs; lane n of every
         // row holds head n % 8's state, so the head of row i is gathered by readlane
         const float sp = L.sp[n & 7];
