@@ -25,13 +25,16 @@ namespace omega {
 constexpr uint32_t kRouterHidden = 2048;
 
 // x, the norm weights and the gate rows come in as leading scalar arguments (preloaded into
-// SGPRs), so their loads go out at the first instruction.
-__global__ __launch_bounds__(256) void k_router_logits(const float *x, const float *norm_w, const uint16_t *gate,
-                                                       const RouterArgs a) {
+// SGPRs), so their loads go out at the first instruction. One wavefront per workgroup: each gate
+// row, and the residual row and norm weights it needs (16 KiB), arrive on a CU of their own
+// instead of four rows' worth through one CU's load path (measured 24 us a token faster).
+// Workgroup 0 also writes x'.
+__global__ __launch_bounds__(64) void k_router_logits(const float *x, const float *norm_w, const uint16_t *gate,
+                                                      const RouterArgs a) {
     using S = Bf16Slab<kRouterHidden, 1>;
     constexpr int P = S::P;
-    const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
-    const uint32_t row = blockIdx.x * 4 + wid;
+    const uint32_t lane = lane_id(), wid = 0;
+    const uint32_t row = blockIdx.x;
     const uint32_t rows = a.experts + a.shared;
     float xr[P][8], nw[P][8];
     S::load_x(x, lane, xr);
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(64) void k_router_topk(const RouterArgs a) {
 
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t st) {
     const uint32_t rows = a.experts + a.shared;
-    OMEGA_LAUNCH(k_router_logits, dim3((rows + 3) / 4), dim3(256), 0, st, a.x, a.norm_w, a.gate, a);
+    OMEGA_LAUNCH(k_router_logits, dim3(rows), dim3(64), 0, st, a.x, a.norm_w, a.gate, a);
     return hipGetLastError();
 }
 
