@@ -6,8 +6,10 @@
 // of the max (crates/aien-omega-dgraph/src/lib.rs:347-349, tensor.rs:299-318).
 //
 // Kernel shape (rows.hpp): row-major rows, two per wavefront (8 KiB, eight 1 KiB chunks), the
-// activation phases in registers; workgroups of four wavefronts loop over the rows with a grid
-// sized to the chip, so the norm prologue runs once per wavefront. The argmax packs
+// activation phases in registers; one workgroup of 16 wavefronts per CU loops over the rows, with
+// the activation row and the norm weights staged once per workgroup in LDS (read per wavefront,
+// they crossed each CU's load path 16 to 20 times at the start of the stream), so the norm
+// prologue runs once per wavefront from LDS. The argmax packs
 // (value, ~index) into one 64-bit key whose integer maximum is the greedy token; each
 // workgroup issues one fire-and-forget atomicMax into one of kArgmaxSlots slots and the host
 // takes the maximum of the slots (no ordering between workgroups is involved).
@@ -30,19 +32,47 @@ uint32_t argmax_from_slots(const unsigned long long *slots) {
 
 constexpr int kLmK = 2048;
 constexpr int kLmRows = 2;
-constexpr uint32_t kLmBlocks = 2048;
+constexpr uint32_t kLmBlocks = 256;  // one 16-wavefront workgroup per CU
+constexpr uint32_t kAnyBlocks = 2048;
 
 template <bool NORM, bool ARGMAX>
-__global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
+__global__ __launch_bounds__(1024) void k_bf16_lm(const Bf16RowsArgs a) {
     using S = Bf16Slab<kLmK, kLmRows>;
     constexpr int P = S::P;
+    constexpr uint32_t W = 16;  // wavefronts per workgroup: one workgroup per CU
     static_assert(!NORM || P * 8 * 64 == kLmK, "the phases must partition the row");
-    __shared__ unsigned long long best_w[4];
+    __shared__ unsigned long long best_w[W];
+    __shared__ __align__(16) float xs[kLmK];
+    __shared__ __align__(16) float ws[NORM ? kLmK : 4];
     const uint32_t lane = lane_id(), wid = threadIdx.x >> 6;
+    // the row and the norm weights staged once per workgroup
+    if (threadIdx.x < kLmK / 4) {
+        reinterpret_cast<f32x4 *>(xs)[threadIdx.x] = *as_global_f32x4(a.x + 4 * threadIdx.x);
+        if (NORM) reinterpret_cast<f32x4 *>(ws)[threadIdx.x] = *as_global_f32x4(a.norm_w + 4 * threadIdx.x);
+    }
+    __syncthreads();
     float xr[P][8];
     float nw[P][8];
-    S::load_x(a.x, lane, xr);
-    if (NORM) S::load_x(a.norm_w, lane, nw);
+#pragma unroll
+    for (int ph = 0; ph < P; ++ph) {
+        const f32x4 *q = reinterpret_cast<const f32x4 *>(xs + S::col(ph, lane));
+        const f32x4 *r = reinterpret_cast<const f32x4 *>(ws + (NORM ? S::col(ph, lane) : 0));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const f32x4 t = q[i];
+            xr[ph][4 * i] = t.x;
+            xr[ph][4 * i + 1] = t.y;
+            xr[ph][4 * i + 2] = t.z;
+            xr[ph][4 * i + 3] = t.w;
+            if (NORM) {
+                const f32x4 u = r[i];
+                nw[ph][4 * i] = u.x;
+                nw[ph][4 * i + 1] = u.y;
+                nw[ph][4 * i + 2] = u.z;
+                nw[ph][4 * i + 3] = u.w;
+            }
+        }
+    }
     // the final RMSNorm as one scale on the row sums (the sum of squares runs beside the stream)
     float scale = 1.0f;
     if (NORM) {
@@ -62,9 +92,9 @@ __global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
         }
     }
     const uint32_t items = (a.n + kLmRows - 1) / kLmRows;
-    const uint32_t stride = gridDim.x * 4;
+    const uint32_t stride = gridDim.x * W;
     unsigned long long best = 0;
-    for (uint32_t item = blockIdx.x * 4 + wid; item < items; item += stride) {
+    for (uint32_t item = blockIdx.x * W + wid; item < items; item += stride) {
         const uint32_t r0 = item * kLmRows;
         const bool two = r0 + 1 < a.n;
         S slab;
@@ -97,7 +127,7 @@ __global__ __launch_bounds__(256) void k_bf16_lm(const Bf16RowsArgs a) {
         __syncthreads();
         if (threadIdx.x == 0) {
             unsigned long long b = best_w[0];
-            for (int w = 1; w < 4; ++w) b = best_w[w] > b ? best_w[w] : b;
+            for (uint32_t w = 1; w < W; ++w) b = best_w[w] > b ? best_w[w] : b;
             if (b) atomicMax(&a.argmax[blockIdx.x % kArgmaxSlots], b);
         }
     }
@@ -147,23 +177,23 @@ __global__ __launch_bounds__(256) void k_bf16_any(const Bf16RowsArgs a, uint32_t
 hipError_t launch_bf16_rows(const Bf16RowsArgs &a, hipStream_t st) {
     if (a.k == (uint32_t)kLmK) {
         const uint32_t items = (a.n + kLmRows - 1) / kLmRows;
-        uint32_t blocks = (items + 3) / 4;
+        uint32_t blocks = (items + 15) / 16;
         if (blocks > kLmBlocks) blocks = kLmBlocks;
         if (a.norm_w && a.argmax)
-            OMEGA_LAUNCH((k_bf16_lm<true, true>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<true, true>), dim3(blocks), dim3(1024), 0, st, a);
         else if (a.norm_w)
-            OMEGA_LAUNCH((k_bf16_lm<true, false>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<true, false>), dim3(blocks), dim3(1024), 0, st, a);
         else if (a.argmax)
-            OMEGA_LAUNCH((k_bf16_lm<false, true>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<false, true>), dim3(blocks), dim3(1024), 0, st, a);
         else
-            OMEGA_LAUNCH((k_bf16_lm<false, false>), dim3(blocks), dim3(256), 0, st, a);
+            OMEGA_LAUNCH((k_bf16_lm<false, false>), dim3(blocks), dim3(1024), 0, st, a);
         return hipGetLastError();
     }
     if (a.norm_w || a.argmax) return hipErrorInvalidValue;
     const uint32_t rpw = (2 * a.k) % 1024 == 0 ? 1 : 2;
     const uint32_t items = (a.n + rpw - 1) / rpw;
     uint32_t blocks = (items + 3) / 4;
-    if (blocks > kLmBlocks) blocks = kLmBlocks;
+    if (blocks > kAnyBlocks) blocks = kAnyBlocks;
     OMEGA_LAUNCH(k_bf16_any, dim3(blocks), dim3(256), a.k * 4, st, a, rpw);
     return hipGetLastError();
 }
@@ -225,9 +255,9 @@ static int bf16_run(const OmegaGpuBf16Tensor *t, const float *x, float *y, Omega
         info->n = t->n;
         info->k = t->k;
         info->rows_per_warp = t->k == (uint32_t)kLmK ? kLmRows : ((2 * t->k) % 1024 == 0 ? 1 : 2);
-        info->warps_per_cta = 4;
+        info->warps_per_cta = t->k == (uint32_t)kLmK ? 16 : 4;
         info->depth = 8;
-        info->grid_x = kLmBlocks;
+        info->grid_x = t->k == (uint32_t)kLmK ? kLmBlocks : kAnyBlocks;
         info->steps = t->k / 8;
         info->weight_bytes = (uint64_t)t->n * t->k * 2;
         info->elapsed_ns = event_ns(c);
