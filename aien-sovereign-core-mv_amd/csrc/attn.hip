@@ -99,7 +99,7 @@ __global__ __launch_bounds__(128) void k_dattn(const float *qkv, const uint32_t 
                       lds, epoch, lane);
     if (s >= 8) return;
     // Merge of q head 8 h + s: wait until every split of kv head h has flagged this epoch (every
-    // split is resident: at most 4 x 64 one-wavefront workgroups), with a bounded number of polls
+    // split is resident: at most 4 x 64 two-wavefront workgroups), with a bounded number of polls
     // (a wait that runs out is counted and the merge goes on; merge_spins 0, a test knob, gives up
     // without a poll).
     {
