@@ -522,7 +522,10 @@ def bench_paged(om, args):
     bf16 K/V ~ N(0,1); each point timed cold (the Infinity Cache and L2 flushed by a 1 GiB fill
     before every call) with HIP events on the library stream: one launch per call where the
     split workgroups all fit the device at once (the splits merged in the same launch, every point
-    here), else the split launch and the combine launch."""
+    here), else the split launch and the combine launch. Each point is also timed back to back:
+    one call per layer of the pool (48 calls in a row, each on K/V the row has not read before,
+    the caches flushed once before the row), the way a decode step issues them; that figure is the
+    row's event span / 48, so one call's event and launch overhead is not charged to it alone."""
     import ctypes as C
 
     max_pages = max(b * l // 16 for b, l in PAGED_POINTS)
@@ -547,9 +550,9 @@ def bench_paged(om, args):
         ld = om.DeviceBuffer.from_array(np.full(seqs, ctx, np.int32))
         od = om.DeviceBuffer(q.nbytes)
 
-        def call():
+        def call(lay=layer):
             rc = lib.omega_gpu_paged_attention_batch_dev(qd.ptr, pool.ptr, C.byref(L_), td.ptr, ld.ptr,
-                                                         pages, seqs, ctx, layer, QH, KVH, HD, od.ptr)
+                                                         pages, seqs, ctx, lay, QH, KVH, HD, od.ptr)
             assert rc == 0, om._s(lib.omega_gpu_attention_last_error())
 
         for _ in range(2):
@@ -562,10 +565,23 @@ def bench_paged(om, args):
             timer.stop()
             times.append(timer.ms() * 1e3)
         us = float(np.median(times))
+        # back to back: the 48 layers' calls in a row on the stream (as a decode step makes them),
+        # each reading K/V no earlier call of the row touched, after one flush; per call = row / 48
+        chained = []
+        for _ in range(max(3, args.paged_reps // 3)):
+            assert hip.hipMemsetAsync(flush.ptr, 1, C.c_size_t(flush.nbytes), stream) == 0
+            timer.start()
+            for lay in range(L):
+                call(lay)
+            timer.stop()
+            chained.append(timer.ms() * 1e3 / L)
+        us_b2b = float(np.median(chained))
         b = paged_bytes(seqs, ctx)
         line = {"workload": "paged_attention", "seqs": seqs, "ctx": ctx, "us_per_call": round(us, 2),
                 "algorithmic_bytes": b, "GBs": round(b / (us * 1e3), 1),
-                "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times)}
+                "frac": round(b / (us * 1e3) / PEAK_GBS, 4), "reps": len(times),
+                "us_per_call_back_to_back": round(us_b2b, 2),
+                "GBs_back_to_back": round(b / (us_b2b * 1e3), 1)}
         print(json.dumps(line), flush=True)
         lines.append(line)
         for buf in (qd, td, ld, od):
