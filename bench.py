@@ -541,7 +541,11 @@ def bench_paged(om, args):
     rng = np.random.default_rng(SEED)
     layer = 7
     lines = []
-    for seqs, ctx in PAGED_POINTS:
+    points = PAGED_POINTS
+    if args.paged_points:
+        points = [tuple(int(v) for v in p.split("x")) for p in args.paged_points.split(",")]
+        assert all(pt in PAGED_POINTS for pt in points), f"points must come from {PAGED_POINTS}"
+    for seqs, ctx in points:
         pages = ctx // 16
         perm = rng.permutation(max_pages)[: seqs * pages].astype(np.int32).reshape(seqs, pages)
         q = rng.standard_normal((seqs, QH * HD)).astype(np.float32)
@@ -595,7 +599,9 @@ def bench_paged(om, args):
         "config": {"workload": "paged attention 32q/4kv x 128, 16-token pages, 48-layer pool geometry",
                    "points": [[p["seqs"], p["ctx"]] for p in lines]},
         "roofline": {"bound": "hbm", "kernel": "k_paged4f (splits merged in the launch)", "achieved": big["GBs"],
-                     "peak": PEAK_GBS, "unit": "GB/s", "frac": big["frac"], "traffic": None},
+                     "peak": PEAK_GBS, "unit": "GB/s", "frac": big["frac"],
+                     "traffic": (committed_traffic(None, "paged_attention_traffic.md")
+                                 if (big["seqs"], big["ctx"]) == PAGED_POINTS[-1] else None)},
         "points": lines, "cpu_baseline": cpu}), flush=True)
 
 
@@ -890,6 +896,8 @@ def main():
     ap.add_argument("--serve-steps", type=int, default=128)
     ap.add_argument("--serve-warmup", type=int, default=4)
     ap.add_argument("--paged-reps", type=int, default=10)
+    ap.add_argument("--paged-points", default="",
+                    help="paged workload: a comma-separated subset of the sweep as SEQSxCTX, e.g. 32x32768")
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--gemv-reps", type=int, default=200)
     ap.add_argument("--prefill-lengths", default="512,2048")
